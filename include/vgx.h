@@ -1,0 +1,192 @@
+/*
+ * vgx.h -- C-ABI of libvgx, the MI355X (gfx950) quantized decode path.
+ *
+ * This is the boundary that replaces the reference engine's `class GPU`
+ * (engine/src/gpu.h:41-633): every GLES2 draw + readback the reference's
+ * Session issues for the decode hot path has one entry point here.  Plain
+ * pointers and sizes only.  Activation, residual, KV and logits buffers are
+ * device pointers (hipMalloc'd or torch tensors); weight bytes are passed
+ * exactly as they lie in an MMCF container (host pointers) and are copied to
+ * HBM at upload.
+ *
+ * Numbers: activations travel as the reference's q16 grid -- int16 holding
+ * round(value*256) (engine/src/common.h:188-195) -- in native little-endian
+ * order; the texel byte order (big-endian pairs) exists only in
+ * vgx_x_pack_i16_2 and in the KV row export, where it is a persisted format.
+ *
+ * Errors: every call returns VGX_OK (0) or a negative status; the message of
+ * the last failure on the calling thread is vgx_last_error().  No call throws
+ * or aborts.  Shapes are validated at upload and at each launch.
+ *
+ * Streams: all device work of a context is issued on its stream in call
+ * order (vgx_ctx_set_stream); only vgx_ctx_sync, vgx_kv_read_rows and
+ * vgx_kv_write_rows block the host.  One context per host thread, as the
+ * reference keeps one GL context per process (engine/src/gpu_internal.h:4-9).
+ */
+#ifndef VGX_H
+#define VGX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VGX_ABI_VERSION 1
+
+enum vgx_status {
+    VGX_OK = 0,
+    VGX_EINVAL = -1, /* bad argument or shape */
+    VGX_EHIP = -2,   /* HIP runtime error (message in vgx_last_error) */
+    VGX_ENOMEM = -3, /* device allocation failed */
+    VGX_ESTATE = -4, /* call out of order (e.g. attention before create) */
+    VGX_ERANGE = -5  /* position / row / size outside what was created */
+};
+
+typedef struct vgx_ctx vgx_ctx;
+typedef struct vgx_mat vgx_mat;
+typedef struct vgx_group vgx_group;
+typedef struct vgx_attn vgx_attn;
+
+int vgx_abi_version(void);
+const char* vgx_strerror(int status);
+const char* vgx_last_error(void);
+
+/* ---- context: replaces GPU::GPU / init_egl (engine/src/gpu.cpp) and
+ *      GPU::sync (engine/src/gpu.h:60); release_scene is vgx_ctx_destroy. */
+int vgx_ctx_create(int device, vgx_ctx** out);
+int vgx_ctx_destroy(vgx_ctx* ctx);
+/* hipStream_t; NULL is HIP's default (null) stream.  A new context issues on
+ * a stream of its own that is ordered with the null stream. */
+int vgx_ctx_set_stream(vgx_ctx* ctx, void* stream);
+void* vgx_ctx_stream(vgx_ctx* ctx);
+int vgx_ctx_sync(vgx_ctx* ctx);
+
+/* ---- weights: replaces GPU::upload(Mat&) (engine/src/gpu_upload.cpp:20-192).
+ * The body and planes are the MMCF tensor bytes unchanged
+ * (docs/checkpoint-container.md, "Tensor record"):
+ *   Q8: rows x cols bytes, q8u8 (dtype 2, prebiased=1) or q8i8 (dtype 3);
+ *       `scale` = record scale; `row_plane` = part 3 (rows f32) or NULL.
+ *   Q4: rows x cols/2 nibble bytes (low nibble = even column); `scale` = the
+ *       record's ps; `q4_scale` / `q4_min` = parts 1 and 2 (rows x cols/32 int16).
+ *   T3: ceil(rows/2) x ceil(cols/8) x 4 bytes (dtype 7); `scale` = record
+ *       scale (the kernels use scale*127, engine/src/model.cpp:927);
+ *       `row_plane` = part 3.
+ * `scale_mul` is Model::apply_hidden_scale's 2^k for a w2 matrix
+ * (engine/src/model.cpp:407-429), 0 or 1 for every other matrix.  */
+enum vgx_kind { VGX_Q8 = 1, VGX_Q4 = 2, VGX_T3 = 3 };
+typedef struct vgx_weight_desc {
+    int kind;
+    int rows, cols;
+    const void* body;
+    size_t body_bytes;
+    int prebiased;
+    float scale;
+    const float* row_plane;
+    const int16_t* q4_scale;
+    const int16_t* q4_min;
+    float scale_mul;
+} vgx_weight_desc;
+
+int vgx_mat_upload(vgx_ctx* ctx, const vgx_weight_desc* desc, vgx_mat** out);
+/* A second device copy of an uploaded matrix (device-to-device). */
+int vgx_mat_clone(vgx_ctx* ctx, const vgx_mat* src, vgx_mat** out);
+int vgx_mat_free(vgx_mat* m);
+int vgx_mat_shape(const vgx_mat* m, int* kind, int* rows, int* cols);
+/* Bytes one GEMV over this matrix must read from HBM for the weights: body
+ * plus the per-row / per-group scale planes as held on the device. */
+size_t vgx_mat_weight_bytes(const vgx_mat* m);
+/* The dequantised matrix, fp32 rows x cols into device memory: the value each
+ * kernel multiplies by (q8/t3: level * row scale; q4: n*(s16*ps) + m16*ps). */
+int vgx_dequant(vgx_ctx* ctx, const vgx_mat* m, float* out);
+
+/* ---- dequant-GEMV family.
+ * vgx_gemv: y = q16(W.x) -- matvec_q8_pair_logits / matvec_t3_pair /
+ *   matvec_i4 (engine/src/shaders.cpp:704-747, 554-573, 1249-1274); with
+ *   `res` (may be NULL) y = q16(W.x + res), one rounding, as
+ *   matvec_q8_add_pair / matvec_i4_add_pair / matvec_t3_add_pair
+ *   (:1161-1214, :1322-1354, :575-600) dispatched by GPU::matvec_add
+ *   (engine/src/gpu_matvec.cpp:225-291).  x: cols int16, y/res: rows int16.  */
+int vgx_gemv(vgx_ctx* ctx, const vgx_mat* W, const int16_t* x, const int16_t* res, int16_t* y);
+/* fp32 activations: x is quantised to the q16 grid exactly as the host does
+ * before every upload (x_pack, engine/src/xformat.cpp:87-93) and y is the row
+ * value in activation units before the q16 store (the store grid / 256). */
+int vgx_gemv_f32(vgx_ctx* ctx, const vgx_mat* W, const float* x, float* y);
+/* Two residual adds through the column halves of one matrix:
+ *   y = q16( W[:, split:].x[split:] + q16( W[:, :split].x[:split] + res ) )
+ * which is GPU::matvec_add(w2a) then matvec_add(w2b) over Model::split_ffn's
+ * column chunks (engine/src/session.cpp:1557-1562, model.cpp:255-265).  */
+int vgx_gemv_add_split(vgx_ctx* ctx, const vgx_mat* W, int split, const int16_t* x,
+                       const int16_t* res, int16_t* y);
+
+/* A fixed list of matrices sharing one input (same kind, same cols), launched
+ * as one kernel; outputs are concatenated in list order.  Replaces
+ * GPU::logits_pass (one draw per <=1536-row tile, engine/src/gpu_matvec.cpp:56-82). */
+int vgx_group_create(vgx_ctx* ctx, int n, const vgx_mat* const* mats, vgx_group** out);
+int vgx_group_free(vgx_group* g);
+int vgx_group_rows(const vgx_group* g);
+int vgx_gemv_group(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, int16_t* y);
+int vgx_gemv_group_f32(vgx_ctx* ctx, const vgx_group* g, const float* x, float* y);
+/* The logits pass followed by argmax_token's first-maximum rule
+ * (engine/src/sampling.cpp:160-162): `token` (device int) receives the
+ * index into the concatenated rows; `logits` (device, may be NULL) the q16 rows. */
+int vgx_logits_argmax(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, int16_t* logits,
+                      int* token);
+
+/* Fused FFN gate: h = q16( SiLU(qz(W1.x)) * qz(W3.x) * 2^-hs ) over all rows
+ * -- matvec_q8_pair_swiglu / i4_gate_flat8b (engine/src/shaders.cpp:756-815,
+ * 1539-1590) as dispatched by GPU::ffn_split_chunked (engine/src/gpu_ffn.cpp:67-132);
+ * the row chunks of split_ffn are rows of the same kernel here.  */
+int vgx_ffn_gate(vgx_ctx* ctx, const vgx_mat* W1, const vgx_mat* W3, const int16_t* x, int hs,
+                 int16_t* h);
+
+/* GPU::rmsnorm (engine/src/gpu_upload.cpp:280-365, shaders rms_stats_split /
+ * rms_norm): w is the norm weight on the q16 grid (x_pack of the f32 vector). */
+int vgx_rmsnorm(vgx_ctx* ctx, int dim, const int16_t* x, const int16_t* w, float eps, int16_t* y);
+
+/* Session::embedding (engine/src/session.cpp:342-371), q8 rows: x = the
+ * host-grid q16 of emb[token]*emb_scale[token].  emb: vocab x dim signed
+ * bytes (device), emb_scale: vocab f32 (device), token: device int. */
+int vgx_embed_q8(vgx_ctx* ctx, const int8_t* emb, const float* emb_scale, int vocab, int dim,
+                 const int* token, int16_t* x);
+
+/* ---- attention over the packed KV cache: replaces GPU::init_attention,
+ * attention_block, kv_rope_write (engine/src/gpu_attn.cpp:41-241, 400-421). */
+typedef struct vgx_attn_desc {
+    int dim, heads, kv_heads, head_dim, seq, layers;
+    int kv_bits;               /* 16 (grid 1/2048) or 8 (grid 1/16) */
+    int rope_half;             /* 1: rotate-half pairs (i, i+hd/2); 0: (2i, 2i+1) */
+    int qk_norm;
+    const float* rope_cos;     /* host [seq][head_dim/2] (Session's tables) */
+    const float* rope_sin;
+    const float* q_norm;       /* host [layers][head_dim] f32, NULL without qk_norm */
+    const float* k_norm;
+    const uint8_t* layer_is_attn; /* host [layers], NULL = every layer */
+} vgx_attn_desc;
+int vgx_attn_create(vgx_ctx* ctx, const vgx_attn_desc* desc, vgx_attn** out);
+int vgx_attn_free(vgx_attn* a);
+/* KV write of position `pos`: K qk-normed, rotated, packed; V packed. */
+int vgx_kv_append(vgx_attn* a, int layer, int pos, const int16_t* qkv);
+/* q prep, scores, stats and the weighted V for position `pos` (rows 0..pos
+ * of the layer's KV must be written). qkv: dim + 2*kv_dim int16; out: dim. */
+int vgx_attn_decode(vgx_attn* a, int layer, int pos, const int16_t* qkv, int16_t* out);
+/* vgx_kv_append then vgx_attn_decode in one launch. */
+int vgx_attn_block(vgx_attn* a, int layer, int pos, const int16_t* qkv, int16_t* out);
+/* The packed KV rows in the reference's texel byte layout (K values then V
+ * values; q16 big-endian, q8 two's-complement bytes) -- what MMKV1 persists
+ * (engine/src/prefix_cache.cpp:59-67).  Host buffers; these block. */
+int vgx_kv_row_bytes(const vgx_attn* a);
+int vgx_kv_read_rows(vgx_attn* a, int layer, int row0, int nrows, void* host);
+int vgx_kv_write_rows(vgx_attn* a, int layer, int row0, int nrows, const void* host);
+
+/* ---- host helpers (no device work) */
+/* quantize_act over n values (engine/src/common.h:188-195). */
+void vgx_quantize_act(const float* v, int n, int16_t* q);
+/* x_pack(I16_2): the texel bytes, 4*ceil(n/2) (engine/src/xformat.cpp:87-93). */
+void vgx_x_pack_i16_2(const float* v, int n, uint8_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

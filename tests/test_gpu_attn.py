@@ -1,0 +1,83 @@
+"""KV pack/unpack and decode attention against the oracle, through the C-ABI.
+
+Bar: bit-exact -- the packed KV rows (in the reference's texel byte layout,
+as MMKV1 persists them) and the q16 attention output at every position."""
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as o
+
+pytestmark = pytest.mark.gpu
+
+CONFIGS = [
+    # name, dim, heads, kv_heads, hd, seq, kv_bits, rope_half, qk_norm, theta, steps
+    ("minimind3-q16", 768, 8, 4, 96, 256, 16, 1, 1, 1e6, 255),
+    ("minimind3-q8", 768, 8, 4, 96, 768, 8, 1, 1, 1e6, 40),
+    ("lfm2", 1024, 16, 8, 64, 256, 16, 1, 1, 1e6, 24),
+    ("bitcpm", 1024, 16, 2, 64, 512, 16, 1, 0, 10000.0, 24),
+    ("interleaved", 256, 4, 2, 64, 64, 16, 0, 1, 10000.0, 20),
+    ("interleaved-q8", 256, 4, 4, 64, 64, 8, 0, 0, 10000.0, 20),
+]
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+@pytest.mark.parametrize("cfg", CONFIGS, ids=[c[0] for c in CONFIGS])
+def test_attention_matches_oracle(gpu, cfg):
+    name, dim, heads, kvh, hd, seq, bits, half, qk, theta, steps = cfg
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    layers = 2
+    rc, rs = o.rope_cos_sin(theta, hd, seq)
+    rtab = o.rope_table(rc, rs)
+    qn = rng.uniform(0.5, 1.5, (layers, hd)).astype(np.float32) if qk else None
+    kn = rng.uniform(0.5, 1.5, (layers, hd)).astype(np.float32) if qk else None
+    A = gpu.attention(dim=dim, heads=heads, kv_heads=kvh, head_dim=hd, seq=seq, layers=layers, kv_bits=bits,
+                      rope_half=half, qk_norm=qk, rope_cos=rc, rope_sin=rs, q_norm=qn, k_norm=kn)
+    c = o.attn_cfg(dim, heads, kvh, hd, seq, bits, half, qk)
+    rb = o.kv_row_bytes(c)
+    assert A.row_bytes == rb
+    kv = [np.zeros(seq * rb, np.uint8) for _ in range(layers)]
+    kv_dim = kvh * hd
+    layer = 1
+    qnq = o.quantize_act(qn[layer]) if qk else None
+    knq = o.quantize_act(kn[layer]) if qk else None
+    scale = 600 if bits == 16 else 300
+    for pos in range(steps):
+        qkv = np.clip(rng.standard_normal(dim + 2 * kv_dim) * scale, -32768, 32767).astype(np.int16)
+        want = o.attn_block(c, qkv, qnq, knq, rtab, pos, kv[layer])
+        if pos % 2 == 0:
+            got = A.block(layer, pos, dev(qkv))
+        else:  # the unfused pair: pack, then attend
+            q = dev(qkv)
+            A.kv_append(layer, pos, q)
+            got = A.decode(layer, pos, q)
+        torch.cuda.synchronize()
+        assert np.array_equal(got.cpu().numpy(), want), (name, pos)
+    rows = A.read_rows(layer, 0, steps)
+    assert np.array_equal(rows, kv[layer][:steps * rb])
+    # the import path writes the same bytes back; attention over them agrees
+    A.write_rows(layer, 0, rows)
+    qkv = np.clip(rng.standard_normal(dim + 2 * kv_dim) * scale, -32768, 32767).astype(np.int16)
+    want = o.attn_block(c, qkv, qnq, knq, rtab, steps, kv[layer])
+    got = A.block(layer, steps, dev(qkv))
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy(), want)
+    A.free()
+
+
+def test_attention_range_errors(gpu):
+    rc, rs = o.rope_cos_sin(10000.0, 64, 8)
+    A = gpu.attention(dim=128, heads=2, kv_heads=1, head_dim=64, seq=8, layers=1, kv_bits=16, rope_half=1,
+                      qk_norm=0, rope_cos=rc, rope_sin=rs)
+    from vgx import lib as vl
+    qkv = dev(np.zeros(256, np.int16))
+    with pytest.raises(vl.VgxError):
+        A.block(0, 8, qkv)  # pos beyond seq
+    with pytest.raises(vl.VgxError):
+        A.block(1, 0, qkv)  # no such layer
+    A.free()

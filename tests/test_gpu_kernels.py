@@ -1,0 +1,235 @@
+"""libvgx's kernels against the oracle, through the C-ABI, on cuda:0.
+
+Bar: bit-exact.  Every output of these kernels is an integer on the q16 grid
+(or an fp32 value computed by the same fp32 operations as the oracle), so the
+comparisons are equality, including for full-range random weights and
+activations where the int32 lanes of the dot products are at their limits.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as o
+from vgx import mmcf
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(768, 768), (384, 768), (2432, 768), (768, 2432), (6400, 768), (1, 64), (7, 32), (33, 96),
+          (1536, 768), (1024, 4096)]
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def q8_matrix(rng, rows, cols, plane=True, full=False, prebiased=True):
+    if full:
+        body = rng.integers(0, 256, (rows, cols), dtype=np.uint8)
+        m = mmcf.Matrix("q8", rows, cols, body.ravel(), float(rng.uniform(1e-4, 1e-2)), True,
+                        rng.uniform(0, 1.2, rows).astype(np.float32) if plane else None)
+    else:
+        w = rng.standard_normal((rows, cols)).astype(np.float32) * 0.02
+        if plane:
+            q, unit, p = mmcf.q8_per_row(w)
+        else:
+            (q, unit), p = mmcf.q8_from_i16(w), None
+        body = (q.view(np.uint8) ^ 0x80).ravel() if prebiased else q.view(np.uint8).ravel()
+        m = mmcf.Matrix("q8", rows, cols, body, float(np.float32(unit)), prebiased, p)
+    return m
+
+
+def q4_matrix(rng, rows, cols):
+    w = rng.standard_normal((rows, cols)).astype(np.float32) * 0.02
+    packed, s16, m16, ps, _ = mmcf.q4mat(w)
+    return mmcf.Matrix("q4", rows, cols, packed.ravel(), ps, s16=s16.ravel(), m16=m16.ravel())
+
+
+def t3_matrix(rng, rows, cols):
+    lev = rng.integers(-1, 2, (rows, cols)).astype(np.float32)
+    w = lev * rng.uniform(0.01, 0.05, (rows, 1)).astype(np.float32)
+    packed, unit, plane = mmcf.t3mat(w)
+    return mmcf.Matrix("t3", rows, cols, np.frombuffer(packed, np.uint8), unit, plane=plane)
+
+
+def wsr_of(m):
+    if m.kind == "t3":
+        return o.row_scales(m.rows, float(np.float32(np.float32(m.scale) * np.float32(127)) * np.float32(m.scale_mul)),
+                            m.plane)
+    return o.row_scales(m.rows, float(np.float32(m.scale) * np.float32(m.scale_mul)), m.plane)
+
+
+def oracle_rowval(m, x):
+    if m.kind == "q8":
+        return o.rowval_q8(m.body, int(m.prebiased), m.rows, m.cols, wsr_of(m), x)
+    if m.kind == "q4":
+        return o.rowval_q4(m.body, m.s16, m.m16, float(np.float32(m.scale) * np.float32(m.scale_mul)),
+                           m.rows, m.cols, x)
+    return o.rowval_t3(m.body, m.rows, m.cols, wsr_of(m), x)
+
+
+def rand_x(rng, n, full=False):
+    if full:
+        return rng.integers(-32768, 32768, n).astype(np.int16)
+    return o.quantize_act(rng.standard_normal(n).astype(np.float32))
+
+
+@pytest.mark.parametrize("rows,cols", SHAPES)
+def test_q8_gemv(gpu, rows, cols):
+    rng = np.random.default_rng(rows * 7 + cols)
+    for plane, full, pre in ((True, False, True), (False, False, True), (True, True, True), (True, False, False)):
+        m = q8_matrix(rng, rows, cols, plane, full, pre)
+        W = gpu.upload(m)
+        x = rand_x(rng, cols, full)
+        res = rand_x(rng, rows)
+        v = oracle_rowval(m, x)
+        y = host(gpu.matvec(W, dev(x)))
+        assert np.array_equal(y, o.store(v)), (plane, full, pre)
+        y2 = host(gpu.matvec(W, dev(x), dev(res)))
+        assert np.array_equal(y2, o.store(v, res)), (plane, full, pre)
+
+
+@pytest.mark.parametrize("rows,cols", [(768, 768), (6400, 768), (2432, 768), (33, 96)])
+def test_q8_gemv_f32(gpu, rows, cols):
+    rng = np.random.default_rng(11)
+    m = q8_matrix(rng, rows, cols)
+    W = gpu.upload(m)
+    xf = rng.standard_normal(cols).astype(np.float32)
+    v = oracle_rowval(m, o.quantize_act(xf))
+    y = host(gpu.matvec_f32(W, dev(xf)))
+    assert np.array_equal(y, o.store_f32(v))
+
+
+@pytest.mark.parametrize("rows,cols", [(768, 768), (384, 768), (2432, 768), (768, 2432), (6400, 768), (5, 32),
+                                       (1024, 4096)])
+def test_q4_gemv(gpu, rows, cols):
+    rng = np.random.default_rng(rows + 3 * cols)
+    m = q4_matrix(rng, rows, cols)
+    W = gpu.upload(m)
+    for full in (False, True):
+        x = rand_x(rng, cols, full)
+        res = rand_x(rng, rows)
+        v = oracle_rowval(m, x)
+        assert np.array_equal(host(gpu.matvec(W, dev(x))), o.store(v))
+        assert np.array_equal(host(gpu.matvec(W, dev(x), dev(res))), o.store(v, res))
+
+
+@pytest.mark.parametrize("rows,cols", [(1024, 1024), (1280, 1024), (4096, 1024), (1024, 4096), (7, 32), (33, 64)])
+def test_t3_gemv(gpu, rows, cols):
+    rng = np.random.default_rng(rows + 5 * cols)
+    m = t3_matrix(rng, rows, cols)
+    W = gpu.upload(m)
+    for full in (False, True):
+        x = rand_x(rng, cols, full)
+        res = rand_x(rng, rows)
+        v = oracle_rowval(m, x)
+        assert np.array_equal(host(gpu.matvec(W, dev(x))), o.store(v))
+        assert np.array_equal(host(gpu.matvec(W, dev(x), dev(res))), o.store(v, res))
+
+
+@pytest.mark.parametrize("kind", ["q8", "q4", "t3"])
+def test_dequant_bit_exact(gpu, kind):
+    rng = np.random.default_rng(21)
+    rows, cols = 70, 128
+    m = {"q8": lambda: q8_matrix(rng, rows, cols), "q4": lambda: q4_matrix(rng, rows, cols),
+         "t3": lambda: t3_matrix(rng, rows, cols)}[kind]()
+    got = host(gpu.dequant(gpu.upload(m)))
+    if kind == "q8":
+        want = o.dequant_q8(m.body, 1, rows, cols, wsr_of(m))
+    elif kind == "q4":
+        want = o.dequant_q4(m.body, m.s16, m.m16, m.scale, rows, cols)
+    else:
+        want = o.dequant_t3(m.body, rows, cols, wsr_of(m))
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("kind,rows,cols", [("q8", 2432, 768), ("q4", 2432, 768), ("t3", 4096, 1024),
+                                            ("q8", 9, 64)])
+def test_ffn_gate(gpu, kind, rows, cols):
+    rng = np.random.default_rng(31)
+    mk = {"q8": q8_matrix, "q4": q4_matrix, "t3": t3_matrix}[kind]
+    m1, m3 = mk(rng, rows, cols), mk(rng, rows, cols)
+    W1, W3 = gpu.upload(m1), gpu.upload(m3)
+    x = rand_x(rng, cols)
+    for hs in (0, 2):
+        h = host(gpu.ffn_gate(W1, W3, dev(x), hs))
+        assert np.array_equal(h, o.gate(oracle_rowval(m1, x), oracle_rowval(m3, x), hs)), hs
+
+
+@pytest.mark.parametrize("kind,rows,cols,split", [("q8", 768, 2432, 1216), ("q4", 768, 2432, 1216),
+                                                  ("t3", 1024, 4096, 2048), ("q8", 40, 64, 32)])
+def test_gemv_add_split(gpu, kind, rows, cols, split):
+    rng = np.random.default_rng(41)
+    mk = {"q8": q8_matrix, "q4": q4_matrix, "t3": t3_matrix}[kind]
+    m = mk(rng, rows, cols)
+    m.scale_mul = 4.0  # metadata key 15, k = 2
+    W = gpu.upload(m)
+    x = rand_x(rng, cols)
+    res = rand_x(rng, rows)
+    a, b = m.slice_cols(0, split), m.slice_cols(split, cols)
+    y1 = o.store(oracle_rowval(a, x[:split]), res)
+    want = o.store(oracle_rowval(b, x[split:]), y1)
+    assert np.array_equal(host(gpu.matvec_add_split(W, split, dev(x), dev(res))), want)
+
+
+def test_group_and_logits_argmax(gpu):
+    rng = np.random.default_rng(51)
+    vocab, dim = 6400, 768
+    w = rng.standard_normal((vocab, dim)).astype(np.float32) * 0.02
+    tiles = []
+    for st in range(0, vocab, mmcf.LOGITS_GRID):
+        q, unit, plane = mmcf.q8_per_row(w[st:st + mmcf.LOGITS_GRID])
+        tiles.append(mmcf.Matrix("q8", q.shape[0], dim, (q.view(np.uint8) ^ 0x80).ravel(), unit, True, plane))
+    g = gpu.group([gpu.upload(t) for t in tiles])
+    x = rand_x(rng, dim)
+    want = np.concatenate([o.store(oracle_rowval(t, x)) for t in tiles])
+    assert np.array_equal(host(g.gemv(dev(x))), want)
+    logits, tok = g.logits_argmax(dev(x))
+    assert np.array_equal(host(logits), want) and int(host(tok)[0]) == o.argmax_i16(want)
+    # ties: the first maximum wins
+    xz = np.zeros(dim, np.int16)
+    _, tok = g.logits_argmax(dev(xz))
+    assert int(host(tok)[0]) == 0
+    xf = rng.standard_normal(dim).astype(np.float32)
+    wantf = np.concatenate([o.store_f32(oracle_rowval(t, o.quantize_act(xf))) for t in tiles])
+    assert np.array_equal(host(g.gemv_f32(dev(xf))), wantf)
+
+
+@pytest.mark.parametrize("dim", [768, 1024, 64, 100])
+def test_rmsnorm(gpu, dim):
+    rng = np.random.default_rng(dim)
+    for scale in (256, 4000):
+        x = np.clip(rng.standard_normal(dim) * scale, -32768, 32767).astype(np.int16)
+        w = o.quantize_act(rng.uniform(0.5, 1.5, dim).astype(np.float32))
+        for eps in (1e-5, 1e-6):
+            assert np.array_equal(host(gpu.rmsnorm(dev(x), dev(w), eps)), o.rmsnorm(x, w, eps))
+
+
+def test_embed_q8(gpu):
+    rng = np.random.default_rng(61)
+    emb = rng.integers(-127, 128, (6400, 768)).astype(np.int8)
+    es = rng.uniform(1e-4, 1e-2, 6400).astype(np.float32)
+    E, S = dev(emb), dev(es)
+    for tok in (0, 17, 6399):
+        t = dev(np.array([tok], np.int32))
+        assert np.array_equal(host(gpu.embed_q8(E, S, t)), o.embed_q8(emb, es, tok))
+
+
+def test_mat_clone_and_errors(gpu):
+    rng = np.random.default_rng(71)
+    m = q8_matrix(rng, 64, 64)
+    W = gpu.upload(m)
+    C = gpu.clone(W)
+    x = dev(rand_x(rng, 64))
+    assert torch.equal(gpu.matvec(W, x), gpu.matvec(C, x))
+    assert W.weight_bytes == 64 * 64 + 64 * 4
+    from vgx import lib as vl
+    bad = mmcf.Matrix("q8", 64, 40, np.zeros(64 * 40, np.uint8), 1.0)
+    with pytest.raises(vl.VgxError):
+        gpu.upload(bad)  # cols not a multiple of 16
+    with pytest.raises(vl.VgxError):
+        gpu.matvec(W, x[1:])  # misaligned activation pointer

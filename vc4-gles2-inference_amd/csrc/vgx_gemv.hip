@@ -1,0 +1,705 @@
+// Dequant-GEMV kernels for gfx950: q8 (q8u8 bytes), q4 (g32 nibbles + int16
+// scale/min planes) and t3 (2-bit ternary texel grid), batch 1.
+//
+// Mapping.  A block is 4 wave64s.  A wave owns RI x (64/LPR) rows: LPR lanes
+// cooperate on one row and step through its 16-byte weight chunks (chunk
+// c = lane + j*LPR), so one wave instruction reads 64 x 16 B of contiguous row
+// segments.  The activation row is staged once per block in LDS, already split
+// into the byte planes the dot instructions want:
+//   x = 256*xh + xl,  xh = signed high byte, xl = unsigned low byte,
+// so an int8 x int16 dot product becomes two 4-wide byte dots:
+//   q8 : sum (u-128)*x = 256*sdot4(u^0x80, xh) + udot4(u, xl) - 128*sum(xl)
+//   t3 : sum lv*x      = 256*sdot4(lv+1, xh) + udot4(lv+1, xl) - sum(x)
+//   q4 : sum n*x       = 256*sdot4(n, xh)    + udot4(n, xl)         (per group)
+// (lv+1 in {0,1,2} comes from a 256-entry byte -> 4 levels table in LDS.)
+// Every sum is an exact integer; the epilogue applies the reference's fp32
+// scale/round/clamp with no contraction (this file is built with
+// -ffp-contract=off).  Rows of a wave are reduced across their LPR lanes by a
+// butterfly that halves the row set per step, so RI rows cost RI-1+log2(LPR)
+// exchanges instead of RI*log2(LPR).
+#include "vgx_internal.h"
+
+#pragma clang fp contract(off)
+
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+__device__ __forceinline__ uint32_t udot4(uint32_t a, uint32_t b, uint32_t c) {
+    return __builtin_amdgcn_udot4(a, b, c, false);
+}
+__device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) {
+    return __builtin_amdgcn_perm(s0, s1, sel);
+}
+
+// quantize_act on the device: rint half-even of v*256, int16 rail.
+__device__ __forceinline__ int q16_host(float v) {
+    float r = __builtin_rintf(v * 256.0f);
+    r = fminf(fmaxf(r, -32768.0f), 32767.0f);
+    return (int)r;
+}
+
+// clamp(floor(v + 0.5)) -- the shader's q16 store of a value in Q units.
+__device__ __forceinline__ int q16_round(float v) {
+    float f = floorf(v + 0.5f);
+    f = fminf(fmaxf(f, -32768.0f), 32767.0f);
+    return (int)f;
+}
+
+template <typename T>
+__device__ __forceinline__ T shfl_xor(T v, int o) {
+    return __shfl_xor(v, o, 64);
+}
+
+// Which matrix / row block this block works on.
+__device__ __forceinline__ int find_mat(const MatDev* mats, int nmat, int blk) {
+    if (nmat == 1) return 0;
+    int lo = 0, hi = nmat - 1;
+    while (lo < hi) {
+        int mid = (lo + hi + 1) >> 1;
+        if (mats[mid].blk_off <= blk) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
+// Pack 16 q16 values (8 dwords, two per dword, element 2k in the low half)
+// into the natural-order planes: xl[k] / xh[k] = low / high bytes of elements
+// 4k..4k+3.
+__device__ __forceinline__ void planes16(const uint32_t d[8], uint32_t xh[4], uint32_t xl[4]) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        xl[k] = perm(d[2 * k + 1], d[2 * k], 0x06040200u);
+        xh[k] = perm(d[2 * k + 1], d[2 * k], 0x07050301u);
+    }
+}
+
+// 4x4 byte transpose of dwords d[0..3] (each = two q16 values, even element
+// low): returns the even-column low bytes, even high, odd low, odd high.
+__device__ __forceinline__ void planes8eo(const uint32_t d[4], uint32_t& xle, uint32_t& xhe,
+                                          uint32_t& xlo, uint32_t& xho) {
+    uint32_t A = perm(d[1], d[0], 0x05010400u);
+    uint32_t B = perm(d[1], d[0], 0x07030602u);
+    uint32_t C = perm(d[3], d[2], 0x05010400u);
+    uint32_t D = perm(d[3], d[2], 0x07030602u);
+    xle = perm(C, A, 0x05040100u);
+    xhe = perm(C, A, 0x07060302u);
+    xlo = perm(D, B, 0x05040100u);
+    xho = perm(D, B, 0x07060302u);
+}
+
+// Load 16 consecutive activations as q16 dwords (from int16 or from f32 with
+// the host quantisation).  Columns >= K read as zero.
+template <bool XF32>
+__device__ __forceinline__ void load_x16(const int16_t* x, const float* xf, int col, int K,
+                                         uint32_t d[8]) {
+    if (!XF32) {
+        if (col + 16 <= K) {
+            const uint4* p = reinterpret_cast<const uint4*>(x + col);
+            uint4 a = p[0], b = p[1];
+            d[0] = a.x; d[1] = a.y; d[2] = a.z; d[3] = a.w;
+            d[4] = b.x; d[5] = b.y; d[6] = b.z; d[7] = b.w;
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                int c0 = col + 2 * k;
+                uint32_t lo = c0 < K ? (uint16_t)x[c0] : 0u;
+                uint32_t hi = c0 + 1 < K ? (uint16_t)x[c0 + 1] : 0u;
+                d[k] = lo | (hi << 16);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            int c0 = col + 2 * k;
+            uint32_t lo = c0 < K ? (uint16_t)(int16_t)q16_host(xf[c0]) : 0u;
+            uint32_t hi = c0 + 1 < K ? (uint16_t)(int16_t)q16_host(xf[c0 + 1]) : 0u;
+            d[k] = lo | (hi << 16);
+        }
+    }
+}
+
+// t3 byte -> four (level + 1) bytes: code 1 -> 2, code 3 -> 0, else 1.
+__device__ __forceinline__ uint32_t t3_lut_entry(uint32_t b) {
+    uint32_t r = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        uint32_t c = (b >> (2 * k)) & 3u;
+        uint32_t lv1 = c == 1u ? 2u : (c == 3u ? 0u : 1u);
+        r |= lv1 << (8 * k);
+    }
+    return r;
+}
+
+// ---------------------------------------------------------------------------
+// Multi-row butterfly over the LPR lanes of a row segment.  v[r][k], r < R,
+// k < NV.  After the call the lane whose segment index has zero low bits
+// (cl % (LPR/R) == 0) holds the complete sums of row `row` in v[0][*].
+template <int LPR, int R, int NV, typename T>
+__device__ __forceinline__ int seg_reduce(T (&v)[R][NV], int cl) {
+    int base = 0;
+    int m = R;
+    int o = LPR / 2;
+#pragma unroll
+    for (int step = 0; (1 << step) < R; ++step) {
+        const bool up = (cl & o) != 0;
+        const int h = m / 2;
+#pragma unroll
+        for (int r = 0; r < R / 2; ++r) {
+            if (r < h) {
+#pragma unroll
+                for (int k = 0; k < NV; ++k) {
+                    T mine = up ? v[r + h][k] : v[r][k];
+                    T other = up ? v[r][k] : v[r + h][k];
+                    v[r][k] = mine + shfl_xor(other, o);
+                }
+            }
+        }
+        base += up ? h : 0;
+        m = h;
+        o >>= 1;
+    }
+    for (; o >= 1; o >>= 1) {
+#pragma unroll
+        for (int k = 0; k < NV; ++k) v[0][k] += shfl_xor(v[0][k], o);
+    }
+    return base;
+}
+
+// ---------------------------------------------------------------------------
+// Per-format chunk math.
+
+// q8: one chunk = 16 bytes of one row = 16 columns; planes: xh, xl (4 dwords).
+__device__ __forceinline__ void q8_chunk(const uint4 w, const uint4 xh, const uint4 xl, int& s1,
+                                         uint32_t& s2) {
+    s1 = sdot4(w.x ^ 0x80808080u, xh.x, s1);
+    s1 = sdot4(w.y ^ 0x80808080u, xh.y, s1);
+    s1 = sdot4(w.z ^ 0x80808080u, xh.z, s1);
+    s1 = sdot4(w.w ^ 0x80808080u, xh.w, s1);
+    s2 = udot4(w.x, xl.x, s2);
+    s2 = udot4(w.y, xl.y, s2);
+    s2 = udot4(w.z, xl.z, s2);
+    s2 = udot4(w.w, xl.w, s2);
+}
+
+// q4: one chunk = one 32-column group (16 nibble bytes); planes per dword j:
+// even-column high/low bytes and odd-column high/low bytes.
+__device__ __forceinline__ int q4_chunk(const uint4 w, const uint4 xhe, const uint4 xle,
+                                        const uint4 xho, const uint4 xlo) {
+    int s1 = 0;
+    uint32_t s2 = 0;
+    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+    const uint32_t he[4] = {xhe.x, xhe.y, xhe.z, xhe.w}, le[4] = {xle.x, xle.y, xle.z, xle.w};
+    const uint32_t ho[4] = {xho.x, xho.y, xho.z, xho.w}, lo[4] = {xlo.x, xlo.y, xlo.z, xlo.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        uint32_t ne = wd[j] & 0x0F0F0F0Fu;
+        uint32_t no = (wd[j] >> 4) & 0x0F0F0F0Fu;
+        s1 = sdot4(ne, he[j], s1);
+        s1 = sdot4(no, ho[j], s1);
+        s2 = udot4(ne, le[j], s2);
+        s2 = udot4(no, lo[j], s2);
+    }
+    return s1 * 256 + (int)s2;
+}
+
+// ---------------------------------------------------------------------------
+// The kernel.  One template per (format, lanes per row, rows per lane,
+// epilogue, input type).
+//
+// LDS layout (dynamic): [planes][scalars]
+//   q8 : per 16-col chunk: xh (16 B), xl (16 B)                    -> 32 B/chunk
+//   t3 : per 32-col chunk: xh (32 B), xl (32 B)  (natural order)    -> 64 B/chunk
+//   q4 : per 32-col group: xhe, xle, xho, xlo (16 B each)           -> 64 B/group
+//        plus X_g (int32) per group
+//   t3 : + 256 u32 level table
+template <int KIND, int LPR, int RI, int EPI, bool XF32>
+__global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
+    extern __shared__ uint4 lds[];
+    constexpr int RPI = 64 / LPR;
+    constexpr int NV = (EPI == EPI_GATE || EPI == EPI_SPLIT) ? 2 : 1;
+    // rows a wave owns: t3 counts row *pairs*
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int rs = lane / LPR;
+    const int cl = lane % LPR;
+
+    const int mi = find_mat(L.mats, L.nmat, blockIdx.x);
+    const MatDev M = L.mats[mi];
+    const int K = M.cols;
+    const int units = KIND == VGX_T3 ? (M.rows + 1) / 2 : M.rows;
+    const int unit0 = (blockIdx.x - M.blk_off) * (kWaves * RPI * RI) + wave * (RPI * RI);
+
+    // --- weight chunk geometry
+    const int nch = KIND == VGX_Q8 ? (K >> 4) : (K >> 5);
+    const size_t ustride = KIND == VGX_Q8 ? (size_t)K : KIND == VGX_Q4 ? (size_t)(K >> 1)
+                                                                     : (size_t)(K >> 3) * 4;
+    const uint8_t* body = M.body;
+    const uint8_t* body3 = (EPI == EPI_GATE) ? L.mats2[mi].body : nullptr;
+    const int niter = (nch + LPR - 1) / LPR;
+
+    // Issue the first chunk's weight loads before staging x so the two
+    // latencies overlap.
+    uint4 w[RI], w3[RI];
+    uint32_t smv[RI], smv3[RI];
+#pragma unroll
+    for (int it = 0; it < RI; ++it) {
+        const int u = unit0 + it * RPI + rs;
+        const int c = cl;
+        const bool ok = u < units && c < nch;
+        w[it] = ok ? *reinterpret_cast<const uint4*>(body + (size_t)u * ustride + (size_t)c * 16)
+                   : make_uint4(0, 0, 0, 0);
+        if (EPI == EPI_GATE)
+            w3[it] = ok ? *reinterpret_cast<const uint4*>(body3 + (size_t)u * ustride + (size_t)c * 16)
+                        : make_uint4(0, 0, 0, 0);
+        if (KIND == VGX_Q4) {
+            smv[it] = ok ? M.sm[(size_t)u * nch + c] : 0u;
+            if (EPI == EPI_GATE) smv3[it] = ok ? L.mats2[mi].sm[(size_t)u * nch + c] : 0u;
+        }
+    }
+
+    // --- stage x planes (and the row-independent sums) in LDS
+    // the byte split's bias sums, per column half (the split epilogue adds the
+    // two halves separately; every other epilogue uses their total)
+    __shared__ int s_xsum[2];
+    if (threadIdx.x < 2) s_xsum[threadIdx.x] = 0;
+    uint32_t* lut = nullptr;
+    int* xg = nullptr;
+    const int plane_u4 = KIND == VGX_Q8 ? 2 * nch : 4 * nch;  // uint4 per plane block
+    if (KIND == VGX_T3) {
+        lut = reinterpret_cast<uint32_t*>(lds + plane_u4);
+        for (int b = threadIdx.x; b < 256; b += kThreads) lut[b] = t3_lut_entry((uint32_t)b);
+    }
+    if (KIND == VGX_Q4) xg = reinterpret_cast<int*>(lds + plane_u4);
+    __syncthreads();
+    int part[2] = {0, 0};
+    if (KIND == VGX_Q8) {
+        for (int c = threadIdx.x; c < nch; c += kThreads) {
+            const int hh = (EPI == EPI_SPLIT && c >= L.split_chunk) ? 1 : 0;
+            uint32_t d[8], xh[4], xl[4];
+            load_x16<XF32>(L.x, L.xf, c * 16, K, d);
+            planes16(d, xh, xl);
+            lds[2 * c] = make_uint4(xh[0], xh[1], xh[2], xh[3]);
+            lds[2 * c + 1] = make_uint4(xl[0], xl[1], xl[2], xl[3]);
+            for (int k = 0; k < 4; ++k) part[hh] = (int)udot4(xl[k], 0x01010101u, (uint32_t)part[hh]);
+        }
+    } else if (KIND == VGX_T3) {
+        for (int c = threadIdx.x; c < nch; c += kThreads) {
+            const int hh = (EPI == EPI_SPLIT && c >= L.split_chunk) ? 1 : 0;
+            uint32_t d[8], xh[4], xl[4], xh2[4], xl2[4];
+            load_x16<XF32>(L.x, L.xf, c * 32, K, d);
+            planes16(d, xh, xl);
+            load_x16<XF32>(L.x, L.xf, c * 32 + 16, K, d);
+            planes16(d, xh2, xl2);
+            lds[4 * c + 0] = make_uint4(xh[0], xh[1], xh[2], xh[3]);
+            lds[4 * c + 1] = make_uint4(xh2[0], xh2[1], xh2[2], xh2[3]);
+            lds[4 * c + 2] = make_uint4(xl[0], xl[1], xl[2], xl[3]);
+            lds[4 * c + 3] = make_uint4(xl2[0], xl2[1], xl2[2], xl2[3]);
+            for (int k = 0; k < 4; ++k) {
+                part[hh] += 256 * sdot4(xh[k], 0x01010101u, 0) + (int)udot4(xl[k], 0x01010101u, 0u);
+                part[hh] += 256 * sdot4(xh2[k], 0x01010101u, 0) + (int)udot4(xl2[k], 0x01010101u, 0u);
+            }
+        }
+    } else {  // Q4
+        for (int c = threadIdx.x; c < nch; c += kThreads) {
+            uint32_t d[8], d2[8];
+            load_x16<XF32>(L.x, L.xf, c * 32, K, d);
+            load_x16<XF32>(L.x, L.xf, c * 32 + 16, K, d2);
+            uint32_t he[4], le[4], ho[4], lo[4];
+            const uint32_t q0[4] = {d[0], d[1], d[2], d[3]}, q1[4] = {d[4], d[5], d[6], d[7]};
+            const uint32_t q2[4] = {d2[0], d2[1], d2[2], d2[3]}, q3[4] = {d2[4], d2[5], d2[6], d2[7]};
+            planes8eo(q0, le[0], he[0], lo[0], ho[0]);
+            planes8eo(q1, le[1], he[1], lo[1], ho[1]);
+            planes8eo(q2, le[2], he[2], lo[2], ho[2]);
+            planes8eo(q3, le[3], he[3], lo[3], ho[3]);
+            lds[4 * c + 0] = make_uint4(he[0], he[1], he[2], he[3]);
+            lds[4 * c + 1] = make_uint4(le[0], le[1], le[2], le[3]);
+            lds[4 * c + 2] = make_uint4(ho[0], ho[1], ho[2], ho[3]);
+            lds[4 * c + 3] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+            int X = 0;
+            for (int k = 0; k < 4; ++k) {
+                X += 256 * (sdot4(he[k], 0x01010101u, 0) + sdot4(ho[k], 0x01010101u, 0));
+                X += (int)(udot4(le[k], 0x01010101u, 0u) + udot4(lo[k], 0x01010101u, 0u));
+            }
+            xg[c] = X;
+        }
+    }
+    if (KIND != VGX_Q4) {
+        for (int o = 32; o >= 1; o >>= 1) {
+            part[0] += shfl_xor(part[0], o);
+            part[1] += shfl_xor(part[1], o);
+        }
+        if (lane == 0) {
+            atomicAdd(&s_xsum[0], part[0]);
+            atomicAdd(&s_xsum[1], part[1]);
+        }
+    }
+    __syncthreads();
+    const int xs0 = KIND == VGX_Q4 ? 0 : s_xsum[0], xs1 = KIND == VGX_Q4 ? 0 : s_xsum[1];
+
+    // --- main loop
+    if (KIND == VGX_Q4) {
+        double acc[RI][NV];
+#pragma unroll
+        for (int it = 0; it < RI; ++it)
+#pragma unroll
+            for (int k = 0; k < NV; ++k) acc[it][k] = 0.0;
+        const float ps = M.ps;
+        const float ps3 = (EPI == EPI_GATE) ? L.mats2[mi].ps : 0.0f;
+        for (int j = 0; j < niter; ++j) {
+            const int c = cl + j * LPR;
+            const bool cok = c < nch;
+            uint4 wn[RI], wn3[RI];
+            uint32_t sn[RI], sn3[RI];
+            const bool more = j + 1 < niter;
+            if (more) {
+#pragma unroll
+                for (int it = 0; it < RI; ++it) {
+                    const int u = unit0 + it * RPI + rs;
+                    const int cn = c + LPR;
+                    const bool ok = u < units && cn < nch;
+                    wn[it] = ok ? *reinterpret_cast<const uint4*>(body + (size_t)u * ustride + (size_t)cn * 16)
+                                : make_uint4(0, 0, 0, 0);
+                    sn[it] = ok ? M.sm[(size_t)u * nch + cn] : 0u;
+                    if (EPI == EPI_GATE) {
+                        wn3[it] = ok ? *reinterpret_cast<const uint4*>(body3 + (size_t)u * ustride + (size_t)cn * 16)
+                                     : make_uint4(0, 0, 0, 0);
+                        sn3[it] = ok ? L.mats2[mi].sm[(size_t)u * nch + cn] : 0u;
+                    }
+                }
+            }
+            if (cok) {
+                const uint4 xhe = lds[4 * c], xle = lds[4 * c + 1], xho = lds[4 * c + 2], xlo = lds[4 * c + 3];
+                const float Xg = (float)xg[c];
+                const int kk = (EPI == EPI_SPLIT && c >= L.split_chunk) ? 1 : 0;
+#pragma unroll
+                for (int it = 0; it < RI; ++it) {
+                    const int D = q4_chunk(w[it], xhe, xle, xho, xlo);
+                    const float sa = (float)(int16_t)(smv[it] & 0xFFFFu) * ps;
+                    const float ma = (float)(int16_t)(smv[it] >> 16) * ps;
+                    const float t1 = sa * (float)D;
+                    const float t2 = ma * Xg;
+                    const float t = t1 + t2;
+                    if (EPI == EPI_SPLIT) {
+                        if (kk) acc[it][NV - 1] += (double)t; else acc[it][0] += (double)t;
+                    } else {
+                        acc[it][0] += (double)t;
+                    }
+                    if (EPI == EPI_GATE) {
+                        const int D3 = q4_chunk(w3[it], xhe, xle, xho, xlo);
+                        const float sb = (float)(int16_t)(smv3[it] & 0xFFFFu) * ps3;
+                        const float mb = (float)(int16_t)(smv3[it] >> 16) * ps3;
+                        const float u1 = sb * (float)D3;
+                        const float u2 = mb * Xg;
+                        const float u = u1 + u2;
+                        acc[it][NV - 1] += (double)u;
+                    }
+                }
+            }
+            if (more) {
+#pragma unroll
+                for (int it = 0; it < RI; ++it) {
+                    w[it] = wn[it];
+                    smv[it] = sn[it];
+                    if (EPI == EPI_GATE) { w3[it] = wn3[it]; smv3[it] = sn3[it]; }
+                }
+            }
+        }
+        const int row_it = seg_reduce<LPR, RI, NV, double>(acc, cl);
+        if ((cl % (LPR / RI > 0 ? LPR / RI : 1)) == 0) {
+            const int u = unit0 + row_it * RPI + rs;
+            if (u < units) {
+                const float v = (float)acc[0][0];
+                if (EPI == EPI_STORE) {
+                    const float t = L.res ? v + (float)L.res[M.out_off + u] : v;
+                    static_cast<int16_t*>(L.y)[M.out_off + u] = (int16_t)q16_round(t);
+                } else if (EPI == EPI_STORE_F32) {
+                    static_cast<float*>(L.y)[M.out_off + u] = v * (1.0f / 256.0f);
+                } else if (EPI == EPI_SPLIT) {
+                    const float vb = (float)acc[0][NV - 1];
+                    const float t = v + (float)L.res[u];
+                    const float y1 = (float)q16_round(t);
+                    static_cast<int16_t*>(L.y)[u] = (int16_t)q16_round(vb + y1);
+                } else {  // gate
+                    const float vb = (float)acc[0][NV - 1];
+                    const float g = (float)q16_round(v), uu = (float)q16_round(vb);
+                    const float a = g / 256.0f;
+                    const float e = (float)exp(-(double)a);
+                    const float dn = 1.0f + e;
+                    const float r = a / dn;
+                    float o = r * (uu / 256.0f);
+                    o = o * ldexpf(1.0f, -L.hs);
+                    static_cast<int16_t*>(L.y)[u] = (int16_t)q16_round(o * 256.0f);
+                }
+            }
+        }
+        return;
+    }
+
+    // q8 and t3: exact int32 partial sums.  t3 carries two rows (a pair) per unit.
+    constexpr int ROWS_PER_UNIT = KIND == VGX_T3 ? 2 : 1;
+    constexpr int NI = 2 * NV * ROWS_PER_UNIT;  // ints per unit: (s1, s2) per row per half
+    int acc[RI][NI];
+#pragma unroll
+    for (int it = 0; it < RI; ++it)
+#pragma unroll
+        for (int k = 0; k < NI; ++k) acc[it][k] = 0;
+
+    for (int j = 0; j < niter; ++j) {
+        const int c = cl + j * LPR;
+        const bool cok = c < nch;
+        uint4 wn[RI], wn3[RI];
+        const bool more = j + 1 < niter;
+        if (more) {
+#pragma unroll
+            for (int it = 0; it < RI; ++it) {
+                const int u = unit0 + it * RPI + rs;
+                const int cn = c + LPR;
+                const bool ok = u < units && cn < nch;
+                wn[it] = ok ? *reinterpret_cast<const uint4*>(body + (size_t)u * ustride + (size_t)cn * 16)
+                            : make_uint4(0, 0, 0, 0);
+                if (EPI == EPI_GATE)
+                    wn3[it] = ok ? *reinterpret_cast<const uint4*>(body3 + (size_t)u * ustride + (size_t)cn * 16)
+                                 : make_uint4(0, 0, 0, 0);
+            }
+        }
+        if (cok) {
+            // column half for the split epilogue
+            const int hb = (EPI == EPI_SPLIT && c >= L.split_chunk) ? 1 : 0;
+            if (KIND == VGX_Q8) {
+                const uint4 xh = lds[2 * c], xl = lds[2 * c + 1];
+#pragma unroll
+                for (int it = 0; it < RI; ++it) {
+                    int s1 = 0;
+                    uint32_t s2 = 0;
+                    q8_chunk(w[it], xh, xl, s1, s2);
+                    const int o = 2 * hb;
+                    acc[it][o] += s1;
+                    acc[it][o + 1] += (int)s2;
+                    if (EPI == EPI_GATE) {
+                        int t1 = 0;
+                        uint32_t t2 = 0;
+                        q8_chunk(w3[it], xh, xl, t1, t2);
+                        acc[it][2] += t1;
+                        acc[it][3] += (int)t2;
+                    }
+                }
+            } else {  // T3: 4 texels = 32 columns of a row pair
+                const uint4 xh0 = lds[4 * c], xh1 = lds[4 * c + 1];
+                const uint4 xl0 = lds[4 * c + 2], xl1 = lds[4 * c + 3];
+                const uint32_t xh[8] = {xh0.x, xh0.y, xh0.z, xh0.w, xh1.x, xh1.y, xh1.z, xh1.w};
+                const uint32_t xl[8] = {xl0.x, xl0.y, xl0.z, xl0.w, xl1.x, xl1.y, xl1.z, xl1.w};
+#pragma unroll
+                for (int it = 0; it < RI; ++it) {
+#pragma unroll
+                    for (int m = 0; m < (EPI == EPI_GATE ? 2 : 1); ++m) {
+                        const uint4 wv = m == 0 ? w[it] : w3[it];
+                        const uint32_t td[4] = {wv.x, wv.y, wv.z, wv.w};
+                        int a1 = 0, b1 = 0;
+                        uint32_t a2 = 0, b2 = 0;
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) {
+                            const uint32_t T = td[t];
+                            const uint32_t l0 = lut[T & 0xFFu], l1 = lut[(T >> 8) & 0xFFu];
+                            const uint32_t l2 = lut[(T >> 16) & 0xFFu], l3 = lut[T >> 24];
+                            a1 = sdot4(l0, xh[2 * t], a1);
+                            a1 = sdot4(l1, xh[2 * t + 1], a1);
+                            a2 = udot4(l0, xl[2 * t], a2);
+                            a2 = udot4(l1, xl[2 * t + 1], a2);
+                            b1 = sdot4(l2, xh[2 * t], b1);
+                            b1 = sdot4(l3, xh[2 * t + 1], b1);
+                            b2 = udot4(l2, xl[2 * t], b2);
+                            b2 = udot4(l3, xl[2 * t + 1], b2);
+                        }
+                        // layout per unit: [half or matrix][row of pair][s1, s2]
+                        const int o = 4 * (m + hb);
+                        acc[it][o + 0] += a1;
+                        acc[it][o + 1] += (int)a2;
+                        acc[it][o + 2] += b1;
+                        acc[it][o + 3] += (int)b2;
+                    }
+                }
+            }
+        }
+        if (more) {
+#pragma unroll
+            for (int it = 0; it < RI; ++it) {
+                w[it] = wn[it];
+                if (EPI == EPI_GATE) w3[it] = wn3[it];
+            }
+        }
+    }
+
+    const int row_it = seg_reduce<LPR, RI, NI, int>(acc, cl);
+    if ((cl % (LPR / RI > 0 ? LPR / RI : 1)) != 0) return;
+    const int u = unit0 + row_it * RPI + rs;
+    if (u >= units) return;
+    // bias of the byte split: q8 -128*sum(xl), t3 -sum(x)
+    // q8: -128*sum(xl) over the columns summed; t3: -sum(x)
+    const long long cmul = KIND == VGX_Q8 ? 128LL : 1LL;
+#pragma unroll
+    for (int hr = 0; hr < ROWS_PER_UNIT; ++hr) {
+        const int row = u * ROWS_PER_UNIT + hr;
+        if (row >= M.rows) break;
+        // value of (matrix-or-half h) for this row
+        auto val = [&](int h, const MatDev& MM) -> float {
+            const int o = KIND == VGX_T3 ? 4 * h + 2 * hr : 2 * h;
+            const long long corr = cmul * (EPI == EPI_SPLIT ? (h ? xs1 : xs0) : (long long)xs0 + xs1);
+            const long long s = 256LL * acc[0][o] + (long long)(uint32_t)acc[0][o + 1] - corr;
+            return (float)s * MM.wsr[row];
+        };
+        if (EPI == EPI_STORE) {
+            const float v = val(0, M);
+            const float t = L.res ? v + (float)L.res[M.out_off + row] : v;
+            static_cast<int16_t*>(L.y)[M.out_off + row] = (int16_t)q16_round(t);
+        } else if (EPI == EPI_STORE_F32) {
+            static_cast<float*>(L.y)[M.out_off + row] = val(0, M) * (1.0f / 256.0f);
+        } else if (EPI == EPI_SPLIT) {
+            const float va = val(0, M), vb = val(1, M);
+            const float y1 = (float)q16_round(va + (float)L.res[row]);
+            static_cast<int16_t*>(L.y)[row] = (int16_t)q16_round(vb + y1);
+        } else {  // gate
+            const float v1 = val(0, M), v3 = val(1, L.mats2[mi]);
+            const float g = (float)q16_round(v1), uu = (float)q16_round(v3);
+            const float a = g / 256.0f;
+            const float e = (float)exp(-(double)a);
+            const float dn = 1.0f + e;
+            const float r = a / dn;
+            float o = r * (uu / 256.0f);
+            o = o * ldexpf(1.0f, -L.hs);
+            static_cast<int16_t*>(L.y)[row] = (int16_t)q16_round(o * 256.0f);
+        }
+    }
+}
+
+// argmax with the first-maximum rule over int16 values, one block.
+__global__ void __launch_bounds__(1024) argmax_kernel(const int16_t* v, int n, int* out) {
+    __shared__ int sv[16], si[16];
+    int best = -65536, bi = 0x7fffffff;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        int x = v[i];
+        if (x > best) { best = x; bi = i; }  // i increases: the first max of this lane is kept
+    }
+    for (int o = 32; o >= 1; o >>= 1) {
+        int ob = __shfl_xor(best, o, 64), oi = __shfl_xor(bi, o, 64);
+        if (ob > best || (ob == best && oi < bi)) { best = ob; bi = oi; }
+    }
+    const int wv = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { sv[wv] = best; si[wv] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int nw = (blockDim.x + 63) / 64;
+        for (int k = 1; k < nw; ++k)
+            if (sv[k] > best || (sv[k] == best && si[k] < bi)) { best = sv[k]; bi = si[k]; }
+        *out = bi;
+    }
+}
+
+// Dequantisation to fp32, one thread per weight.
+__global__ void dequant_kernel(const MatDev M, float* out) {
+    const size_t n = (size_t)M.rows * M.cols;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const int r = (int)(i / M.cols), c = (int)(i % M.cols);
+        float v;
+        if (M.kind == VGX_Q8) {
+            v = (float)((int)M.body[i] - 128) * M.wsr[r];
+        } else if (M.kind == VGX_Q4) {
+            const uint8_t b = M.body[(size_t)r * (M.cols / 2) + c / 2];
+            const int nb = (c & 1) ? (b >> 4) : (b & 15);
+            const uint32_t sm = M.sm[(size_t)r * (M.cols / 32) + c / 32];
+            const float sa = (float)(int16_t)(sm & 0xFFFFu) * M.ps;
+            const float ma = (float)(int16_t)(sm >> 16) * M.ps;
+            v = (float)nb * sa + ma;
+        } else {
+            const size_t stride = (size_t)(M.cols / 8) * 4;
+            const uint8_t b = M.body[(size_t)(r / 2) * stride + (size_t)(c >> 3) * 4 + (r & 1) * 2 + ((c >> 2) & 1)];
+            const unsigned code = (b >> (2 * (c & 3))) & 3u;
+            const int lv = (code & 1u) ? ((code & 2u) ? -1 : 1) : 0;
+            v = (float)lv * M.wsr[r];
+        }
+        out[i] = v;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Dispatch tables.
+using KernFn = void (*)(const GemvLaunch);
+
+template <int KIND, int EPI, bool XF32>
+KernFn pick_kernel(int lpr, int ri) {
+#define VGX_K(LP, R) \
+    if (lpr == LP && ri == R) return gemv_kernel<KIND, LP, R, EPI, XF32>;
+    VGX_K(8, 1) VGX_K(8, 4) VGX_K(16, 1) VGX_K(16, 4) VGX_K(32, 1) VGX_K(32, 4) VGX_K(64, 1) VGX_K(64, 4)
+#undef VGX_K
+    return nullptr;
+}
+
+template <int KIND>
+KernFn pick_epi(int epi, int lpr, int ri) {
+    switch (epi) {
+        case EPI_STORE: return pick_kernel<KIND, EPI_STORE, false>(lpr, ri);
+        case EPI_STORE_F32: return pick_kernel<KIND, EPI_STORE_F32, true>(lpr, ri);
+        case EPI_GATE: return pick_kernel<KIND, EPI_GATE, false>(lpr, ri);
+        case EPI_SPLIT: return pick_kernel<KIND, EPI_SPLIT, false>(lpr, ri);
+    }
+    return nullptr;
+}
+
+size_t lds_bytes(int kind, int cols) {
+    if (kind == VGX_Q8) return (size_t)(cols / 16) * 32;
+    if (kind == VGX_T3) return (size_t)(cols / 32) * 64 + 256 * 4;
+    return (size_t)(cols / 32) * 64 + (size_t)(cols / 32) * 4;
+}
+
+}  // namespace
+
+// Lanes per row: enough chunks per lane (about four) to keep several loads in
+// flight, at most one wave per row; rows per lane: 4 when the matrix has
+// enough rows to give every CU several waves anyway, else 1.
+int vgx_gemv_plan(int kind, int rows, int cols, int num_cu, int* lpr, int* ri, int* rows_per_block) {
+    const int nch = kind == VGX_Q8 ? cols / 16 : cols / 32;
+    int l = 8;
+    while (l < 64 && l * 4 < nch) l <<= 1;
+    const int units = kind == VGX_T3 ? (rows + 1) / 2 : rows;
+    const int rpi = 64 / l;
+    const int waves1 = (units + rpi - 1) / rpi;
+    int r = waves1 >= 16 * num_cu ? 4 : 1;
+    *lpr = l;
+    *ri = r;
+    *rows_per_block = kWaves * rpi * r;  // in units (row pairs for t3)
+    return 0;
+}
+
+int vgx_gemv_launch(const GemvLaunch& L, hipStream_t s) {
+    KernFn fn = nullptr;
+    const int epi = L.xf ? EPI_STORE_F32 : (L.mats2 ? EPI_GATE : (L.split_chunk > 0 ? EPI_SPLIT : EPI_STORE));
+    switch (L.kind) {
+        case VGX_Q8: fn = pick_epi<VGX_Q8>(epi, L.lpr, L.ri); break;
+        case VGX_Q4: fn = pick_epi<VGX_Q4>(epi, L.lpr, L.ri); break;
+        case VGX_T3: fn = pick_epi<VGX_T3>(epi, L.lpr, L.ri); break;
+    }
+    if (!fn) return vgx_fail(VGX_EINVAL, "gemv: no kernel for this shape");
+    const size_t shm = lds_bytes(L.kind, L.cols);
+    if (shm > 160 * 1024) return vgx_fail(VGX_EINVAL, "gemv: activation row too long for LDS");
+    hipLaunchKernelGGL(fn, dim3(L.blocks), dim3(kThreads), shm, s, L);
+    VGX_LAUNCH_CHECK("gemv launch");
+    return VGX_OK;
+}
+
+int vgx_argmax_launch(const int16_t* v, int n, int* out, hipStream_t s) {
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, v, n, out);
+    VGX_LAUNCH_CHECK("argmax launch");
+    return VGX_OK;
+}
+
+int vgx_dequant_launch(const MatDev& d, float* out, hipStream_t s) {
+    const size_t n = (size_t)d.rows * d.cols;
+    int blocks = (int)((n + 255) / 256);
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(dequant_kernel, dim3(blocks), dim3(256), 0, s, d, out);
+    VGX_LAUNCH_CHECK("dequant launch");
+    return VGX_OK;
+}

@@ -1,0 +1,96 @@
+// Internal definitions shared by the libvgx translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "vgx.h"
+
+// ---------------------------------------------------------------------------
+// Error plumbing: every entry point returns a status and records a message on
+// the calling thread.
+int vgx_fail(int status, const std::string& msg);
+int vgx_hip_fail(hipError_t e, const char* what);
+
+#define VGX_HIP(call)                                                        \
+    do {                                                                     \
+        hipError_t e_ = (call);                                              \
+        if (e_ != hipSuccess) return vgx_hip_fail(e_, #call);                \
+    } while (0)
+
+#define VGX_LAUNCH_CHECK(what)                                               \
+    do {                                                                     \
+        hipError_t e_ = hipGetLastError();                                   \
+        if (e_ != hipSuccess) return vgx_hip_fail(e_, what);                 \
+    } while (0)
+
+// ---------------------------------------------------------------------------
+// Device-side description of one uploaded matrix.  The layout in HBM:
+//   Q8: body rows x cols bytes, q8u8 (level + 128), 256-byte aligned rows
+//       start at r*cols; wsr: rows f32 per-row scales (the value the kernel
+//       multiplies the exact integer dot product by).
+//   Q4: body rows x cols/2 nibble bytes (the container's), sm: rows x groups
+//       u32 = (u16)s16 | (u16)m16 << 16 (parts 1 and 2 interleaved so one
+//       4-byte load carries a group's scale and minimum), ps scalar.
+//   T3: body = the container's texel grid, ceil(rows/2) x cols/8 x 4 bytes;
+//       wsr: rows f32.
+struct MatDev {
+    const uint8_t* body;
+    const float* wsr;
+    const uint32_t* sm;
+    float ps;
+    int kind;
+    int rows, cols;
+    int out_off;  // row offset of this matrix in a group's concatenated output
+    int blk_off;  // first block of this matrix in a group launch
+    int pad0, pad1;
+};
+
+struct vgx_ctx {
+    int device = 0;
+    int num_cu = 256;
+    hipStream_t own = nullptr;
+    hipStream_t stream = nullptr;
+};
+
+struct vgx_mat {
+    vgx_ctx* ctx = nullptr;
+    MatDev d{};
+    MatDev* d_dev = nullptr;  // the descriptor in device memory (single launches)
+    size_t body_bytes = 0, plane_bytes = 0;
+    void* body_alloc = nullptr;
+    void* plane_alloc = nullptr;
+};
+
+struct vgx_group {
+    vgx_ctx* ctx = nullptr;
+    int n = 0, kind = 0, cols = 0, rows = 0, blocks = 0;
+    int lpr = 64, ri = 1;
+    MatDev* d_dev = nullptr;  // n descriptors with out_off / blk_off filled
+};
+
+// ---------------------------------------------------------------------------
+// Launch helpers implemented in vgx_gemv.hip.
+enum GemvEpi { EPI_STORE = 0, EPI_STORE_F32 = 1, EPI_GATE = 2, EPI_SPLIT = 3 };
+
+struct GemvLaunch {
+    const MatDev* mats;   // device descriptors
+    int nmat;
+    int blocks;           // total blocks
+    const int16_t* x;     // q16 input (or nullptr)
+    const float* xf;      // f32 input (EPI_STORE_F32)
+    const int16_t* res;   // residual (EPI_STORE / EPI_SPLIT)
+    void* y;              // int16 or f32 output
+    const MatDev* mats2;  // W3 for EPI_GATE
+    int hs;               // hidden store exponent (EPI_GATE)
+    int split_chunk;      // first chunk of the second column half (EPI_SPLIT)
+    int kind, cols, lpr, ri;
+};
+
+int vgx_gemv_plan(int kind, int rows, int cols, int num_cu, int* lpr, int* ri, int* rows_per_block);
+int vgx_gemv_launch(const GemvLaunch& L, hipStream_t s);
+int vgx_argmax_launch(const int16_t* v, int n, int* out, hipStream_t s);
+int vgx_dequant_launch(const MatDev& d, float* out, hipStream_t s);

@@ -1,0 +1,94 @@
+// RMSNorm and the q8 embedding row.
+#include <cmath>
+#include <string>
+
+#include "vgx_internal.h"
+
+#pragma clang fp contract(off)
+
+namespace {
+
+__device__ __forceinline__ int q16_round(float v) {
+    float f = floorf(v + 0.5f);
+    f = fminf(fmaxf(f, -32768.0f), 32767.0f);
+    return (int)f;
+}
+
+// GPU::rmsnorm (engine/src/gpu_upload.cpp:280-365) as one workgroup:
+// rms_stats_split's 32 partial sums of v^2 over contiguous slices of
+// ceil(dim/32) values, each on the 1/4096 grid (P = sum x^2 in Q units, stored
+// value floor(P/16 + 1/2)), their total ss, inv = inversesqrt(ss/dim + eps),
+// y = q16(x * inv * w).
+__global__ void __launch_bounds__(256) rmsnorm_kernel(const int16_t* x, const int16_t* w, int dim,
+                                                       float eps, int16_t* y) {
+    __shared__ long long part[32];
+    __shared__ float s_inv;
+    const int per = (dim + 31) / 32;
+    const int tid = threadIdx.x;
+    // 8 threads per partial slice
+    {
+        const int p = tid >> 3, sub = tid & 7;
+        long long P = 0;
+        for (int k = sub; k < per; k += 8) {
+            const int i = p * per + k;
+            if (i < dim) P += (long long)x[i] * x[i];
+        }
+        for (int o = 4; o >= 1; o >>= 1) P += __shfl_xor(P, o, 64);
+        if (sub == 0) part[p] = (P + 8) >> 4;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        long long tot = 0;
+        for (int p = 0; p < 32; ++p) tot += part[p];
+        const float ss = (float)tot / 4096.0f;
+        s_inv = (float)(1.0 / sqrt((double)(ss / (float)dim + eps)));
+    }
+    __syncthreads();
+    const float inv = s_inv;
+    for (int i = tid; i < dim; i += blockDim.x) {
+        const float xv = (float)x[i] / 256.0f;
+        const float wv = (float)w[i] / 256.0f;
+        const float v = (xv * inv) * wv;
+        y[i] = (int16_t)q16_round(v * 256.0f);
+    }
+}
+
+// Session::embedding, q8 rows (engine/src/session.cpp:362-365).
+__global__ void embed_q8_kernel(const int8_t* emb, const float* scale, int vocab, int dim,
+                                const int* token, int16_t* x) {
+    int tok = *token;
+    if (tok < 0) tok = 0;
+    if (tok >= vocab) tok = vocab - 1;
+    const float s = scale[tok];
+    for (int i = threadIdx.x + blockIdx.x * blockDim.x; i < dim; i += blockDim.x * gridDim.x) {
+        const float v = (float)emb[(size_t)tok * dim + i] * s;
+        float r = __builtin_rintf(v * 256.0f);
+        r = fminf(fmaxf(r, -32768.0f), 32767.0f);
+        x[i] = (int16_t)r;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int vgx_rmsnorm(vgx_ctx* ctx, int dim, const int16_t* x, const int16_t* w, float eps, int16_t* y) {
+    if (!ctx || !x || !w || !y) return vgx_fail(VGX_EINVAL, "vgx_rmsnorm: NULL argument");
+    if (dim <= 0 || dim > 65536) return vgx_fail(VGX_EINVAL, "vgx_rmsnorm: dim outside 1..65536");
+    VGX_HIP(hipSetDevice(ctx->device));
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(256), 0, ctx->stream, x, w, dim, eps, y);
+    VGX_LAUNCH_CHECK("rmsnorm launch");
+    return VGX_OK;
+}
+
+int vgx_embed_q8(vgx_ctx* ctx, const int8_t* emb, const float* emb_scale, int vocab, int dim,
+                 const int* token, int16_t* x) {
+    if (!ctx || !emb || !emb_scale || !token || !x) return vgx_fail(VGX_EINVAL, "vgx_embed_q8: NULL argument");
+    if (vocab <= 0 || dim <= 0) return vgx_fail(VGX_EINVAL, "vgx_embed_q8: empty shape");
+    VGX_HIP(hipSetDevice(ctx->device));
+    hipLaunchKernelGGL(embed_q8_kernel, dim3(1), dim3(256), 0, ctx->stream, emb, emb_scale, vocab, dim, token, x);
+    VGX_LAUNCH_CHECK("embed launch");
+    return VGX_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,240 @@
+"""Host-side mirror of the reference engine's GPU object over libvgx.
+
+`GPU` has the reference's entry points (engine/src/gpu.h:41-633: upload,
+matvec / matvec_add, ffn_split_chunked, rmsnorm, attention_block,
+kv_rope_write, logits_from) with the same argument meaning; device buffers are
+torch tensors on the GPU (plumbing only: every number is computed by libvgx).
+"""
+import ctypes
+
+import numpy as np
+import torch
+
+from . import lib as _l
+from .mmcf import Matrix
+
+
+def _ptr(t):
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _np_ptr(a):
+    return ctypes.c_void_p(0 if a is None else a.ctypes.data)
+
+
+class Mat:
+    """An uploaded weight matrix (GPU::upload's result)."""
+
+    def __init__(self, gpu, handle, m):
+        self.gpu, self.h, self.rows, self.cols, self.kind = gpu, handle, m.rows, m.cols, m.kind
+
+    @property
+    def weight_bytes(self):
+        return int(_l.load().vgx_mat_weight_bytes(self.h))
+
+    def free(self):
+        if self.h:
+            _l.load().vgx_mat_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Group:
+    """Matrices sharing one input, launched as one kernel (logits tiles)."""
+
+    def __init__(self, gpu, mats):
+        L = _l.load()
+        arr = (ctypes.c_void_p * len(mats))(*[m.h for m in mats])
+        h = ctypes.c_void_p()
+        _l.check(L.vgx_group_create(gpu.ctx, len(mats), arr, ctypes.byref(h)))
+        self.gpu, self.h, self.mats = gpu, h, list(mats)
+        self.rows = int(L.vgx_group_rows(h))
+
+    def gemv(self, x, out=None):
+        out = out if out is not None else torch.empty(self.rows, dtype=torch.int16, device=x.device)
+        _l.check(_l.load().vgx_gemv_group(self.gpu.ctx, self.h, _ptr(x), _ptr(out)))
+        return out
+
+    def gemv_f32(self, x, out=None):
+        out = out if out is not None else torch.empty(self.rows, dtype=torch.float32, device=x.device)
+        _l.check(_l.load().vgx_gemv_group_f32(self.gpu.ctx, self.h, _ptr(x), _ptr(out)))
+        return out
+
+    def logits_argmax(self, x, logits=None, token=None):
+        logits = logits if logits is not None else torch.empty(self.rows, dtype=torch.int16, device=x.device)
+        token = token if token is not None else torch.empty(1, dtype=torch.int32, device=x.device)
+        _l.check(_l.load().vgx_logits_argmax(self.gpu.ctx, self.h, _ptr(x), _ptr(logits), _ptr(token)))
+        return logits, token
+
+    def free(self):
+        if self.h:
+            _l.load().vgx_group_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Attention:
+    """GPU::init_attention's state: KV cache, RoPE table, q/k norm weights."""
+
+    def __init__(self, gpu, dim, heads, kv_heads, head_dim, seq, layers, kv_bits, rope_half, qk_norm,
+                 rope_cos, rope_sin, q_norm=None, k_norm=None, layer_is_attn=None):
+        L = _l.load()
+        self._keep = [np.ascontiguousarray(rope_cos, np.float32), np.ascontiguousarray(rope_sin, np.float32),
+                      None if q_norm is None else np.ascontiguousarray(q_norm, np.float32),
+                      None if k_norm is None else np.ascontiguousarray(k_norm, np.float32),
+                      None if layer_is_attn is None else np.ascontiguousarray(layer_is_attn, np.uint8)]
+        d = _l.AttnDesc(dim, heads, kv_heads, head_dim, seq, layers, kv_bits, int(rope_half), int(qk_norm),
+                        _np_ptr(self._keep[0]), _np_ptr(self._keep[1]), _np_ptr(self._keep[2]),
+                        _np_ptr(self._keep[3]), _np_ptr(self._keep[4]))
+        h = ctypes.c_void_p()
+        _l.check(L.vgx_attn_create(gpu.ctx, ctypes.byref(d), ctypes.byref(h)))
+        self.gpu, self.h, self.dim, self.seq = gpu, h, dim, seq
+        self.row_bytes = int(L.vgx_kv_row_bytes(h))
+
+    def kv_append(self, layer, pos, qkv):
+        _l.check(_l.load().vgx_kv_append(self.h, layer, pos, _ptr(qkv)))
+
+    def decode(self, layer, pos, qkv, out=None):
+        out = out if out is not None else torch.empty(self.dim, dtype=torch.int16, device=qkv.device)
+        _l.check(_l.load().vgx_attn_decode(self.h, layer, pos, _ptr(qkv), _ptr(out)))
+        return out
+
+    def block(self, layer, pos, qkv, out=None):
+        out = out if out is not None else torch.empty(self.dim, dtype=torch.int16, device=qkv.device)
+        _l.check(_l.load().vgx_attn_block(self.h, layer, pos, _ptr(qkv), _ptr(out)))
+        return out
+
+    def read_rows(self, layer, row0, nrows):
+        buf = np.empty(nrows * self.row_bytes, np.uint8)
+        _l.check(_l.load().vgx_kv_read_rows(self.h, layer, row0, nrows, _np_ptr(buf)))
+        return buf
+
+    def write_rows(self, layer, row0, data):
+        data = np.ascontiguousarray(data, np.uint8)
+        _l.check(_l.load().vgx_kv_write_rows(self.h, layer, row0, data.size // self.row_bytes, _np_ptr(data)))
+
+    def free(self):
+        if self.h:
+            _l.load().vgx_attn_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class GPU:
+    """One libvgx context on one device, issuing on torch's current stream."""
+
+    def __init__(self, device=0):
+        L = _l.load()
+        h = ctypes.c_void_p()
+        _l.check(L.vgx_ctx_create(device, ctypes.byref(h)))
+        self.ctx, self.device = h, torch.device("cuda", device)
+        self.use_torch_stream()
+
+    def use_torch_stream(self):
+        s = torch.cuda.current_stream(self.device).cuda_stream
+        _l.check(_l.load().vgx_ctx_set_stream(self.ctx, ctypes.c_void_p(s)))
+
+    def sync(self):
+        _l.check(_l.load().vgx_ctx_sync(self.ctx))
+
+    # -- weights
+    def upload(self, m: Matrix):
+        keep = [np.ascontiguousarray(m.body, np.uint8)]
+        plane = s16 = m16 = None
+        if m.plane is not None:
+            plane = np.ascontiguousarray(m.plane, np.float32)
+        if m.kind == "q4":
+            s16 = np.ascontiguousarray(m.s16, np.int16)
+            m16 = np.ascontiguousarray(m.m16, np.int16)
+        d = _l.WeightDesc(_l.KIND[m.kind], m.rows, m.cols, _np_ptr(keep[0]), keep[0].size, int(m.prebiased),
+                          float(m.scale), _np_ptr(plane), _np_ptr(s16), _np_ptr(m16), float(m.scale_mul))
+        h = ctypes.c_void_p()
+        _l.check(_l.load().vgx_mat_upload(self.ctx, ctypes.byref(d), ctypes.byref(h)))
+        return Mat(self, h, m)
+
+    def clone(self, mat):
+        h = ctypes.c_void_p()
+        _l.check(_l.load().vgx_mat_clone(self.ctx, mat.h, ctypes.byref(h)))
+        c = Mat.__new__(Mat)
+        c.gpu, c.h, c.rows, c.cols, c.kind = self, h, mat.rows, mat.cols, mat.kind
+        return c
+
+    def dequant(self, mat):
+        out = torch.empty((mat.rows, mat.cols), dtype=torch.float32, device=self.device)
+        _l.check(_l.load().vgx_dequant(self.ctx, mat.h, _ptr(out)))
+        return out
+
+    def group(self, mats):
+        return Group(self, mats)
+
+    # -- GEMV family
+    def matvec(self, mat, x, res=None, out=None):
+        """matvec_to / matvec_add: y = q16(W.x [+ res])."""
+        out = out if out is not None else torch.empty(mat.rows, dtype=torch.int16, device=x.device)
+        _l.check(_l.load().vgx_gemv(self.ctx, mat.h, _ptr(x), _ptr(res), _ptr(out)))
+        return out
+
+    def matvec_f32(self, mat, x, out=None):
+        out = out if out is not None else torch.empty(mat.rows, dtype=torch.float32, device=x.device)
+        _l.check(_l.load().vgx_gemv_f32(self.ctx, mat.h, _ptr(x), _ptr(out)))
+        return out
+
+    def matvec_add_split(self, mat, split, x, res, out=None):
+        """matvec_add(w2a) then matvec_add(w2b) over the column halves."""
+        out = out if out is not None else torch.empty(mat.rows, dtype=torch.int16, device=x.device)
+        _l.check(_l.load().vgx_gemv_add_split(self.ctx, mat.h, split, _ptr(x), _ptr(res), _ptr(out)))
+        return out
+
+    def ffn_gate(self, w1, w3, x, hs=0, out=None):
+        out = out if out is not None else torch.empty(w1.rows, dtype=torch.int16, device=x.device)
+        _l.check(_l.load().vgx_ffn_gate(self.ctx, w1.h, w3.h, _ptr(x), hs, _ptr(out)))
+        return out
+
+    def rmsnorm(self, x, w, eps=1e-5, out=None):
+        out = out if out is not None else torch.empty_like(x)
+        _l.check(_l.load().vgx_rmsnorm(self.ctx, x.numel(), _ptr(x), _ptr(w), float(eps), _ptr(out)))
+        return out
+
+    def embed_q8(self, emb, emb_scale, token, out=None):
+        vocab, dim = emb.shape
+        out = out if out is not None else torch.empty(dim, dtype=torch.int16, device=emb.device)
+        _l.check(_l.load().vgx_embed_q8(self.ctx, _ptr(emb), _ptr(emb_scale), vocab, dim, _ptr(token), _ptr(out)))
+        return out
+
+    def attention(self, **kw):
+        return Attention(self, **kw)
+
+    def close(self):
+        if self.ctx:
+            _l.load().vgx_ctx_destroy(self.ctx)
+            self.ctx = None
+
+
+def quantize_act(v):
+    """quantize_act on the host (libvgx's helper)."""
+    v = np.ascontiguousarray(v, np.float32).ravel()
+    q = np.empty(v.size, np.int16)
+    _l.load().vgx_quantize_act(_np_ptr(v), v.size, _np_ptr(q))
+    return q
+
+
+def x_pack_i16_2(v):
+    v = np.ascontiguousarray(v, np.float32).ravel()
+    out = np.empty(4 * ((v.size + 1) // 2), np.uint8)
+    _l.load().vgx_x_pack_i16_2(_np_ptr(v), v.size, _np_ptr(out))
+    return out
