@@ -63,6 +63,48 @@ def cpu_baseline(seconds):
                       "%.1f s, oracle exact-integer q8 GEMV with OpenMP" % (passes, dt)}
 
 
+def decode_bench(runs):
+    """MiniMind3-64M q8 (per-row scales), KV q16, SEQ 256: 32 prompt tokens
+    then 64 greedy tokens through the engine; decode tokens/s over the 63
+    steps after the prompt, median of `runs` after one warm-up run."""
+    import numpy as np
+    from vgx import synth
+    from vgx.engine import Engine
+
+    spec = synth.minimind3_spec(seq=256)
+    blob = synth.container(spec, "q8", seed=0, q8_row=True)
+    prompt = synth.prompt(32, spec.vocab, seed=0)
+    eng = Engine(blob, kv_bits=16)
+    eng.generate(prompt, 64)
+    pf, dc, toks = [], [], None
+    for _ in range(runs):
+        toks, p, d = eng.generate(prompt, 64)
+        pf.append(p)
+        dc.append(d)
+    eng.close()
+    ms_tok = float(np.median(dc)) / 63
+    return blob, prompt, toks, {
+        "model": "MiniMind3-64M-shaped, q8 per-row, seed 0", "prompt": 32, "gen": 64, "seq": 256, "kv": "q16",
+        "tokens_per_s": round(1000.0 / ms_tok, 1), "ms_per_token": round(ms_tok, 4),
+        "prefill_ms": round(float(np.median(pf)), 3), "runs": runs}
+
+
+def decode_cpu_baseline(blob, prompt, steps):
+    """The float CPU path (oracle/model.py FModel: the reference's numpy
+    forward semantics on the dequantised container) for `steps` positions."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as o
+    from model import FModel
+
+    f = FModel(blob)
+    t0 = time.perf_counter()
+    for pos in range(steps):
+        f.step(int(prompt[pos % len(prompt)]), pos)
+    dt = time.perf_counter() - t0
+    return {"tokens_per_s": round(steps / dt, 2), "cores": o.threads(),
+            "sample": "%d positions of the float path (numpy fp32 BLAS, dequantised q8 weights)" % steps}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -72,6 +114,8 @@ def main():
     ap.add_argument("--warm-reps", type=int, default=1000)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--decode-runs", type=int, default=5)
+    ap.add_argument("--cpu-decode-steps", type=int, default=16)
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py runs on one GPU: the decode path is single-device (see DESIGN.md); --gpus %d "
@@ -160,9 +204,18 @@ def main():
                      "kernel": "gemv_kernel<q8, EPI_STORE_F32> (one launch per shape per step)"},
         "gemv": shapes_out,
     }
+    g.close()
+    for s in per_shape:
+        s["grp"].free()
+        for mm in s["mats"]:
+            mm.free()
+    torch.cuda.synchronize()
+    blob, prompt, toks, dec = decode_bench(args.decode_runs)
+    out["decode"] = dec
+    out["decode_tokens_per_s"] = dec["tokens_per_s"]
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
-    g.close()
+        out["decode"]["cpu_float_path"] = decode_cpu_baseline(blob, prompt, args.cpu_decode_steps)
     print(json.dumps(out))
 
 

@@ -1,0 +1,46 @@
+/*
+ * vgx_engine.h -- the decode engine above libvgx: MMCF loader, layer loop
+ * and greedy generation, as one C-ABI object.
+ *
+ * It re-provides the reference's Session (engine/src/session.h:41-93) over
+ * libvgx: vgx_engine_step is Session::step (forward_gpu_hidden + the logits
+ * readback, engine/src/session.cpp:1797-1821); vgx_engine_generate is the
+ * chat decode loop with greedy selection (engine/src/chat.cpp:313-352,
+ * argmax_token's first-maximum rule) with the token chained on the device,
+ * as Session::step_greedy does with GPU_ARGMAX (engine/src/session.cpp:1827-1842).
+ * Status codes are libvgx's (vgx.h).
+ */
+#ifndef VGX_ENGINE_H
+#define VGX_ENGINE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct vgx_engine vgx_engine;
+
+/* Open an MMCF container (a path, or bytes the caller keeps alive until
+ * close) on `device`.  seq: KV length, 0 = the container's; kv_bits: 16 or 8
+ * (the reference's KV=q16 / KV=q8). */
+int vgx_engine_open(const char* path, int device, int seq, int kv_bits, vgx_engine** out);
+int vgx_engine_open_bytes(const void* data, size_t size, int device, int seq, int kv_bits,
+                          vgx_engine** out);
+int vgx_engine_close(vgx_engine* e);
+int vgx_engine_info(const vgx_engine* e, int* dim, int* layers, int* vocab, int* seq);
+/* One position: logits_host (vocab int16, q16 grid) and next (argmax) may be NULL. */
+int vgx_engine_step(vgx_engine* e, int token, int pos, int16_t* logits_host, int* next);
+/* Greedy generation: n_prompt tokens at positions 0.., then n_gen tokens into
+ * out.  prefill_ms covers the prompt (its last step yields out[0]); decode_ms
+ * the n_gen-1 steps after it.  Either timing pointer may be NULL. */
+int vgx_engine_generate(vgx_engine* e, const int* prompt, int n_prompt, int n_gen, int* out,
+                        double* prefill_ms, double* decode_ms);
+/* The message of the last failed engine call on this thread. */
+const char* vgx_engine_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

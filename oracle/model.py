@@ -1,0 +1,250 @@
+"""Whole-model oracle: the reference engine's decode step on the q16 grid, and
+the reference's float CPU path, over an MMCF container.
+
+TEST INFRASTRUCTURE ONLY (tests/, smoke, bench.py's cpu_baseline).  The
+container is parsed here with its own small reader (the layout of
+docs/checkpoint-container.md:62-271), independent of the product's.
+
+QModel.step follows Session::forward_gpu_hidden (engine/src/session.cpp:1459-1584)
+with the GPU kernels' numerics (oracle.py); FModel.step follows
+engine/tools/ref_forward.py:47-115 on the dequantised container weights, with
+the engine's conventions (block RMSNorm eps from key 11 or 1e-5, q/k RMSNorm
+eps 1e-6, RoPE tables of Session, engine/src/session.cpp:188-202).
+"""
+import struct
+
+import numpy as np
+
+import oracle as o
+
+
+def parse(blob):
+    """(meta dict, {id: (dtype, rows, cols, scale, body ndarray uint8)})."""
+    b = memoryview(blob)
+    assert bytes(b[:4]) == b"MMCF"
+    ver, hsz, n, _caps, moff, msize, doff, _fsize = struct.unpack_from("<HHIIIIQQ", b, 4)
+    assert ver == 2 and hsz == 64
+    meta, p = {}, moff
+    while p + 8 <= moff + msize:
+        key, _t, ln = struct.unpack_from("<HHI", b, p)
+        meta[key] = bytes(b[p + 8:p + 8 + ln])
+        p += 8 + ln
+    recs = {}
+    table = doff - 48 * n
+    for i in range(n):
+        r = table + 48 * i
+        tid, dt, _fl, _g, _pad = struct.unpack_from("<HBBBB", b, r)
+        rows, cols, off, nb = struct.unpack_from("<IIQQ", b, r + 6)
+        scale, = struct.unpack_from("<f", b, r + 34)
+        recs[tid] = (dt, rows, cols, scale, np.frombuffer(b[doff + off:doff + off + nb], np.uint8))
+    return meta, recs
+
+
+class _Mat:
+    def __init__(self, kind, rows, cols, body, scale, prebiased=1, plane=None, s16=None, m16=None, mul=1.0):
+        self.kind, self.rows, self.cols, self.body, self.scale = kind, rows, cols, body, scale
+        self.prebiased, self.plane, self.s16, self.m16, self.mul = prebiased, plane, s16, m16, mul
+
+    def wsr(self):
+        s = np.float32(self.scale) * (np.float32(127) if self.kind == "t3" else np.float32(1))
+        return o.row_scales(self.rows, float(np.float32(s) * np.float32(self.mul)), self.plane)
+
+    def cols_slice(self, a, b):
+        if self.kind == "q8":
+            body = np.ascontiguousarray(self.body.reshape(self.rows, self.cols)[:, a:b])
+            return _Mat("q8", self.rows, b - a, body, self.scale, self.prebiased, self.plane, mul=self.mul)
+        if self.kind == "q4":
+            g = self.cols // 32
+            body = np.ascontiguousarray(self.body.reshape(self.rows, self.cols // 2)[:, a // 2:b // 2])
+            s16 = np.ascontiguousarray(self.s16.reshape(self.rows, g)[:, a // 32:b // 32])
+            m16 = np.ascontiguousarray(self.m16.reshape(self.rows, g)[:, a // 32:b // 32])
+            return _Mat("q4", self.rows, b - a, body, self.scale, s16=s16, m16=m16, mul=self.mul)
+        body = np.ascontiguousarray(self.body.reshape((self.rows + 1) // 2, self.cols // 8, 4)[:, a // 8:b // 8])
+        return _Mat("t3", self.rows, b - a, body, self.scale, plane=self.plane, mul=self.mul)
+
+    def rowval(self, x):
+        if self.kind == "q8":
+            return o.rowval_q8(self.body, self.prebiased, self.rows, self.cols, self.wsr(), x)
+        if self.kind == "q4":
+            ps = float(np.float32(self.scale) * np.float32(self.mul))
+            return o.rowval_q4(self.body, self.s16, self.m16, ps, self.rows, self.cols, x)
+        return o.rowval_t3(self.body, self.rows, self.cols, self.wsr(), x)
+
+    def dequant(self):
+        if self.kind == "q8":
+            return o.dequant_q8(self.body, self.prebiased, self.rows, self.cols, self.wsr())
+        if self.kind == "q4":
+            ps = float(np.float32(self.scale) * np.float32(self.mul))
+            return o.dequant_q4(self.body, self.s16, self.m16, ps, self.rows, self.cols)
+        return o.dequant_t3(self.body, self.rows, self.cols, self.wsr())
+
+
+class _Base:
+    def __init__(self, blob, seq=None, kv_bits=16):
+        meta, self.recs = parse(blob)
+        d = struct.unpack("<7i", meta[1])
+        self.dim, self.hidden, self.layers, self.heads, self.kv_heads, self.vocab, seq0 = d
+        self.seq = seq or seq0
+        th, half, qk, _ = struct.unpack("<fBBH", meta[2])
+        self.theta, self.rope_half, self.qk_norm = th, half, qk
+        self.eps = struct.unpack("<f", meta[11])[0] if 11 in meta else 1e-5
+        self.hid = list(meta.get(15, b"")) or [0] * self.layers
+        self.hd = self.dim // self.heads
+        self.kv_dim = self.kv_heads * self.hd
+        self.kv_bits = kv_bits
+        self.chunk = (self.hidden + 1) // 2 if self.hidden > 2048 else 0
+        self.mats = []
+        for l in range(self.layers):
+            L = {"qkv": self.mat(0x10, l), "wo": self.mat(0x11, l)}
+            if (0x14 | l << 8) in self.recs:
+                w13 = self.mat(0x14, l)
+                L["w1"], L["w3"] = self.rows_of(w13, 0, self.hidden), self.rows_of(w13, self.hidden, 2 * self.hidden)
+            else:
+                L["w1"], L["w3"] = self.mat(0x12, l), self.mat(0x13, l)
+            L["w2"] = self.mat(0x15, l, mul=float(1 << self.hid[l]))
+            self.mats.append(L)
+        self.emb = self.recs[1][4].view(np.int8).reshape(self.vocab, self.dim)
+        self.es = self.recs[2][4].view(np.float32)
+        self.tiles = []
+        i = 0
+        while (0x20 | i << 8) in self.recs:
+            self.tiles.append(self.mat(0x20, i))
+            i += 1
+        if not self.tiles:
+            unit = self.es.max()
+            for st in range(0, self.vocab, 1536):
+                rows = min(1536, self.vocab - st)
+                body = np.ascontiguousarray(self.emb[st:st + rows]).view(np.uint8)
+                self.tiles.append(_Mat("q8", rows, self.dim, body, float(unit), 0,
+                                       (self.es[st:st + rows] / np.float32(unit)).astype(np.float32)))
+        f32 = lambda k: self.recs[k][4].view(np.float32)
+        self.rms_att = f32(3).reshape(self.layers, self.dim)
+        self.rms_ffn = f32(4).reshape(self.layers, self.dim)
+        self.rms_final = f32(5)
+        self.qn = f32(6).reshape(self.layers, self.hd) if self.qk_norm else None
+        self.kn = f32(7).reshape(self.layers, self.hd) if self.qk_norm else None
+        self.rcos, self.rsin = o.rope_cos_sin(self.theta, self.hd, self.seq)
+
+    def mat(self, kind, layer, mul=1.0):
+        base = kind | (layer << 8)
+        dt, rows, cols, scale, body = self.recs[base]
+        plane = self.recs[base | (3 << 14)][4].view(np.float32) if (base | (3 << 14)) in self.recs else None
+        if dt in (2, 3):
+            return _Mat("q8", rows, cols, body, scale, 1 if dt == 2 else 0, plane, mul=mul)
+        if dt == 7:
+            return _Mat("t3", rows, cols, body, scale, plane=plane, mul=mul)
+        if dt == 4:
+            return _Mat("q4", rows, cols, body, scale, s16=self.recs[base | (1 << 14)][4].view(np.int16),
+                        m16=self.recs[base | (2 << 14)][4].view(np.int16), mul=mul)
+        raise ValueError("dtype %d" % dt)
+
+    @staticmethod
+    def rows_of(m, a, b):
+        if m.kind == "q8":
+            return _Mat("q8", b - a, m.cols, m.body.reshape(m.rows, m.cols)[a:b].ravel(), m.scale, m.prebiased,
+                        None if m.plane is None else m.plane[a:b], mul=m.mul)
+        if m.kind == "q4":
+            g = m.cols // 32
+            return _Mat("q4", b - a, m.cols, m.body.reshape(m.rows, m.cols // 2)[a:b].ravel(), m.scale,
+                        s16=m.s16.reshape(m.rows, g)[a:b].ravel(), m16=m.m16.reshape(m.rows, g)[a:b].ravel(),
+                        mul=m.mul)
+        st = (m.cols // 8) * 4
+        return _Mat("t3", b - a, m.cols, m.body[(a // 2) * st:((b + 1) // 2) * st], m.scale,
+                    plane=m.plane[a:b], mul=m.mul)
+
+
+class QModel(_Base):
+    """The engine's decode step on the q16 grid; logits are q16 integers."""
+
+    def __init__(self, blob, seq=None, kv_bits=16):
+        super().__init__(blob, seq, kv_bits)
+        self.cfg = o.attn_cfg(self.dim, self.heads, self.kv_heads, self.hd, self.seq, kv_bits,
+                              self.rope_half, self.qk_norm)
+        self.rtab = o.rope_table(self.rcos, self.rsin)
+        self.kv = [np.zeros(self.seq * o.kv_row_bytes(self.cfg), np.uint8) for _ in range(self.layers)]
+        self.w_att = [o.quantize_act(self.rms_att[l]) for l in range(self.layers)]
+        self.w_ffn = [o.quantize_act(self.rms_ffn[l]) for l in range(self.layers)]
+        self.w_fin = o.quantize_act(self.rms_final)
+        self.qnq = [o.quantize_act(self.qn[l]) for l in range(self.layers)] if self.qk_norm else None
+        self.knq = [o.quantize_act(self.kn[l]) for l in range(self.layers)] if self.qk_norm else None
+        if self.chunk:
+            self.w2ab = [(L["w2"].cols_slice(0, self.chunk), L["w2"].cols_slice(self.chunk, self.hidden))
+                         for L in self.mats]
+
+    def step(self, token, pos, want_logits=True):
+        h = o.embed_q8(self.emb, self.es, token)
+        for l, L in enumerate(self.mats):
+            xb = o.rmsnorm(h, self.w_att[l], self.eps)
+            qkv = o.store(L["qkv"].rowval(xb))
+            att = o.attn_block(self.cfg, qkv, self.qnq[l] if self.qnq else None,
+                               self.knq[l] if self.knq else None, self.rtab, pos, self.kv[l])
+            x1 = o.store(L["wo"].rowval(att), h)
+            xb = o.rmsnorm(x1, self.w_ffn[l], self.eps)
+            hb = o.gate(L["w1"].rowval(xb), L["w3"].rowval(xb), self.hid[l])
+            if self.chunk:
+                a, b = self.w2ab[l]
+                h = o.store(b.rowval(hb[self.chunk:]), o.store(a.rowval(hb[:self.chunk]), x1))
+            else:
+                h = o.store(L["w2"].rowval(hb), x1)
+        if not want_logits:
+            return None
+        xf = o.rmsnorm(h, self.w_fin, self.eps)
+        return np.concatenate([o.store(t.rowval(xf)) for t in self.tiles])
+
+
+class FModel(_Base):
+    """The float CPU path on the dequantised container weights."""
+
+    def __init__(self, blob, seq=None):
+        super().__init__(blob, seq)
+        # key 15's 2^k on w2 only undoes the hidden's q16 store scale, which
+        # the float path does not apply
+        self.W = []
+        for L in self.mats:
+            w2 = L["w2"]
+            L = dict(L, w2=_Mat(w2.kind, w2.rows, w2.cols, w2.body, w2.scale, w2.prebiased, w2.plane,
+                                w2.s16, w2.m16, 1.0))
+            self.W.append({k: m.dequant() for k, m in L.items()})
+        self.head = np.concatenate([t.dequant() for t in self.tiles])
+        self.kc = np.zeros((self.layers, self.seq, self.kv_heads, self.hd), np.float32)
+        self.vc = np.zeros_like(self.kc)
+
+    def _rope(self, x, pos):
+        c, s = self.rcos[pos], self.rsin[pos]
+        if self.rope_half:
+            x1, x2 = x[..., :self.hd // 2], x[..., self.hd // 2:]
+            return np.concatenate([x1 * c - x2 * s, x2 * c + x1 * s], axis=-1)
+        out = np.empty_like(x)
+        out[..., 0::2] = x[..., 0::2] * c - x[..., 1::2] * s
+        out[..., 1::2] = x[..., 1::2] * c + x[..., 0::2] * s
+        return out
+
+    @staticmethod
+    def _rms(x, w, eps):
+        return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps) * w
+
+    def step(self, token, pos):
+        x = self.emb[token].astype(np.float32) * self.es[token]
+        for l, W in enumerate(self.W):
+            xn = self._rms(x, self.rms_att[l], self.eps)
+            qkv = W["qkv"] @ xn
+            q = qkv[:self.dim].reshape(self.heads, self.hd)
+            k = qkv[self.dim:self.dim + self.kv_dim].reshape(self.kv_heads, self.hd)
+            v = qkv[self.dim + self.kv_dim:].reshape(self.kv_heads, self.hd)
+            if self.qk_norm:
+                q = self._rms(q, self.qn[l], 1e-6)
+                k = self._rms(k, self.kn[l], 1e-6)
+            q, k = self._rope(q, pos), self._rope(k, pos)
+            self.kc[l, pos], self.vc[l, pos] = k, v
+            rep = self.heads // self.kv_heads
+            K = np.repeat(self.kc[l, :pos + 1], rep, axis=1)
+            V = np.repeat(self.vc[l, :pos + 1], rep, axis=1)
+            sc = np.einsum("hd,thd->ht", q, K) / np.sqrt(self.hd)
+            p = np.exp(sc - sc.max(axis=1, keepdims=True))
+            p /= p.sum(axis=1, keepdims=True)
+            att = np.einsum("ht,thd->hd", p, V).reshape(self.dim)
+            x = x + W["wo"] @ att
+            xn = self._rms(x, self.rms_ffn[l], self.eps)
+            g, u = W["w1"] @ xn, W["w3"] @ xn
+            x = x + W["w2"] @ ((g / (1 + np.exp(-g))) * u)
+        return self.head @ self._rms(x, self.rms_final, self.eps)

@@ -12,8 +12,8 @@ from vgx import lib as vl
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def declared():
-    text = open(os.path.join(ROOT, "include", "vgx.h")).read()
+def declared(header="vgx.h"):
+    text = open(os.path.join(ROOT, "include", header)).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(vgx_[a-z0-9_]+)\s*\(", text)))
 
@@ -25,6 +25,15 @@ def test_every_declared_symbol_is_exported():
     missing = [n for n in names if not hasattr(L, n)]
     assert not missing, missing
     assert sorted(vl.exported_symbols()) == names
+
+
+def test_engine_symbols_exported():
+    from vgx import engine as ve
+    L = ve.load()
+    names = declared("vgx_engine.h")
+    assert not [n for n in names if not hasattr(L, n)]
+    assert sorted(ve.exported_symbols()) == names
+    assert os.access(ve.CLI_PATH, os.X_OK)
 
 
 def test_host_only_calls():

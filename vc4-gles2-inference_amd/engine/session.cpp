@@ -1,0 +1,363 @@
+// The decode engine: weights from an MMCF container uploaded through libvgx,
+// the reference's fused GPU layer loop (Session::forward_gpu_hidden,
+// engine/src/session.cpp:1459-1584) issued as libvgx launches on one stream,
+// and greedy generation with the token kept on the device.
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "mmcf_reader.h"
+#include "vgx.h"
+#include "vgx_engine.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int st, const std::string& msg) {
+    g_err = msg;
+    return st;
+}
+
+}  // namespace
+
+struct vgx_engine {
+    vgxe::Container c;
+    vgxe::ModelMeta m;
+    vgx_ctx* ctx = nullptr;
+    vgx_attn* attn = nullptr;
+    struct Layer {
+        vgx_mat *qkv = nullptr, *wo = nullptr, *w1 = nullptr, *w3 = nullptr, *w2 = nullptr;
+        int16_t *rms_att = nullptr, *rms_ffn = nullptr;
+        int hs = 0;
+    };
+    std::vector<Layer> L;
+    std::vector<vgx_mat*> head_tiles;
+    vgx_group* head = nullptr;
+    int8_t* emb = nullptr;
+    float* emb_scale = nullptr;
+    int16_t *h = nullptr, *x1 = nullptr, *xb = nullptr, *qkv = nullptr, *att = nullptr, *hbuf = nullptr;
+    int16_t *xf = nullptr, *logits = nullptr, *rms_final = nullptr;
+    int* toks = nullptr;  // device token slots: [0, seq) prompt/decode history, [seq] the host step's
+    int seq = 0, kv_bits = 16, ffn_chunk = 0;
+    std::vector<void*> allocs;
+
+    ~vgx_engine() {
+        for (auto& l : L) {
+            vgx_mat_free(l.qkv); vgx_mat_free(l.wo); vgx_mat_free(l.w1); vgx_mat_free(l.w3); vgx_mat_free(l.w2);
+        }
+        vgx_group_free(head);
+        for (vgx_mat* t : head_tiles) vgx_mat_free(t);
+        vgx_attn_free(attn);
+        for (void* p : allocs) (void)hipFree(p);
+        vgx_ctx_destroy(ctx);
+    }
+
+    template <typename T>
+    int dalloc(T** p, size_t n) {
+        void* q = nullptr;
+        hipError_t e = hipMalloc(&q, n * sizeof(T) + 16);
+        if (e != hipSuccess) return fail(VGX_ENOMEM, std::string("hipMalloc: ") + hipGetErrorString(e));
+        allocs.push_back(q);
+        *p = static_cast<T*>(q);
+        return VGX_OK;
+    }
+
+    template <typename T>
+    int upload(T** p, const T* src, size_t n) {
+        int st = dalloc(p, n);
+        if (st) return st;
+        hipError_t e = hipMemcpy(*p, src, n * sizeof(T), hipMemcpyHostToDevice);
+        return e == hipSuccess ? VGX_OK : fail(VGX_EHIP, hipGetErrorString(e));
+    }
+
+    // One weight matrix (rows r0..r1 of the record) through vgx_mat_upload:
+    // GPU::upload's job (engine/src/gpu_upload.cpp:20-192), the bytes as the
+    // container holds them.
+    int upload_mat(int kind, int layer, int r0, int r1, float scale_mul, vgx_mat** out) {
+        const vgxe::Record* r = c.find(kind, layer, 0);
+        if (!r) return fail(VGX_EINVAL, "missing tensor kind 0x" + std::to_string(kind) + " layer " + std::to_string(layer));
+        if (r1 < 0) r1 = (int)r->rows;
+        const vgxe::Record* plane = c.find(kind, layer, 3);
+        vgx_weight_desc d{};
+        d.rows = r1 - r0;
+        d.cols = (int)r->cols;
+        d.scale = r->scale;
+        d.scale_mul = scale_mul;
+        if (plane && (plane->rows != r->rows || plane->bytes != (uint64_t)r->rows * 4))
+            return fail(VGX_EINVAL, "row plane does not match its matrix");
+        d.row_plane = plane ? reinterpret_cast<const float*>(plane->body) + r0 : nullptr;
+        switch (r->dtype) {
+            case vgxe::DT_Q8U8:
+            case vgxe::DT_Q8I8:
+                d.kind = VGX_Q8;
+                d.prebiased = r->dtype == vgxe::DT_Q8U8;
+                d.body = r->body + (size_t)r0 * r->cols;
+                d.body_bytes = (size_t)d.rows * r->cols;
+                break;
+            case vgxe::DT_Q4: {
+                const vgxe::Record* s = c.find(kind, layer, 1);
+                const vgxe::Record* mn = c.find(kind, layer, 2);
+                if (!s || !mn) return fail(VGX_EINVAL, "q4 matrix without its scale/min planes");
+                const size_t g = r->cols / 32;
+                d.kind = VGX_Q4;
+                d.body = r->body + (size_t)r0 * (r->cols / 2);
+                d.body_bytes = (size_t)d.rows * (r->cols / 2);
+                d.q4_scale = reinterpret_cast<const int16_t*>(s->body) + (size_t)r0 * g;
+                d.q4_min = reinterpret_cast<const int16_t*>(mn->body) + (size_t)r0 * g;
+                break;
+            }
+            case vgxe::DT_T3: {
+                if (r0 % 2) return fail(VGX_EINVAL, "t3 row slice off a row pair");
+                const size_t stride = (size_t)((r->cols + 7) / 8) * 4;
+                d.kind = VGX_T3;
+                d.body = r->body + (size_t)(r0 / 2) * stride;
+                d.body_bytes = (size_t)((d.rows + 1) / 2) * stride;
+                break;
+            }
+            default:
+                return fail(VGX_EINVAL, "tensor dtype " + std::to_string(r->dtype) + " is not a kernel matrix");
+        }
+        return vgx_mat_upload(ctx, &d, out);
+    }
+
+    int init(int device, int seq_req, int kv_req) {
+        m = c.meta();
+        if (!m.layer_conv.empty())
+            for (uint8_t t : m.layer_conv)
+                if (t) return fail(VGX_EINVAL, "conv (hybrid) layers are not supported by this engine yet");
+        seq = seq_req > 0 ? seq_req : m.seq;
+        kv_bits = kv_req;
+        if (kv_bits != 16 && kv_bits != 8) return fail(VGX_EINVAL, "kv_bits must be 16 or 8");
+        int st = vgx_ctx_create(device, &ctx);
+        if (st) return fail(st, vgx_last_error());
+        // split_ffn (engine/src/model.cpp:246-266): two chunks over 2048
+        ffn_chunk = m.hidden > 2048 ? (m.hidden + 1) / 2 : 0;
+        const int D = m.dim, hd = m.head_dim();
+        L.resize(m.layers);
+        std::vector<int16_t> q16(D);
+        const vgxe::Record* ra = c.find(vgxe::T_RMS_ATT);
+        const vgxe::Record* rf = c.find(vgxe::T_RMS_FFN);
+        const vgxe::Record* rfin = c.find(vgxe::T_RMS_FINAL);
+        if (ra->bytes != (uint64_t)m.layers * D * 4 || rf->bytes != ra->bytes || rfin->bytes != (uint64_t)D * 4)
+            return fail(VGX_EINVAL, "rms weight shapes");
+        for (int l = 0; l < m.layers; ++l) {
+            Layer& ly = L[l];
+            ly.hs = m.hid_scale.empty() ? 0 : m.hid_scale[l];
+            if ((st = upload_mat(vgxe::T_QKV, l, 0, -1, 0.0f, &ly.qkv))) return st;
+            if ((st = upload_mat(vgxe::T_WO, l, 0, -1, 0.0f, &ly.wo))) return st;
+            if (c.find(vgxe::T_W13, l)) {
+                if ((st = upload_mat(vgxe::T_W13, l, 0, m.hidden, 0.0f, &ly.w1))) return st;
+                if ((st = upload_mat(vgxe::T_W13, l, m.hidden, 2 * m.hidden, 0.0f, &ly.w3))) return st;
+            } else {
+                if ((st = upload_mat(vgxe::T_W1, l, 0, -1, 0.0f, &ly.w1))) return st;
+                if ((st = upload_mat(vgxe::T_W3, l, 0, -1, 0.0f, &ly.w3))) return st;
+            }
+            // Model::apply_hidden_scale (engine/src/model.cpp:407-429)
+            if ((st = upload_mat(vgxe::T_W2, l, 0, -1, ly.hs ? (float)(1u << ly.hs) : 0.0f, &ly.w2))) return st;
+            // the norm vectors on the q16 grid (make_q16_pair_texture = x_pack)
+            vgx_quantize_act(reinterpret_cast<const float*>(ra->body) + (size_t)l * D, D, q16.data());
+            if ((st = upload(&ly.rms_att, q16.data(), D))) return st;
+            vgx_quantize_act(reinterpret_cast<const float*>(rf->body) + (size_t)l * D, D, q16.data());
+            if ((st = upload(&ly.rms_ffn, q16.data(), D))) return st;
+        }
+        vgx_quantize_act(reinterpret_cast<const float*>(rfin->body), D, q16.data());
+        if ((st = upload(&rms_final, q16.data(), D))) return st;
+        // embedding (signed q8 rows + f32 row scales)
+        const vgxe::Record* e = c.find(vgxe::T_EMB);
+        const vgxe::Record* es = c.find(vgxe::T_EMB_SCALE);
+        if (e->dtype != vgxe::DT_Q8I8 || e->rows != (uint32_t)m.vocab || e->cols != (uint32_t)D ||
+            es->bytes != (uint64_t)m.vocab * 4)
+            return fail(VGX_EINVAL, "this engine reads q8 embedding rows");
+        if ((st = upload(&emb, reinterpret_cast<const int8_t*>(e->body), (size_t)m.vocab * D))) return st;
+        if ((st = upload(&emb_scale, reinterpret_cast<const float*>(es->body), (size_t)m.vocab))) return st;
+        // LM head: the logits tiles, or the embedding rows for a dedup head
+        // (engine/src/model.cpp:1566-1586)
+        for (int i = 0; c.find(vgxe::T_LOGITS, i); ++i) {
+            vgx_mat* t = nullptr;
+            if ((st = upload_mat(vgxe::T_LOGITS, i, 0, -1, 0.0f, &t))) return st;
+            head_tiles.push_back(t);
+        }
+        if (head_tiles.empty()) {
+            const float* s = reinterpret_cast<const float*>(es->body);
+            float unit = 0.0f;
+            for (int v = 0; v < m.vocab; ++v) unit = s[v] > unit ? s[v] : unit;
+            if (unit <= 0.0f) return fail(VGX_EINVAL, "a dedup head needs embedding scales");
+            for (int st0 = 0; st0 < m.vocab; st0 += 1536) {
+                const int rows = m.vocab - st0 < 1536 ? m.vocab - st0 : 1536;
+                std::vector<float> plane(rows);
+                for (int k = 0; k < rows; ++k) plane[k] = s[st0 + k] / unit;
+                vgx_weight_desc d{};
+                d.kind = VGX_Q8; d.rows = rows; d.cols = D; d.prebiased = 0; d.scale = unit;
+                d.body = e->body + (size_t)st0 * D; d.body_bytes = (size_t)rows * D; d.row_plane = plane.data();
+                vgx_mat* t = nullptr;
+                if ((st = vgx_mat_upload(ctx, &d, &t))) return st;
+                head_tiles.push_back(t);
+            }
+        }
+        if ((st = vgx_group_create(ctx, (int)head_tiles.size(), head_tiles.data(), &head))) return st;
+        // attention state: Session's rope tables (engine/src/session.cpp:188-202)
+        const int half = hd / 2;
+        std::vector<float> rc((size_t)seq * half), rs((size_t)seq * half);
+        for (int p = 0; p < seq; ++p)
+            for (int i = 0; i < half; ++i) {
+                float freq = 1.0f / powf(m.theta, (2.0f * i) / hd);
+                float a = p * freq;
+                rc[(size_t)p * half + i] = cosf(a);
+                rs[(size_t)p * half + i] = sinf(a);
+            }
+        vgx_attn_desc ad{};
+        ad.dim = D; ad.heads = m.heads; ad.kv_heads = m.kv_heads; ad.head_dim = hd; ad.seq = seq;
+        ad.layers = m.layers; ad.kv_bits = kv_bits; ad.rope_half = m.rope_half; ad.qk_norm = m.qk_norm;
+        ad.rope_cos = rc.data(); ad.rope_sin = rs.data();
+        if (m.qk_norm) {
+            const vgxe::Record* qn = c.find(vgxe::T_Q_NORM);
+            const vgxe::Record* kn = c.find(vgxe::T_K_NORM);
+            if (!qn || !kn || qn->bytes != (uint64_t)m.layers * hd * 4 || kn->bytes != qn->bytes)
+                return fail(VGX_EINVAL, "q/k norm weights missing or misshapen");
+            ad.q_norm = reinterpret_cast<const float*>(qn->body);
+            ad.k_norm = reinterpret_cast<const float*>(kn->body);
+        }
+        if ((st = vgx_attn_create(ctx, &ad, &attn))) return st;
+        const int qkv_rows = D + 2 * m.kv_dim();
+        if ((st = dalloc(&h, D)) || (st = dalloc(&x1, D)) || (st = dalloc(&xb, D)) || (st = dalloc(&att, D)) ||
+            (st = dalloc(&xf, D)) || (st = dalloc(&qkv, qkv_rows)) || (st = dalloc(&hbuf, m.hidden)) ||
+            (st = dalloc(&logits, (size_t)m.vocab)) || (st = dalloc(&toks, (size_t)seq + 1)))
+            return st;
+        hipError_t he = hipDeviceSynchronize();
+        return he == hipSuccess ? VGX_OK : fail(VGX_EHIP, hipGetErrorString(he));
+    }
+
+    // Session::forward_gpu_hidden for one position; the token is read from
+    // device memory.  With want_logits the final RMSNorm, the LM head and the
+    // argmax (into *next_dev) follow.
+    int forward(const int* token_dev, int pos, bool want_logits, int* next_dev) {
+        int st;
+        const int D = m.dim;
+        const float eps = m.rms_eps;
+        if ((st = vgx_embed_q8(ctx, emb, emb_scale, m.vocab, D, token_dev, h))) return st;
+        for (int l = 0; l < m.layers; ++l) {
+            Layer& ly = L[l];
+            if ((st = vgx_rmsnorm(ctx, D, h, ly.rms_att, eps, xb))) return st;
+            if ((st = vgx_gemv(ctx, ly.qkv, xb, nullptr, qkv))) return st;
+            if ((st = vgx_attn_block(attn, l, pos, qkv, att))) return st;
+            if ((st = vgx_gemv(ctx, ly.wo, att, h, x1))) return st;
+            if ((st = vgx_rmsnorm(ctx, D, x1, ly.rms_ffn, eps, xb))) return st;
+            if ((st = vgx_ffn_gate(ctx, ly.w1, ly.w3, xb, ly.hs, hbuf))) return st;
+            if (ffn_chunk) st = vgx_gemv_add_split(ctx, ly.w2, ffn_chunk, hbuf, x1, h);
+            else st = vgx_gemv(ctx, ly.w2, hbuf, x1, h);
+            if (st) return st;
+        }
+        if (!want_logits) return VGX_OK;
+        if ((st = vgx_rmsnorm(ctx, D, h, rms_final, eps, xf))) return st;
+        return vgx_logits_argmax(ctx, head, xf, logits, next_dev);
+    }
+};
+
+extern "C" {
+
+static int engine_finish_open(vgx_engine* e, int device, int seq, int kv_bits, vgx_engine** out) {
+    g_err.clear();
+    int st = e->init(device, seq, kv_bits);
+    if (st) {
+        std::string msg = g_err.empty() ? vgx_last_error() : g_err;
+        delete e;
+        g_err = msg;
+        return st;
+    }
+    *out = e;
+    return VGX_OK;
+}
+
+int vgx_engine_open(const char* path, int device, int seq, int kv_bits, vgx_engine** out) {
+    if (!path || !out) return fail(VGX_EINVAL, "vgx_engine_open: NULL argument");
+    *out = nullptr;
+    vgx_engine* e = new vgx_engine();
+    std::string err;
+    if (!e->c.open(path, err)) { delete e; return fail(VGX_EINVAL, err); }
+    return engine_finish_open(e, device, seq, kv_bits, out);
+}
+
+int vgx_engine_open_bytes(const void* data, size_t size, int device, int seq, int kv_bits, vgx_engine** out) {
+    if (!data || !out) return fail(VGX_EINVAL, "vgx_engine_open_bytes: NULL argument");
+    *out = nullptr;
+    vgx_engine* e = new vgx_engine();
+    std::string err;
+    if (!e->c.open_bytes(static_cast<const uint8_t*>(data), size, err)) { delete e; return fail(VGX_EINVAL, err); }
+    return engine_finish_open(e, device, seq, kv_bits, out);
+}
+
+int vgx_engine_close(vgx_engine* e) {
+    delete e;
+    return VGX_OK;
+}
+
+int vgx_engine_info(const vgx_engine* e, int* dim, int* layers, int* vocab, int* seq) {
+    if (!e) return fail(VGX_EINVAL, "vgx_engine_info: NULL engine");
+    if (dim) *dim = e->m.dim;
+    if (layers) *layers = e->m.layers;
+    if (vocab) *vocab = e->m.vocab;
+    if (seq) *seq = e->seq;
+    return VGX_OK;
+}
+
+int vgx_engine_step(vgx_engine* e, int token, int pos, int16_t* logits_host, int* next) {
+    g_err.clear();
+    if (!e) return fail(VGX_EINVAL, "vgx_engine_step: NULL engine");
+    if (pos < 0 || pos >= e->seq) return fail(VGX_ERANGE, "vgx_engine_step: position outside the KV length");
+    if (token < 0 || token >= e->m.vocab) return fail(VGX_EINVAL, "vgx_engine_step: token outside the vocabulary");
+    hipStream_t s = static_cast<hipStream_t>(vgx_ctx_stream(e->ctx));
+    int* slot = e->toks + e->seq;
+    if (hipMemcpyAsync(slot, &token, sizeof(int), hipMemcpyHostToDevice, s) != hipSuccess)
+        return fail(VGX_EHIP, "token upload");
+    int st = e->forward(slot, pos, true, slot);
+    if (st) return st;
+    if (logits_host && hipMemcpyAsync(logits_host, e->logits, (size_t)e->m.vocab * 2, hipMemcpyDeviceToHost, s) != hipSuccess)
+        return fail(VGX_EHIP, "logits readback");
+    int nx = 0;
+    if (hipMemcpyAsync(&nx, slot, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess) return fail(VGX_EHIP, "token readback");
+    if (hipStreamSynchronize(s) != hipSuccess) return fail(VGX_EHIP, "step sync");
+    if (next) *next = nx;
+    return VGX_OK;
+}
+
+int vgx_engine_generate(vgx_engine* e, const int* prompt, int n_prompt, int n_gen, int* out,
+                        double* prefill_ms, double* decode_ms) {
+    g_err.clear();
+    if (!e || !prompt || !out) return fail(VGX_EINVAL, "vgx_engine_generate: NULL argument");
+    if (n_prompt <= 0 || n_gen <= 0 || n_prompt + n_gen - 1 > e->seq)
+        return fail(VGX_ERANGE, "vgx_engine_generate: prompt + generation longer than the KV length");
+    for (int i = 0; i < n_prompt; ++i)
+        if (prompt[i] < 0 || prompt[i] >= e->m.vocab) return fail(VGX_EINVAL, "prompt token outside the vocabulary");
+    hipStream_t s = static_cast<hipStream_t>(vgx_ctx_stream(e->ctx));
+    // history: toks[0..n_prompt) the prompt, then the generated tokens
+    int* gen = e->toks + n_prompt;
+    if (hipMemcpy(e->toks, prompt, (size_t)n_prompt * sizeof(int), hipMemcpyHostToDevice) != hipSuccess)
+        return fail(VGX_EHIP, "prompt upload");
+    if (hipDeviceSynchronize() != hipSuccess) return fail(VGX_EHIP, "sync");
+    auto t0 = std::chrono::steady_clock::now();
+    int st;
+    for (int p = 0; p < n_prompt; ++p)
+        if ((st = e->forward(e->toks + p, p, p == n_prompt - 1, gen))) return st;
+    if (hipStreamSynchronize(s) != hipSuccess) return fail(VGX_EHIP, "prefill sync");
+    auto t1 = std::chrono::steady_clock::now();
+    for (int i = 1; i < n_gen; ++i)
+        if ((st = e->forward(gen + i - 1, n_prompt + i - 1, true, gen + i))) return st;
+    if (hipStreamSynchronize(s) != hipSuccess) return fail(VGX_EHIP, "decode sync");
+    auto t2 = std::chrono::steady_clock::now();
+    if (hipMemcpy(out, gen, (size_t)n_gen * sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
+        return fail(VGX_EHIP, "token readback");
+    if (prefill_ms) *prefill_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+    if (decode_ms) *decode_ms = std::chrono::duration<double, std::milli>(t2 - t1).count();
+    return VGX_OK;
+}
+
+const char* vgx_engine_last_error(void) { return g_err.empty() ? vgx_last_error() : g_err.c_str(); }
+
+}  // extern "C"

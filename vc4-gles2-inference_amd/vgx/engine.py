@@ -1,0 +1,92 @@
+"""ctypes binding of the decode engine (include/vgx_engine.h)."""
+import ctypes
+import os
+
+import numpy as np
+
+from . import lib as _l
+
+LIB_PATH = os.path.join(_l.PKG, "lib", "libvgx_engine.so")
+CLI_PATH = os.path.join(_l.PKG, "bin", "engine_mm3")
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_SIGS = {
+    "vgx_engine_open": (_I, [ctypes.c_char_p, _I, _I, _I, ctypes.POINTER(_P)]),
+    "vgx_engine_open_bytes": (_I, [_P, ctypes.c_size_t, _I, _I, _I, ctypes.POINTER(_P)]),
+    "vgx_engine_close": (_I, [_P]),
+    "vgx_engine_info": (_I, [_P, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I)]),
+    "vgx_engine_step": (_I, [_P, _I, _I, _P, ctypes.POINTER(_I)]),
+    "vgx_engine_generate": (_I, [_P, _P, _I, _I, _P, ctypes.POINTER(ctypes.c_double),
+                                 ctypes.POINTER(ctypes.c_double)]),
+    "vgx_engine_last_error": (ctypes.c_char_p, []),
+}
+_lib = None
+
+
+def load():
+    global _lib
+    if _lib is None:
+        _l.load()  # libvgx first: the engine links it
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError("libvgx_engine is not built (%s)" % LIB_PATH)
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            getattr(L, name).restype = res
+            getattr(L, name).argtypes = args
+        _lib = L
+    return _lib
+
+
+def exported_symbols():
+    return sorted(_SIGS)
+
+
+def _check(st):
+    if st != 0:
+        raise _l.VgxError(st, load().vgx_engine_last_error().decode())
+
+
+class Engine:
+    """An MMCF model on one GPU: step (Session::step) and greedy generate."""
+
+    def __init__(self, blob=None, path=None, device=0, seq=0, kv_bits=16):
+        L = load()
+        h = ctypes.c_void_p()
+        if path is not None:
+            _check(L.vgx_engine_open(path.encode(), device, seq, kv_bits, ctypes.byref(h)))
+            self._blob = None
+        else:
+            self._blob = np.frombuffer(blob, np.uint8).copy()  # the engine borrows it until close
+            _check(L.vgx_engine_open_bytes(self._blob.ctypes.data, self._blob.size, device, seq, kv_bits,
+                                           ctypes.byref(h)))
+        self.h = h
+        d, l, v, s = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        _check(L.vgx_engine_info(h, ctypes.byref(d), ctypes.byref(l), ctypes.byref(v), ctypes.byref(s)))
+        self.dim, self.layers, self.vocab, self.seq = d.value, l.value, v.value, s.value
+
+    def step(self, token, pos, logits=True):
+        out = np.empty(self.vocab, np.int16) if logits else None
+        nx = ctypes.c_int()
+        _check(load().vgx_engine_step(self.h, int(token), int(pos),
+                                      ctypes.c_void_p(out.ctypes.data if logits else 0), ctypes.byref(nx)))
+        return out, nx.value
+
+    def generate(self, prompt, n_gen):
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.empty(n_gen, np.int32)
+        pf, dc = ctypes.c_double(), ctypes.c_double()
+        _check(load().vgx_engine_generate(self.h, p.ctypes.data, p.size, n_gen, out.ctypes.data,
+                                          ctypes.byref(pf), ctypes.byref(dc)))
+        return out, pf.value, dc.value
+
+    def close(self):
+        if self.h:
+            load().vgx_engine_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
