@@ -115,6 +115,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-runs", type=int, default=5)
+    ap.add_argument("--skip-decode", action="store_true")
+    ap.add_argument("--copy-mb", type=int, default=0, help="also time a device copy of this many MiB")
     ap.add_argument("--cpu-decode-steps", type=int, default=16)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -204,18 +206,33 @@ def main():
                      "kernel": "gemv_kernel<q8, EPI_STORE_F32> (one launch per shape per step)"},
         "gemv": shapes_out,
     }
-    g.close()
     for s in per_shape:
         s["grp"].free()
         for mm in s["mats"]:
             mm.free()
+    g.close()
     torch.cuda.synchronize()
-    blob, prompt, toks, dec = decode_bench(args.decode_runs)
-    out["decode"] = dec
-    out["decode_tokens_per_s"] = dec["tokens_per_s"]
+    if args.copy_mb:
+        # a plain device copy of known size: the scale for the FETCH_SIZE /
+        # WRITE_SIZE counters of a profiling run of this command
+        # (an elementwise kernel, not copy_, which a DMA engine may serve)
+        a = torch.empty(args.copy_mb << 18, dtype=torch.float32, device="cuda").fill_(1.0)
+        b = torch.empty_like(a)
+        for _ in range(args.steps):
+            torch.mul(a, 1.0, out=b)
+        torch.cuda.synchronize()
+        out["copy_calibration"] = {"kernel": "at::native elementwise mul, float32",
+                                   "bytes_read": a.numel() * 4, "bytes_written": b.numel() * 4,
+                                   "dispatches": args.steps}
+        del a, b
+    if not args.skip_decode:
+        blob, prompt, toks, dec = decode_bench(args.decode_runs)
+        out["decode"] = dec
+        out["decode_tokens_per_s"] = dec["tokens_per_s"]
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
-        out["decode"]["cpu_float_path"] = decode_cpu_baseline(blob, prompt, args.cpu_decode_steps)
+        if not args.skip_decode:
+            out["decode"]["cpu_float_path"] = decode_cpu_baseline(blob, prompt, args.cpu_decode_steps)
     print(json.dumps(out))
 
 
