@@ -118,7 +118,15 @@ def main():
     ap.add_argument("--skip-decode", action="store_true")
     ap.add_argument("--copy-mb", type=int, default=0, help="also time a device copy of this many MiB")
     ap.add_argument("--cpu-decode-steps", type=int, default=16)
+    ap.add_argument("--only", choices=["gemv", "decode"], default=None,
+                    help="run one leg (for profiling); the JSON line then carries that leg only")
     args = ap.parse_args()
+    if args.only == "decode":
+        blob, prompt, toks, dec = decode_bench(args.decode_runs)
+        print(json.dumps({"decode": dec}))
+        return
+    if args.only == "gemv":
+        args.skip_decode, args.no_cpu = True, True
     if args.gpus != 1:
         print("bench.py runs on one GPU: the decode path is single-device (see DESIGN.md); --gpus %d "
               "is not measured" % args.gpus, file=sys.stderr)

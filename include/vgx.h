@@ -145,6 +145,29 @@ int vgx_ffn_gate(vgx_ctx* ctx, const vgx_mat* W1, const vgx_mat* W3, const int16
  * rms_norm): w is the norm weight on the q16 grid (x_pack of the f32 vector). */
 int vgx_rmsnorm(vgx_ctx* ctx, int dim, const int16_t* x, const int16_t* w, float eps, int16_t* y);
 
+/* ---- RMSNorm fused into the GEMV that consumes it.  Each is GPU::rmsnorm
+ * (engine/src/gpu_upload.cpp:280-365) over x (cols values) with weight rms_w
+ * (q16, device, 16-byte aligned) and eps > 0, followed by the named GEMV on
+ * its q16 output, in one launch and with identical results; the normalised
+ * vector is not written out.  The pairs they replace:
+ *   vgx_gemv_rms          rmsnorm + vgx_gemv (the attention norm and the qkv
+ *                         draw, engine/src/session.cpp:1483 then 1502)
+ *   vgx_ffn_gate_rms      rmsnorm + vgx_ffn_gate (session.cpp:1516, 1538-1569)
+ *   vgx_gemv_group_rms    rmsnorm + vgx_gemv_group
+ *   vgx_logits_argmax_rms the final norm + vgx_logits_argmax
+ *                         (session.cpp:1580, sampling.cpp:160-162); the
+ *                         argmax runs in the same launch (the last workgroup
+ *                         to finish takes it), so launches over one group must
+ *                         not overlap. */
+int vgx_gemv_rms(vgx_ctx* ctx, const vgx_mat* W, const int16_t* x, const int16_t* rms_w, float eps,
+                 const int16_t* res, int16_t* y);
+int vgx_ffn_gate_rms(vgx_ctx* ctx, const vgx_mat* W1, const vgx_mat* W3, const int16_t* x,
+                     const int16_t* rms_w, float eps, int hs, int16_t* h);
+int vgx_gemv_group_rms(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, const int16_t* rms_w, float eps,
+                       int16_t* y);
+int vgx_logits_argmax_rms(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, const int16_t* rms_w, float eps,
+                          int16_t* logits, int* token);
+
 /* Session::embedding (engine/src/session.cpp:342-371), q8 rows: x = the
  * host-grid q16 of emb[token]*emb_scale[token].  emb: vocab x dim signed
  * bytes (device), emb_scale: vocab f32 (device), token: device int. */

@@ -734,14 +734,24 @@ void vgxo_attn_scores(const vgxo_attn_cfg* c, const int16_t* qrot, const uint8_t
 }
 
 /* att_stats (:334-369), linear sum grid: per head (max, sum exp(s - max)) as
- * two q16 values at scales 1024 and 32.  st[2h] = max, st[2h+1] = sum. */
+ * two q16 values at scales 1024 and 32.  st[2h] = max, st[2h+1] = sum.
+ *
+ * The build's summation order for both attention sums (this one and att_v's):
+ * positions in chunks of VGXO_ATTN_CHUNK, each chunk summed in double in
+ * position order from 0.0, then the chunk sums added in chunk order from 0.0.
+ * With at most one chunk this is the plain sequential sum. */
 void vgxo_attn_stats(const vgxo_attn_cfg* c, const int16_t* scores, int pos, int16_t* st) {
     for (int h = 0; h < c->heads; ++h) {
         const int16_t* sc = scores + (size_t)h * c->seq;
         float mx = -1e30f;
         for (int t = 0; t <= pos; ++t) { float s = (float)sc[t] / 1024.0f; if (s > mx) mx = s; }
         double sum = 0.0;
-        for (int t = 0; t <= pos; ++t) sum += (double)exp_d((float)sc[t] / 1024.0f - mx);
+        for (int t0 = 0; t0 <= pos; t0 += VGXO_ATTN_CHUNK) {
+            double cs = 0.0;
+            for (int t = t0; t <= pos && t < t0 + VGXO_ATTN_CHUNK; ++t)
+                cs += (double)exp_d((float)sc[t] / 1024.0f - mx);
+            sum += cs;
+        }
         float fs = (float)sum;
         float qm = floorf(mx * 1024.0f + 0.5f), qs = floorf(fs * 32.0f + 0.5f);
         st[2 * h] = (int16_t)(qm < -32768.0f ? -32768 : qm > 32767.0f ? 32767 : (int)qm);
@@ -750,7 +760,8 @@ void vgxo_attn_stats(const vgxo_attn_cfg* c, const int16_t* scores, int pos, int
 }
 
 /* att_v (:383-459): p_t = exp(s_t - max) / sum from the stored stats, out =
- * q16(sum_t p_t v_t); the build accumulates p*v in double. */
+ * q16(sum_t p_t v_t); the build accumulates p*v in double, in the chunked
+ * order of vgxo_attn_stats. */
 void vgxo_attn_v(const vgxo_attn_cfg* c, const int16_t* scores, const int16_t* st, const uint8_t* kv,
                  int pos, int16_t* out) {
     const int hd = c->head_dim, group = c->heads / c->kv_heads, kv_dim = c->kv_heads * hd;
@@ -762,10 +773,14 @@ void vgxo_attn_v(const vgxo_attn_cfg* c, const int16_t* scores, const int16_t* s
         const float invs = sum > 0.0f ? 1.0f / sum : 0.0f;
         for (int i = 0; i < hd; ++i) {
             double a = 0.0;
-            for (int t = 0; t <= pos; ++t) {
-                float p = exp_d((float)scores[(size_t)h * c->seq + t] / 1024.0f - mx) * invs;
-                float v = vgxo_kv_decode(c, kv + (size_t)t * rb, kv_dim + kvh * hd + i);
-                a += (double)p * (double)v;
+            for (int t0 = 0; t0 <= pos; t0 += VGXO_ATTN_CHUNK) {
+                double ca = 0.0;
+                for (int t = t0; t <= pos && t < t0 + VGXO_ATTN_CHUNK; ++t) {
+                    float p = exp_d((float)scores[(size_t)h * c->seq + t] / 1024.0f - mx) * invs;
+                    float v = vgxo_kv_decode(c, kv + (size_t)t * rb, kv_dim + kvh * hd + i);
+                    ca += (double)p * (double)v;
+                }
+                a += ca;
             }
             out[h * hd + i] = vgxo_q16_store((float)a);
         }

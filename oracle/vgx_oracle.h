@@ -80,6 +80,8 @@ void vgxo_rmsnorm(const int16_t* x, const int16_t* w, int dim, float eps, int16_
 void vgxo_rmsnorm_stats(const int16_t* x, int dim, int64_t* partials32, int64_t* total);
 
 /* ---- attention and KV pack/unpack (engine/src/shaders_attn.cpp) ----------- */
+/* positions per chunk of the attention sums' summation order */
+#define VGXO_ATTN_CHUNK 32
 typedef struct {
     int dim, heads, kv_heads, head_dim, seq;
     int kv_bits;   /* 16 or 8 */

@@ -209,6 +209,83 @@ def test_rmsnorm(gpu, dim):
             assert np.array_equal(host(gpu.rmsnorm(dev(x), dev(w), eps)), o.rmsnorm(x, w, eps))
 
 
+def _rms_case(rng, dim, scale):
+    x = np.clip(rng.standard_normal(dim) * scale, -32768, 32767).astype(np.int16)
+    w = o.quantize_act(rng.uniform(0.5, 1.5, dim).astype(np.float32))
+    return x, w
+
+
+@pytest.mark.parametrize("kind,rows,cols", [("q8", 768, 768), ("q8", 2432, 768), ("q4", 1536, 768),
+                                            ("t3", 1024, 1024), ("q8", 7, 32), ("t3", 33, 96)])
+def test_gemv_rms(gpu, kind, rows, cols):
+    # rmsnorm then the GEMV in one launch == the two oracle functions in turn
+    rng = np.random.default_rng(rows * 7 + cols)
+    mk = {"q8": q8_matrix, "q4": q4_matrix, "t3": t3_matrix}[kind]
+    m = mk(rng, rows, cols)
+    W = gpu.upload(m)
+    for scale, eps in ((256, 1e-5), (4000, 1e-6), (3, 1e-5)):
+        x, w = _rms_case(rng, cols, scale)
+        xn = o.rmsnorm(x, w, eps)
+        res = rand_x(rng, rows)
+        assert np.array_equal(host(gpu.matvec_rms(W, dev(x), dev(w), eps)), o.store(oracle_rowval(m, xn)))
+        got = host(gpu.matvec_rms(W, dev(x), dev(w), eps, res=dev(res)))
+        assert np.array_equal(got, o.store(oracle_rowval(m, xn), res)), (scale, eps)
+
+
+@pytest.mark.parametrize("kind,rows,cols", [("q8", 2432, 768), ("q4", 2432, 768), ("t3", 512, 1024)])
+def test_ffn_gate_rms(gpu, kind, rows, cols):
+    rng = np.random.default_rng(71)
+    mk = {"q8": q8_matrix, "q4": q4_matrix, "t3": t3_matrix}[kind]
+    m1, m3 = mk(rng, rows, cols), mk(rng, rows, cols)
+    W1, W3 = gpu.upload(m1), gpu.upload(m3)
+    x, w = _rms_case(rng, cols, 900)
+    xn = o.rmsnorm(x, w, 1e-5)
+    for hs in (0, 1):
+        h = host(gpu.ffn_gate_rms(W1, W3, dev(x), dev(w), 1e-5, hs))
+        assert np.array_equal(h, o.gate(oracle_rowval(m1, xn), oracle_rowval(m3, xn), hs)), hs
+
+
+@pytest.mark.parametrize("tile", [mmcf.LOGITS_GRID, 600])
+def test_logits_argmax_rms(gpu, tile):
+    # the final norm, the LM head and the argmax in one launch; tile 600 gives
+    # 11 matrices, more than the launch carries by value
+    rng = np.random.default_rng(81 + tile)
+    vocab, dim = 6400, 768
+    wh = rng.standard_normal((vocab, dim)).astype(np.float32) * 0.02
+    tiles = []
+    for st in range(0, vocab, tile):
+        q, unit, plane = mmcf.q8_per_row(wh[st:st + tile])
+        tiles.append(mmcf.Matrix("q8", q.shape[0], dim, (q.view(np.uint8) ^ 0x80).ravel(), unit, True, plane))
+    g = gpu.group([gpu.upload(t) for t in tiles])
+    logits = torch.empty(vocab, dtype=torch.int16, device="cuda")
+    token = torch.empty(1, dtype=torch.int32, device="cuda")
+    # several launches in a row: the finished-workgroup counter is back at 0
+    # after each
+    for k in range(4):
+        x, w = _rms_case(rng, dim, 300 * (k + 1))
+        xn = o.rmsnorm(x, w, 1e-5)
+        want = np.concatenate([o.store(oracle_rowval(t, xn)) for t in tiles])
+        assert np.array_equal(host(g.gemv_rms(dev(x), dev(w), 1e-5)), want)
+        g.logits_argmax_rms(dev(x), dev(w), 1e-5, logits, token)
+        assert np.array_equal(host(logits), want)
+        assert int(host(token)[0]) == o.argmax_i16(want), k
+    # all-zero logits: the first maximum (index 0)
+    g.logits_argmax_rms(dev(np.zeros(dim, np.int16)), dev(w), 1e-5, logits, token)
+    assert int(host(token)[0]) == 0
+
+
+def test_rms_entry_point_refusals(gpu):
+    rng = np.random.default_rng(91)
+    m = q8_matrix(rng, 64, 64)
+    W = gpu.upload(m)
+    x, w = _rms_case(rng, 64, 256)
+    from vgx.lib import VgxError
+    with pytest.raises(VgxError):
+        gpu.matvec_rms(W, dev(x), dev(w), 0.0)
+    with pytest.raises(VgxError):
+        gpu.matvec_rms(W, dev(x), dev(w)[1:], 1e-5)  # misaligned weight
+
+
 def test_embed_q8(gpu):
     rng = np.random.default_rng(61)
     emb = rng.integers(-127, 128, (6400, 768)).astype(np.int8)

@@ -257,12 +257,12 @@ def test_attention_integer_equations():
     """check_att.py's recomputation (engine/scripts/check_att.py:86-121), in the
     linear sum domain: scores from the exact dot, max/sum of the stored grid,
     out from p = exp(s - max)/sum over the decoded V."""
-    for kv_bits in (16, 8):
-        rng, cfg, rtab, qn, kn = _attn_setup(kv_bits)
+    # pos 29 sums one chunk of positions, pos 70 three (the chunked order)
+    for kv_bits, pos in ((16, 29), (8, 29), (16, 70), (8, 70)):
+        rng, cfg, rtab, qn, kn = _attn_setup(kv_bits, seq=80)
         kv_dim = cfg.kv_heads * cfg.head_dim
         rb = o.kv_row_bytes(cfg)
         kv = np.zeros(cfg.seq * rb, np.uint8)
-        pos = 29
         for t in range(pos + 1):
             qkv = np.clip(rng.standard_normal(cfg.dim + 2 * kv_dim) * 200, -32768, 32767).astype(np.int16)
             out = o.attn_block(cfg, qkv, qn, kn, rtab, t, kv)

@@ -253,16 +253,20 @@ int vgx_dequant(vgx_ctx* ctx, const vgx_mat* m, float* out) {
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 static int launch_single(vgx_ctx* ctx, const vgx_mat* W, const int16_t* x, const float* xf,
-                         const int16_t* res, void* y, const vgx_mat* W3, int hs, int split) {
+                         const int16_t* res, void* y, const vgx_mat* W3, int hs, int split,
+                         const int16_t* rw = nullptr, float eps = 0.0f) {
     if (!ctx || !W || !y) return vgx_fail(VGX_EINVAL, "gemv: NULL argument");
     if (!x && !xf) return vgx_fail(VGX_EINVAL, "gemv: x is NULL");
     if (!aligned16(x ? (const void*)x : (const void*)xf))
         return vgx_fail(VGX_EINVAL, "gemv: x must be 16-byte aligned");
+    if (rw && !aligned16(rw)) return vgx_fail(VGX_EINVAL, "gemv: the RMSNorm weight must be 16-byte aligned");
+    if (rw && !(eps > 0.0f)) return vgx_fail(VGX_EINVAL, "gemv: the RMSNorm epsilon must be positive");
     VGX_HIP(hipSetDevice(ctx->device));
     GemvLaunch L{};
     int lpr, ri, rpb;
     vgx_gemv_plan(W->d.kind, W->d.rows, W->d.cols, ctx->num_cu, &lpr, &ri, &rpb);
     const int units = W->d.kind == VGX_T3 ? (W->d.rows + 1) / 2 : W->d.rows;
+    L.md[0] = W->d;
     L.mats = W->d_dev;
     L.nmat = 1;
     L.blocks = (units + rpb - 1) / rpb;
@@ -270,13 +274,16 @@ static int launch_single(vgx_ctx* ctx, const vgx_mat* W, const int16_t* x, const
     L.xf = xf;
     L.res = res;
     L.y = y;
-    L.mats2 = W3 ? W3->d_dev : nullptr;
+    L.gate = W3 ? 1 : 0;
+    if (W3) L.md3 = W3->d;
     L.hs = hs;
     L.split_chunk = split;
     L.kind = W->d.kind;
     L.cols = W->d.cols;
     L.lpr = lpr;
     L.ri = ri;
+    L.rw = rw;
+    L.eps = eps;
     return vgx_gemv_launch(L, ctx->stream);
 }
 
@@ -305,6 +312,22 @@ int vgx_ffn_gate(vgx_ctx* ctx, const vgx_mat* W1, const vgx_mat* W3, const int16
         return vgx_fail(VGX_EINVAL, "vgx_ffn_gate: W1 and W3 differ in kind or shape");
     if (hs < 0 || hs > 5) return vgx_fail(VGX_EINVAL, "vgx_ffn_gate: hs outside 0..5");
     return launch_single(ctx, W1, x, nullptr, nullptr, h, W3, hs, 0);
+}
+
+int vgx_gemv_rms(vgx_ctx* ctx, const vgx_mat* W, const int16_t* x, const int16_t* rms_w, float eps,
+                 const int16_t* res, int16_t* y) {
+    if (!rms_w) return vgx_fail(VGX_EINVAL, "vgx_gemv_rms: NULL RMSNorm weight");
+    return launch_single(ctx, W, x, nullptr, res, y, nullptr, 0, 0, rms_w, eps);
+}
+
+int vgx_ffn_gate_rms(vgx_ctx* ctx, const vgx_mat* W1, const vgx_mat* W3, const int16_t* x,
+                     const int16_t* rms_w, float eps, int hs, int16_t* h) {
+    if (!W1 || !W3) return vgx_fail(VGX_EINVAL, "vgx_ffn_gate_rms: NULL matrix");
+    if (!rms_w) return vgx_fail(VGX_EINVAL, "vgx_ffn_gate_rms: NULL RMSNorm weight");
+    if (W1->d.kind != W3->d.kind || W1->d.rows != W3->d.rows || W1->d.cols != W3->d.cols)
+        return vgx_fail(VGX_EINVAL, "vgx_ffn_gate_rms: W1 and W3 differ in kind or shape");
+    if (hs < 0 || hs > 5) return vgx_fail(VGX_EINVAL, "vgx_ffn_gate_rms: hs outside 0..5");
+    return launch_single(ctx, W1, x, nullptr, nullptr, h, W3, hs, 0, rms_w, eps);
 }
 
 // ---------------------------------------------------------------------------
@@ -346,8 +369,11 @@ int vgx_group_create(vgx_ctx* ctx, int n, const vgx_mat* const* mats, vgx_group*
     }
     g->blocks = blk;
     g->rows = off;
+    g->host = ds;
     hipError_t e = hipMalloc(&g->d_dev, sizeof(MatDev) * (size_t)n);
     if (e == hipSuccess) e = hipMemcpy(g->d_dev, ds.data(), sizeof(MatDev) * (size_t)n, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMalloc(&g->counter, 256);
+    if (e == hipSuccess) e = hipMemset(g->counter, 0, 256);
     if (e != hipSuccess) { vgx_group_free(g); return vgx_hip_fail(e, "vgx_group_create"); }
     *out = g;
     return VGX_OK;
@@ -356,20 +382,26 @@ int vgx_group_create(vgx_ctx* ctx, int n, const vgx_mat* const* mats, vgx_group*
 int vgx_group_free(vgx_group* g) {
     if (!g) return VGX_OK;
     if (g->d_dev) (void)hipFree(g->d_dev);
+    if (g->counter) (void)hipFree(g->counter);
     delete g;
     return VGX_OK;
 }
 
 int vgx_group_rows(const vgx_group* g) { return g ? g->rows : 0; }
 
-static int launch_group(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, const float* xf, void* y) {
+static int launch_group(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, const float* xf, void* y,
+                        const int16_t* rw = nullptr, float eps = 0.0f, int* argmax_out = nullptr) {
     if (!ctx || !g || !y || (!x && !xf)) return vgx_fail(VGX_EINVAL, "gemv_group: NULL argument");
     if (!aligned16(x ? (const void*)x : (const void*)xf))
         return vgx_fail(VGX_EINVAL, "gemv_group: x must be 16-byte aligned");
+    if (rw && !aligned16(rw)) return vgx_fail(VGX_EINVAL, "gemv_group: the RMSNorm weight must be 16-byte aligned");
+    if (rw && !(eps > 0.0f)) return vgx_fail(VGX_EINVAL, "gemv_group: the RMSNorm epsilon must be positive");
     VGX_HIP(hipSetDevice(ctx->device));
     GemvLaunch L{};
     L.mats = g->d_dev;
     L.nmat = g->n;
+    if (g->n <= kInlineMats)
+        for (int i = 0; i < g->n; ++i) L.md[i] = g->host[i];
     L.blocks = g->blocks;
     L.x = x;
     L.xf = xf;
@@ -378,6 +410,12 @@ static int launch_group(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, cons
     L.cols = g->cols;
     L.lpr = g->lpr;
     L.ri = g->ri;
+    L.rw = rw;
+    L.eps = eps;
+    L.argmax_out = argmax_out;
+    L.counter = g->counter;
+    L.argmax_key = reinterpret_cast<unsigned long long*>(g->counter + 2);
+    L.total_rows = g->rows;
     return vgx_gemv_launch(L, ctx->stream);
 }
 
@@ -394,6 +432,19 @@ int vgx_logits_argmax(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, int16_
     int st = launch_group(ctx, g, x, nullptr, logits);
     if (st != VGX_OK) return st;
     return vgx_argmax_launch(logits, g->rows, token, ctx->stream);
+}
+
+int vgx_gemv_group_rms(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, const int16_t* rms_w, float eps,
+                       int16_t* y) {
+    if (!rms_w) return vgx_fail(VGX_EINVAL, "vgx_gemv_group_rms: NULL RMSNorm weight");
+    return launch_group(ctx, g, x, nullptr, y, rms_w, eps);
+}
+
+int vgx_logits_argmax_rms(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, const int16_t* rms_w, float eps,
+                          int16_t* logits, int* token) {
+    if (!token || !logits) return vgx_fail(VGX_EINVAL, "vgx_logits_argmax_rms: NULL output");
+    if (!rms_w) return vgx_fail(VGX_EINVAL, "vgx_logits_argmax_rms: NULL RMSNorm weight");
+    return launch_group(ctx, g, x, nullptr, logits, rms_w, eps, token);
 }
 
 // ---------------------------------------------------------------------------

@@ -1,12 +1,15 @@
 // Decode attention over the packed KV cache, with the KV pack (append).
 //
-// One workgroup per KV head: it packs this position's K (qk-norm, RoPE) and V
-// into the layer's KV row, prepares the GROUP query heads that read this KV
-// head (q-norm factor on its 1/65536 grid, RoPE, q16), scores every position
-// 0..pos (exact integer dot products, 1/1024 grid), forms the per-head
-// (max, sum) statistics on their q16 grids and the weighted V sum.  The
-// sequential reductions (sum of exp, sum over t of p*v) run in the same order
-// as the oracle in double, so the output is reproducible bit for bit.
+// One workgroup of 1024 threads per KV head: it packs this position's K
+// (qk-norm, RoPE) and V into the layer's KV row, prepares the GROUP query
+// heads that read this KV head (q-norm factor on its 1/65536 grid, RoPE, q16),
+// scores every position 0..pos (exact integer dot products, 1/1024 grid), forms
+// the per-head (max, sum) statistics on their q16 grids and the weighted V sum.
+// Scores and exponentials run one (head, position) per thread; the K row of a
+// position is read as 16-byte vectors.  The two double-precision sums (sum of
+// exp, sum over t of p*v) use a fixed order -- chunks of kChunk positions,
+// each summed in position order, then the chunk sums in chunk order -- and the
+// oracle sums in the same order, so the output is reproducible bit for bit.
 //
 // HBM layout of a layer's cache: seq rows of [K: kv_dim | V: kv_dim], int16
 // little-endian (kv_bits 16, grid 1/2048) or int8 (kv_bits 8, grid 1/16).
@@ -21,9 +24,20 @@
 
 #pragma clang fp contract(off)
 
+namespace {
+
+constexpr int kThreads = 1024;
+constexpr int kChunk = 32;  // positions per chunk of the summation order
+
+}  // namespace
+
 struct AttnDev {
     int dim, heads, kv_heads, hd, seq, kv_bits, rope_half, qk_norm, group;
     int row_bytes;
+    int vR;      // chunks per round of the weighted-V pass
+    int nchmax;  // chunks of a full cache
+    // LDS byte offsets
+    int o_ssk, o_mx, o_invs, o_newk, o_newv, o_qrot, o_sc, o_ep, o_csum, o_vpart, o_acc;
 };
 
 struct vgx_attn {
@@ -38,8 +52,6 @@ struct vgx_attn {
 };
 
 namespace {
-
-constexpr int kThreads = 256;
 
 __device__ __forceinline__ int q16_round(float v) {
     float f = floorf(v + 0.5f);
@@ -84,10 +96,49 @@ __device__ __forceinline__ void rope_pair(int rope_half, int hd, int i, int& j, 
     }
 }
 
-// Sum over a head (hd <= 256 values, one per thread i < hd) of v^2 as int64,
-// through LDS atomics.
-__device__ __forceinline__ void head_ss_add(unsigned long long* acc, long long v) {
-    atomicAdd(acc, (unsigned long long)v);
+__device__ __forceinline__ int lo16(unsigned w) { return (int)(short)(w & 0xffffu); }
+__device__ __forceinline__ int hi16(unsigned w) { return (int)w >> 16; }
+__device__ __forceinline__ int byte_s(unsigned w, int k) { return ((int)(w << (24 - 8 * k))) >> 24; }
+
+// Exact q . k over one head: q from LDS (int32 per element), k one cache row's
+// head slice read as 16-byte vectors (hd*KVB/8 bytes, 16-byte aligned).
+template <int KVB>
+__device__ __forceinline__ long long dot_row(const int* q, const uint8_t* k, int hd) {
+    const uint4* kv4 = reinterpret_cast<const uint4*>(k);
+    const int4* q4 = reinterpret_cast<const int4*>(q);
+    long long d = 0;
+    if (KVB == 16) {
+        const int nv = hd / 8;
+#pragma unroll 4
+        for (int v = 0; v < nv; ++v) {
+            const uint4 w = kv4[v];
+            const int4 a = q4[2 * v], b = q4[2 * v + 1];
+            d += (long long)a.x * lo16(w.x);
+            d += (long long)a.y * hi16(w.x);
+            d += (long long)a.z * lo16(w.y);
+            d += (long long)a.w * hi16(w.y);
+            d += (long long)b.x * lo16(w.z);
+            d += (long long)b.y * hi16(w.z);
+            d += (long long)b.z * lo16(w.w);
+            d += (long long)b.w * hi16(w.w);
+        }
+    } else {
+        const int nv = hd / 16;
+#pragma unroll 2
+        for (int v = 0; v < nv; ++v) {
+            const uint4 w = kv4[v];
+            const unsigned ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int4 a = q4[4 * v + u];
+                d += (long long)a.x * byte_s(ws[u], 0);
+                d += (long long)a.y * byte_s(ws[u], 1);
+                d += (long long)a.z * byte_s(ws[u], 2);
+                d += (long long)a.w * byte_s(ws[u], 3);
+            }
+        }
+    }
+    return d;
 }
 
 template <int KVB>
@@ -95,75 +146,75 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
                                                         const int16_t* qn, const int16_t* kn,
                                                         const int16_t* qkv, int16_t* out, int pos,
                                                         int do_write, int do_attend) {
-    extern __shared__ uint8_t smem[];
+    extern __shared__ __align__(16) uint8_t smem[];
     const int kvh = blockIdx.x;
-    const int hd = A.hd, G = A.group, kv_dim = A.kv_heads * hd;
-    const int half = hd / 2;
+    const int hd = A.hd, G = A.group, kv_dim = A.kv_heads * hd, GH = G * hd, seq = A.seq;
     const int tid = threadIdx.x;
     const int npos = pos + 1;
+    const int nch = (npos + kChunk - 1) / kChunk;
 
-    // LDS carve-up
-    unsigned long long* ssk = reinterpret_cast<unsigned long long*>(smem);  // 1 + G
-    int* newk = reinterpret_cast<int*>(smem + 8 * 32);                     // hd
-    int* newv = newk + 256;                                                // hd
-    int* qrot = newv + 256;                                                // G*hd
-    float* mxs = reinterpret_cast<float*>(qrot + 16 * 256);               // G
-    float* invs = mxs + 16;                                                // G
-    int16_t* sc = reinterpret_cast<int16_t*>(invs + 16);                   // G*seq
-    float* ep = reinterpret_cast<float*>(sc + (size_t)G * A.seq + (A.seq & 1 ? G : 0));  // G*seq
+    unsigned long long* ssk = reinterpret_cast<unsigned long long*>(smem + A.o_ssk);  // 1 + G
+    float* mxs = reinterpret_cast<float*>(smem + A.o_mx);                             // G
+    float* invs = reinterpret_cast<float*>(smem + A.o_invs);                          // G
+    int* newk = reinterpret_cast<int*>(smem + A.o_newk);                              // hd
+    int* newv = reinterpret_cast<int*>(smem + A.o_newv);                              // hd
+    int* qrot = reinterpret_cast<int*>(smem + A.o_qrot);                              // G*hd
+    int16_t* sc = reinterpret_cast<int16_t*>(smem + A.o_sc);                          // G*seq
+    float* ep = reinterpret_cast<float*>(smem + A.o_ep);                              // G*seq
+    double* csum = reinterpret_cast<double*>(smem + A.o_csum);                        // G*nchmax
+    double* vpart = reinterpret_cast<double*>(smem + A.o_vpart);                      // vR*G*hd
+    double* acc = reinterpret_cast<double*>(smem + A.o_acc);                          // G*hd
 
-    if (tid < 32) ssk[tid] = 0ull;
+    if (tid <= G) ssk[tid] = 0ull;
     __syncthreads();
 
-    const int16_t* kq = qkv + A.dim + kvh * hd;          // this head's K (q16)
-    const int16_t* vq = qkv + A.dim + kv_dim + kvh * hd; // and V
+    const int16_t* kq = qkv + A.dim + kvh * hd;           // this head's K (q16)
+    const int16_t* vq = qkv + A.dim + kv_dim + kvh * hd;  // and V
     uint8_t* row = kv + (size_t)pos * A.row_bytes;
-    const int32_t* rt = rtab + (size_t)pos * half * 2;
+    const int32_t* rt = rtab + (size_t)pos * (hd / 2) * 2;
 
     // sums of squares: K head (slot 0) and the G query heads (slots 1..G)
     if (A.qk_norm) {
-        if (do_write && tid < hd) head_ss_add(&ssk[0], (long long)kq[tid] * kq[tid]);
+        if (do_write && tid < hd) atomicAdd(&ssk[0], (unsigned long long)(long long)(kq[tid] * kq[tid]));
         if (do_attend) {
-            for (int idx = tid; idx < G * hd; idx += kThreads) {
+            for (int idx = tid; idx < GH; idx += kThreads) {
                 const int g = idx / hd, i = idx - g * hd;
-                const int16_t v = qkv[(kvh * G + g) * hd + i];
-                head_ss_add(&ssk[1 + g], (long long)v * v);
+                const int v = qkv[(kvh * G + g) * hd + i];
+                atomicAdd(&ssk[1 + g], (unsigned long long)(long long)(v * v));
             }
         }
     }
     __syncthreads();
 
     // --- KV pack of position pos (att_kv_rope)
-    if (do_write) {
+    if (do_write && tid < hd) {
         float rk = 1.0f;
         if (A.qk_norm) {
             const float ss = (float)(long long)ssk[0] * (1.0f / 65536.0f);
             rk = rsqrt_d(ss / (float)hd + 1e-6f);
         }
-        if (tid < hd) {
-            const int i = tid;
-            int j, ti;
-            bool first;
-            rope_pair(A.rope_half, hd, i, j, ti, first);
-            float vv = (float)kq[i] / 256.0f, bb = (float)kq[j] / 256.0f;
-            if (A.qk_norm) {
-                vv = (vv * rk) * ((float)kn[i] / 256.0f);
-                bb = (bb * rk) * ((float)kn[j] / 256.0f);
-            }
-            const float co = (float)rt[2 * ti] / 4096.0f, sn = (float)rt[2 * ti + 1] / 4096.0f;
-            const float o = first ? (vv * co) - (bb * sn) : (bb * sn) + (vv * co);
-            const int q = kv_enc<KVB>(o);
-            kv_put<KVB>(row, kvh * hd + i, q);
-            newk[i] = q;
-            const int qv = kv_enc<KVB>((float)vq[i] / 256.0f);
-            kv_put<KVB>(row, kv_dim + kvh * hd + i, qv);
-            newv[i] = qv;
+        const int i = tid;
+        int j, ti;
+        bool first;
+        rope_pair(A.rope_half, hd, i, j, ti, first);
+        float vv = (float)kq[i] / 256.0f, bb = (float)kq[j] / 256.0f;
+        if (A.qk_norm) {
+            vv = (vv * rk) * ((float)kn[i] / 256.0f);
+            bb = (bb * rk) * ((float)kn[j] / 256.0f);
         }
+        const float co = (float)rt[2 * ti] / 4096.0f, sn = (float)rt[2 * ti + 1] / 4096.0f;
+        const float o = first ? (vv * co) - (bb * sn) : (bb * sn) + (vv * co);
+        const int q = kv_enc<KVB>(o);
+        kv_put<KVB>(row, kvh * hd + i, q);
+        newk[i] = q;
+        const int qv = kv_enc<KVB>((float)vq[i] / 256.0f);
+        kv_put<KVB>(row, kv_dim + kvh * hd + i, qv);
+        newv[i] = qv;
     }
     if (!do_attend) return;
 
     // --- q prep (att_qnorm_scale + att_qrot)
-    for (int idx = tid; idx < G * hd; idx += kThreads) {
+    for (int idx = tid; idx < GH; idx += kThreads) {
         const int g = idx / hd, i = idx - g * hd;
         const int h = kvh * G + g;
         const int16_t* qh = qkv + h * hd;
@@ -184,84 +235,147 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
         }
         const float co = (float)rt[2 * ti] / 4096.0f, sn = (float)rt[2 * ti + 1] / 4096.0f;
         const float o = first ? (qv * co) - (b * sn) : (b * sn) + (qv * co);
-        qrot[g * hd + i] = q16_round(o * 256.0f);
+        qrot[idx] = q16_round(o * 256.0f);
     }
     __syncthreads();
 
-    // --- scores (att_score): exact dot, times 1/sqrt(hd), 1/1024 grid
+    // --- scores (att_score): exact dot, times 1/sqrt(hd), 1/1024 grid; one
+    // (position, head) per thread, the heads of a position in adjacent lanes
     const float invsqrt = 1.0f / sqrtf((float)hd);
     const float unit = KVB == 16 ? 1.0f / 524288.0f : 1.0f / 4096.0f;
+    const uint8_t* khead = kv + (size_t)kvh * hd * (KVB / 8);
     for (int idx = tid; idx < G * npos; idx += kThreads) {
-        const int g = idx / npos, t = idx - g * npos;
+        const int t = idx / G, g = idx - t * G;
         const int* qg = qrot + g * hd;
         long long d = 0;
         if (t == pos && do_write) {
             for (int i = 0; i < hd; ++i) d += (long long)qg[i] * newk[i];
         } else {
-            const uint8_t* r = kv + (size_t)t * A.row_bytes;
-            for (int i = 0; i < hd; ++i) d += (long long)qg[i] * kv_get<KVB>(r, kvh * hd + i);
+            d = dot_row<KVB>(qg, khead + (size_t)t * A.row_bytes, hd);
         }
         const float s = (float)d * unit;
         float f = floorf((s * invsqrt) * 1024.0f + 0.5f);
         f = fminf(fmaxf(f, -32768.0f), 32767.0f);
-        sc[(size_t)g * A.seq + t] = (int16_t)f;
+        sc[(size_t)g * seq + t] = (int16_t)f;
     }
     __syncthreads();
 
-    // --- stats (att_stats): max per head (exact), exp per position, sequential sum
+    // --- stats (att_stats): max per head (exact), one wave per head
     const int wave = tid >> 6, lane = tid & 63;
     for (int g = wave; g < G; g += kThreads / 64) {
         int m = -32768;
-        for (int t = lane; t < npos; t += 64) m = max(m, (int)sc[(size_t)g * A.seq + t]);
+        for (int t = lane; t < npos; t += 64) m = max(m, (int)sc[(size_t)g * seq + t]);
         for (int o = 32; o >= 1; o >>= 1) m = max(m, __shfl_xor(m, o, 64));
         if (lane == 0) mxs[g] = (float)m / 1024.0f;
     }
     __syncthreads();
     for (int idx = tid; idx < G * npos; idx += kThreads) {
         const int g = idx / npos, t = idx - g * npos;
-        ep[(size_t)g * A.seq + t] = exp_d((float)sc[(size_t)g * A.seq + t] / 1024.0f - mxs[g]);
+        ep[(size_t)g * seq + t] = exp_d((float)sc[(size_t)g * seq + t] / 1024.0f - mxs[g]);
+    }
+    __syncthreads();
+    // chunk sums of exp, in position order within a chunk
+    for (int idx = tid; idx < G * nch; idx += kThreads) {
+        const int g = idx / nch, c = idx - g * nch;
+        const int t0 = c * kChunk, t1 = min(t0 + kChunk, npos);
+        const float* e = ep + (size_t)g * seq;
+        double cs = 0.0;
+        for (int t = t0; t < t1; ++t) cs += (double)e[t];
+        csum[g * A.nchmax + c] = cs;
     }
     __syncthreads();
     if (tid < G) {
         const int g = tid;
         double sum = 0.0;
-        for (int t = 0; t < npos; ++t) sum += (double)ep[(size_t)g * A.seq + t];
+        for (int c = 0; c < nch; ++c) sum += csum[g * A.nchmax + c];
         const float fs = (float)sum;
         float qs = floorf(fs * 32.0f + 0.5f);
         qs = fminf(fmaxf(qs, -32768.0f), 32767.0f);
         const float sd = qs / 32.0f;
         invs[g] = sd > 0.0f ? 1.0f / sd : 0.0f;
-        // the stored max is the grid value itself: mxs[g] already is q/1024
-    }
-    __syncthreads();
-    for (int idx = tid; idx < G * npos; idx += kThreads) {
-        const int g = idx / npos, t = idx - g * npos;
-        ep[(size_t)g * A.seq + t] = ep[(size_t)g * A.seq + t] * invs[g];
     }
     __syncthreads();
 
-    // --- weighted V (att_v)
+    // --- weighted V (att_v): rounds of vR chunks; a thread sums one chunk of
+    // one (head, element), then the round's chunk sums join the running total
+    // in chunk order
     const float vunit = KVB == 16 ? 1.0f / 2048.0f : 1.0f / 16.0f;
-    for (int idx = tid; idx < G * hd; idx += kThreads) {
-        const int g = idx / hd, i = idx - g * hd;
-        const float* pg = ep + (size_t)g * A.seq;
-        double a = 0.0;
-        for (int t = 0; t < npos; ++t) {
-            const int q = (t == pos && do_write) ? newv[i]
-                                                 : kv_get<KVB>(kv + (size_t)t * A.row_bytes, kv_dim + kvh * hd + i);
-            const float v = (float)q * vunit;
-            a += (double)pg[t] * (double)v;
+    const uint8_t* vhead = kv + (size_t)(kv_dim + kvh * hd) * (KVB / 8);
+    const bool own_last = do_write != 0;  // position pos comes from LDS
+    for (int c0 = 0; c0 < nch; c0 += A.vR) {
+        const int nr = min(A.vR, nch - c0);
+        for (int idx = tid; idx < nr * GH; idx += kThreads) {
+            const int r = idx / GH, gi = idx - r * GH;
+            const int g = gi / hd, i = gi - g * hd;
+            const int t0 = (c0 + r) * kChunk, t1 = min(t0 + kChunk, npos);
+            const int tend = (own_last && t1 == npos) ? t1 - 1 : t1;
+            const float* pg = ep + (size_t)g * seq;
+            const float iv = invs[g];
+            const uint8_t* vp = vhead + (size_t)i * (KVB / 8);
+            double a = 0.0;
+            int t = t0;
+            for (; t + 8 <= tend; t += 8) {
+                int q[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) q[u] = kv_get<KVB>(vp + (size_t)(t + u) * A.row_bytes, 0);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const float p = pg[t + u] * iv;
+                    const float v = (float)q[u] * vunit;
+                    a += (double)p * (double)v;
+                }
+            }
+            for (; t < tend; ++t) {
+                const float p = pg[t] * iv;
+                const float v = (float)kv_get<KVB>(vp + (size_t)t * A.row_bytes, 0) * vunit;
+                a += (double)p * (double)v;
+            }
+            if (tend != t1) {
+                const float p = pg[pos] * iv;
+                const float v = (float)newv[i] * vunit;
+                a += (double)p * (double)v;
+            }
+            vpart[idx] = a;
         }
-        out[(kvh * G + g) * hd + i] = (int16_t)q16_round((float)a * 256.0f);
+        __syncthreads();
+        const bool last = c0 + nr >= nch;
+        for (int gi = tid; gi < GH; gi += kThreads) {
+            double s = c0 == 0 ? 0.0 : acc[gi];
+            for (int r = 0; r < nr; ++r) s += vpart[r * GH + gi];
+            if (last) {
+                const int g = gi / hd, i = gi - g * hd;
+                out[(kvh * G + g) * hd + i] = (int16_t)q16_round((float)s * 256.0f);
+            } else {
+                acc[gi] = s;
+            }
+        }
+        __syncthreads();
     }
 }
 
-size_t attn_lds(const AttnDev& A) {
-    // ssk(256 B) + newk/newv (2*256 ints) + qrot (16*256 ints) + mxs/invs (32 floats)
-    size_t b = 256 + 2 * 256 * 4 + 16 * 256 * 4 + 32 * 4;
-    b += (size_t)A.group * A.seq * 2 + (A.seq & 1 ? (size_t)A.group * 2 : 0);
-    b += (size_t)A.group * A.seq * 4;
-    return b;
+// LDS carve-up of one workgroup; returns the bytes used.
+size_t attn_layout(AttnDev& A) {
+    const int G = A.group, hd = A.hd, GH = G * hd;
+    A.nchmax = (A.seq + kChunk - 1) / kChunk;
+    A.vR = GH >= kThreads ? 1 : kThreads / GH;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off = (off + bytes + 15) & ~(size_t)15;
+        return (int)o;
+    };
+    A.o_ssk = take(8 * (size_t)(1 + G));
+    A.o_mx = take(4 * (size_t)G);
+    A.o_invs = take(4 * (size_t)G);
+    A.o_newk = take(4 * (size_t)hd);
+    A.o_newv = take(4 * (size_t)hd);
+    A.o_qrot = take(4 * (size_t)GH);
+    A.o_sc = take(2 * (size_t)G * A.seq);
+    A.o_ep = take(4 * (size_t)G * A.seq);
+    A.o_csum = take(8 * (size_t)G * A.nchmax);
+    A.o_vpart = take(8 * (size_t)A.vR * GH);
+    A.o_acc = take(8 * (size_t)GH);
+    return off;
 }
 
 int launch(vgx_attn* at, int layer, int pos, const int16_t* qkv, int16_t* out, int w, int att) {
@@ -311,7 +425,7 @@ int vgx_attn_create(vgx_ctx* ctx, const vgx_attn_desc* d, vgx_attn** out) {
     A.kv_bits = d->kv_bits; A.rope_half = d->rope_half ? 1 : 0; A.qk_norm = d->qk_norm ? 1 : 0;
     A.group = d->heads / d->kv_heads;
     A.row_bytes = 2 * d->kv_heads * d->head_dim * (d->kv_bits / 8);
-    at->lds = attn_lds(A);
+    at->lds = attn_layout(A);
     if (at->lds > 160 * 1024) {
         delete at;
         return vgx_fail(VGX_EINVAL, "vgx_attn_create: seq too long for one workgroup's LDS");

@@ -56,14 +56,28 @@ __device__ __forceinline__ T shfl_xor(T v, int o) {
 }
 
 // Which matrix / row block this block works on.
-__device__ __forceinline__ int find_mat(const MatDev* mats, int nmat, int blk) {
-    if (nmat == 1) return 0;
-    int lo = 0, hi = nmat - 1;
+__device__ __forceinline__ int find_mat(const GemvLaunch& L, int blk) {
+    if (L.nmat == 1) return 0;
+    int lo = 0, hi = L.nmat - 1;
     while (lo < hi) {
         int mid = (lo + hi + 1) >> 1;
-        if (mats[mid].blk_off <= blk) lo = mid; else hi = mid - 1;
+        const int off = L.nmat <= kInlineMats ? L.md[mid].blk_off : L.mats[mid].blk_off;
+        if (off <= blk) lo = mid; else hi = mid - 1;
     }
     return lo;
+}
+
+// Select a[r][c] for indices held in registers (unrolled compares, so the
+// array stays in registers).
+template <int R, int C, typename T>
+__device__ __forceinline__ T pick(const T (&a)[R][C], int r, int c) {
+    T v = a[0][0];
+#pragma unroll
+    for (int k = 0; k < R; ++k)
+#pragma unroll
+        for (int j = 0; j < C; ++j)
+            if (r == k && c == j) v = a[k][j];
+    return v;
 }
 
 // Pack 16 q16 values (8 dwords, two per dword, element 2k in the low half)
@@ -91,27 +105,51 @@ __device__ __forceinline__ void planes8eo(const uint32_t d[4], uint32_t& xle, ui
     xho = perm(D, B, 0x07060302u);
 }
 
-// Load 16 consecutive activations as q16 dwords (from int16 or from f32 with
-// the host quantisation).  Columns >= K read as zero.
-template <bool XF32>
-__device__ __forceinline__ void load_x16(const int16_t* x, const float* xf, int col, int K,
-                                         uint32_t d[8]) {
-    if (!XF32) {
+// GPU::rmsnorm's output element (engine/src/gpu_upload.cpp:280-365):
+// q16(x * inv * w) with the shader's floor(v + 0.5) store.
+__device__ __forceinline__ uint32_t rms_elem(uint32_t xv16, uint32_t wv16, float inv) {
+    const float xv = (float)(int16_t)xv16 / 256.0f;
+    const float wv = (float)(int16_t)wv16 / 256.0f;
+    const float v = (xv * inv) * wv;
+    return (uint32_t)(uint16_t)(int16_t)q16_round(v * 256.0f);
+}
+
+// Load 16 consecutive activations as q16 dwords: from int16, from f32 with
+// the host quantisation, or from int16 through RMSNorm (inv = the row's
+// inverse RMS, rw the q16 weight).  Columns >= K read as zero.
+template <int XM>
+__device__ __forceinline__ void load_x16(const GemvLaunch& L, int col, int K, float inv, uint32_t d[8]) {
+    const int16_t* x = L.x;
+    if (XM != X_F32) {
         if (col + 16 <= K) {
             const uint4* p = reinterpret_cast<const uint4*>(x + col);
             uint4 a = p[0], b = p[1];
             d[0] = a.x; d[1] = a.y; d[2] = a.z; d[3] = a.w;
             d[4] = b.x; d[5] = b.y; d[6] = b.z; d[7] = b.w;
+            if (XM == X_RMS) {
+                const uint4* q = reinterpret_cast<const uint4*>(L.rw + col);
+                const uint4 c = q[0], e = q[1];
+                const uint32_t wd[8] = {c.x, c.y, c.z, c.w, e.x, e.y, e.z, e.w};
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    d[k] = rms_elem(d[k] & 0xFFFFu, wd[k] & 0xFFFFu, inv) |
+                           (rms_elem(d[k] >> 16, wd[k] >> 16, inv) << 16);
+            }
         } else {
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
                 int c0 = col + 2 * k;
                 uint32_t lo = c0 < K ? (uint16_t)x[c0] : 0u;
                 uint32_t hi = c0 + 1 < K ? (uint16_t)x[c0 + 1] : 0u;
+                if (XM == X_RMS) {
+                    lo = c0 < K ? rms_elem(lo, (uint16_t)L.rw[c0], inv) : 0u;
+                    hi = c0 + 1 < K ? rms_elem(hi, (uint16_t)L.rw[c0 + 1], inv) : 0u;
+                }
                 d[k] = lo | (hi << 16);
             }
         }
     } else {
+        const float* xf = L.xf;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             int c0 = col + 2 * k;
@@ -207,6 +245,44 @@ __device__ __forceinline__ int q4_chunk(const uint4 w, const uint4 xhe, const ui
 }
 
 // ---------------------------------------------------------------------------
+// argmax_token (engine/src/sampling.cpp:160-162) fused into the LM-head
+// launch.  A stored logit q at output row r is the key
+//   (q + 32768) << 32 | (0xFFFFFFFF - r)
+// so the largest key is the largest logit and, among equal logits, the first
+// row.  Each workgroup reduces its keys and folds the result into the device
+// key with atomicMax, then counts itself done; the count's increment is
+// computed from atomicMax's returned value, so the max is performed before
+// the count.  The workgroup that brings the count to gridDim.x takes the key
+// with atomicExch (which leaves 0 for the next launch), decodes the row and
+// resets the count.  Only atomics cross workgroups: nothing waits, nothing
+// is fenced.
+__device__ __forceinline__ unsigned long long argmax_key(int q, int row) {
+    return ((unsigned long long)(unsigned)(q + 32768) << 32) | (unsigned long long)(0xFFFFFFFFu - (unsigned)row);
+}
+
+__device__ __forceinline__ void argmax_tail(const GemvLaunch& L, unsigned long long key) {
+    __shared__ unsigned long long s_k[kWaves];
+    for (int o = 32; o >= 1; o >>= 1) {
+        const unsigned long long other = shfl_xor(key, o);
+        key = other > key ? other : key;
+    }
+    if ((threadIdx.x & 63) == 0) s_k[threadIdx.x >> 6] = key;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < kWaves; ++k) key = s_k[k] > key ? s_k[k] : key;
+        const unsigned long long prev = atomicMax(L.argmax_key, key);
+        // never ~0 (the value field is at most 0xFFFF): the increment depends
+        // on the returned value
+        const unsigned inc = prev == ~0ull ? 0u : 1u;
+        if (atomicAdd(L.counter, inc) == gridDim.x - 1) {
+            const unsigned long long fin = atomicExch(L.argmax_key, 0ull);
+            *L.argmax_out = (int)(0xFFFFFFFFu - (unsigned)(fin & 0xFFFFFFFFull));
+            atomicExch(L.counter, 0u);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // The kernel.  One template per (format, lanes per row, rows per lane,
 // epilogue, input type).
 //
@@ -216,7 +292,7 @@ __device__ __forceinline__ int q4_chunk(const uint4 w, const uint4 xhe, const ui
 //   q4 : per 32-col group: xhe, xle, xho, xlo (16 B each)           -> 64 B/group
 //        plus X_g (int32) per group
 //   t3 : + 256 u32 level table
-template <int KIND, int LPR, int RI, int EPI, bool XF32>
+template <int KIND, int LPR, int RI, int EPI, int XM>
 __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
     extern __shared__ uint4 lds[];
     constexpr int RPI = 64 / LPR;
@@ -227,19 +303,44 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
     const int rs = lane / LPR;
     const int cl = lane % LPR;
 
-    const int mi = find_mat(L.mats, L.nmat, blockIdx.x);
-    const MatDev M = L.mats[mi];
+    // descriptors: by value in the launch arguments (no dependent load) for
+    // up to kInlineMats matrices, else from the device table
+    const bool inl = L.nmat <= kInlineMats;
+    const int mi = find_mat(L, blockIdx.x);
+    const MatDev M = inl ? L.md[mi] : L.mats[mi];
+    const MatDev M3 = L.md3;  // W3 of the gate epilogue (single-matrix launches)
     const int K = M.cols;
     const int units = KIND == VGX_T3 ? (M.rows + 1) / 2 : M.rows;
     const int unit0 = (blockIdx.x - M.blk_off) * (kWaves * RPI * RI) + wave * (RPI * RI);
+    constexpr int RPU = KIND == VGX_T3 ? 2 : 1;  // rows per unit
 
     // --- weight chunk geometry
     const int nch = KIND == VGX_Q8 ? (K >> 4) : (K >> 5);
     const size_t ustride = KIND == VGX_Q8 ? (size_t)K : KIND == VGX_Q4 ? (size_t)(K >> 1)
                                                                      : (size_t)(K >> 3) * 4;
     const uint8_t* body = M.body;
-    const uint8_t* body3 = (EPI == EPI_GATE) ? L.mats2[mi].body : nullptr;
+    const uint8_t* body3 = (EPI == EPI_GATE) ? M3.body : nullptr;
     const int niter = (nch + LPR - 1) / LPR;
+
+    // The epilogue's per-row operands (row scales, residual) of every row this
+    // lane may store, loaded now so their latency hides under the main loop --
+    // for one row per lane only: with RI rows the registers they hold across
+    // the loop would cost occupancy, which the streaming launches need more.
+    constexpr bool PF = RI == 1;
+    float pw[RI][RPU], pw3[RI][RPU];
+    int pres[RI][RPU];
+#pragma unroll
+    for (int it = 0; it < (PF ? RI : 0); ++it) {
+#pragma unroll
+        for (int hr = 0; hr < RPU; ++hr) {
+            const int row = (unit0 + it * RPI + rs) * RPU + hr;
+            const bool rok = row < M.rows;
+            pw[it][hr] = (KIND != VGX_Q4 && rok) ? M.wsr[row] : 0.0f;
+            pw3[it][hr] = (KIND != VGX_Q4 && EPI == EPI_GATE && rok) ? M3.wsr[row] : 0.0f;
+            const bool has_res = (EPI == EPI_STORE || EPI == EPI_STORE_ARGMAX || EPI == EPI_SPLIT) && L.res;
+            pres[it][hr] = (has_res && rok) ? (int)L.res[M.out_off + row] : 0;
+        }
+    }
 
     // Issue the first chunk's weight loads before staging x so the two
     // latencies overlap.
@@ -257,7 +358,7 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
                         : make_uint4(0, 0, 0, 0);
         if (KIND == VGX_Q4) {
             smv[it] = ok ? M.sm[(size_t)u * nch + c] : 0u;
-            if (EPI == EPI_GATE) smv3[it] = ok ? L.mats2[mi].sm[(size_t)u * nch + c] : 0u;
+            if (EPI == EPI_GATE) smv3[it] = ok ? M3.sm[(size_t)u * nch + c] : 0u;
         }
     }
 
@@ -274,13 +375,35 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
         for (int b = threadIdx.x; b < 256; b += kThreads) lut[b] = t3_lut_entry((uint32_t)b);
     }
     if (KIND == VGX_Q4) xg = reinterpret_cast<int*>(lds + plane_u4);
+    // RMSNorm statistics (rms_stats_split, engine/src/gpu_upload.cpp:280-365):
+    // 32 partial sums of x^2 over contiguous slices of ceil(K/32) values, each
+    // stored as floor(P/16 + 1/2); 8 lanes per slice.
+    __shared__ long long s_rms[32];
+    if (XM == X_RMS) {
+        const int per = (K + 31) / 32;
+        const int p = threadIdx.x >> 3, sub = threadIdx.x & 7;
+        long long P = 0;
+        for (int k = sub; k < per; k += 8) {
+            const int i = p * per + k;
+            if (i < K) P += (long long)L.x[i] * L.x[i];
+        }
+        for (int o = 4; o >= 1; o >>= 1) P += shfl_xor(P, o);
+        if (sub == 0) s_rms[p] = (P + 8) >> 4;
+    }
     __syncthreads();
+    float rinv = 0.0f;
+    if (XM == X_RMS) {
+        long long tot = 0;
+        for (int p = 0; p < 32; ++p) tot += s_rms[p];
+        const float ss = (float)tot / 4096.0f;
+        rinv = (float)(1.0 / sqrt((double)(ss / (float)K + L.eps)));
+    }
     int part[2] = {0, 0};
     if (KIND == VGX_Q8) {
         for (int c = threadIdx.x; c < nch; c += kThreads) {
             const int hh = (EPI == EPI_SPLIT && c >= L.split_chunk) ? 1 : 0;
             uint32_t d[8], xh[4], xl[4];
-            load_x16<XF32>(L.x, L.xf, c * 16, K, d);
+            load_x16<XM>(L, c * 16, K, rinv, d);
             planes16(d, xh, xl);
             lds[2 * c] = make_uint4(xh[0], xh[1], xh[2], xh[3]);
             lds[2 * c + 1] = make_uint4(xl[0], xl[1], xl[2], xl[3]);
@@ -290,9 +413,9 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
         for (int c = threadIdx.x; c < nch; c += kThreads) {
             const int hh = (EPI == EPI_SPLIT && c >= L.split_chunk) ? 1 : 0;
             uint32_t d[8], xh[4], xl[4], xh2[4], xl2[4];
-            load_x16<XF32>(L.x, L.xf, c * 32, K, d);
+            load_x16<XM>(L, c * 32, K, rinv, d);
             planes16(d, xh, xl);
-            load_x16<XF32>(L.x, L.xf, c * 32 + 16, K, d);
+            load_x16<XM>(L, c * 32 + 16, K, rinv, d);
             planes16(d, xh2, xl2);
             lds[4 * c + 0] = make_uint4(xh[0], xh[1], xh[2], xh[3]);
             lds[4 * c + 1] = make_uint4(xh2[0], xh2[1], xh2[2], xh2[3]);
@@ -306,8 +429,8 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
     } else {  // Q4
         for (int c = threadIdx.x; c < nch; c += kThreads) {
             uint32_t d[8], d2[8];
-            load_x16<XF32>(L.x, L.xf, c * 32, K, d);
-            load_x16<XF32>(L.x, L.xf, c * 32 + 16, K, d2);
+            load_x16<XM>(L, c * 32, K, rinv, d);
+            load_x16<XM>(L, c * 32 + 16, K, rinv, d2);
             uint32_t he[4], le[4], ho[4], lo[4];
             const uint32_t q0[4] = {d[0], d[1], d[2], d[3]}, q1[4] = {d[4], d[5], d[6], d[7]};
             const uint32_t q2[4] = {d2[0], d2[1], d2[2], d2[3]}, q3[4] = {d2[4], d2[5], d2[6], d2[7]};
@@ -348,7 +471,7 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
 #pragma unroll
             for (int k = 0; k < NV; ++k) acc[it][k] = 0.0;
         const float ps = M.ps;
-        const float ps3 = (EPI == EPI_GATE) ? L.mats2[mi].ps : 0.0f;
+        const float ps3 = (EPI == EPI_GATE) ? M3.ps : 0.0f;
         for (int j = 0; j < niter; ++j) {
             const int c = cl + j * LPR;
             const bool cok = c < nch;
@@ -367,7 +490,7 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
                     if (EPI == EPI_GATE) {
                         wn3[it] = ok ? *reinterpret_cast<const uint4*>(body3 + (size_t)u * ustride + (size_t)cn * 16)
                                      : make_uint4(0, 0, 0, 0);
-                        sn3[it] = ok ? L.mats2[mi].sm[(size_t)u * nch + cn] : 0u;
+                        sn3[it] = ok ? M3.sm[(size_t)u * nch + cn] : 0u;
                     }
                 }
             }
@@ -409,18 +532,23 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
             }
         }
         const int row_it = seg_reduce<LPR, RI, NV, double>(acc, cl);
+        unsigned long long akey = 0ull;
         if ((cl % (LPR / RI > 0 ? LPR / RI : 1)) == 0) {
             const int u = unit0 + row_it * RPI + rs;
             if (u < units) {
                 const float v = (float)acc[0][0];
-                if (EPI == EPI_STORE) {
-                    const float t = L.res ? v + (float)L.res[M.out_off + u] : v;
-                    static_cast<int16_t*>(L.y)[M.out_off + u] = (int16_t)q16_round(t);
+                const float rv = PF ? (float)pick(pres, row_it, 0)
+                                    : (L.res ? (float)L.res[M.out_off + u] : 0.0f);
+                if (EPI == EPI_STORE || EPI == EPI_STORE_ARGMAX) {
+                    const float t = L.res ? v + rv : v;
+                    const int q = q16_round(t);
+                    static_cast<int16_t*>(L.y)[M.out_off + u] = (int16_t)q;
+                    if (EPI == EPI_STORE_ARGMAX) akey = argmax_key(q, M.out_off + u);
                 } else if (EPI == EPI_STORE_F32) {
                     static_cast<float*>(L.y)[M.out_off + u] = v * (1.0f / 256.0f);
                 } else if (EPI == EPI_SPLIT) {
                     const float vb = (float)acc[0][NV - 1];
-                    const float t = v + (float)L.res[u];
+                    const float t = v + rv;
                     const float y1 = (float)q16_round(t);
                     static_cast<int16_t*>(L.y)[u] = (int16_t)q16_round(vb + y1);
                 } else {  // gate
@@ -436,6 +564,7 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
                 }
             }
         }
+        if (EPI == EPI_STORE_ARGMAX) argmax_tail(L, akey);
         return;
     }
 
@@ -534,35 +663,41 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
     }
 
     const int row_it = seg_reduce<LPR, RI, NI, int>(acc, cl);
-    if ((cl % (LPR / RI > 0 ? LPR / RI : 1)) != 0) return;
     const int u = unit0 + row_it * RPI + rs;
-    if (u >= units) return;
+    unsigned long long akey = 0ull;
+    if ((cl % (LPR / RI > 0 ? LPR / RI : 1)) == 0 && u < units) {
     // bias of the byte split: q8 -128*sum(xl), t3 -sum(x)
-    // q8: -128*sum(xl) over the columns summed; t3: -sum(x)
     const long long cmul = KIND == VGX_Q8 ? 128LL : 1LL;
 #pragma unroll
     for (int hr = 0; hr < ROWS_PER_UNIT; ++hr) {
         const int row = u * ROWS_PER_UNIT + hr;
         if (row >= M.rows) break;
-        // value of (matrix-or-half h) for this row
-        auto val = [&](int h, const MatDev& MM) -> float {
+        // value of (matrix-or-half h) for this row, times the row scale
+        auto val = [&](int h, float scale) -> float {
             const int o = KIND == VGX_T3 ? 4 * h + 2 * hr : 2 * h;
             const long long corr = cmul * (EPI == EPI_SPLIT ? (h ? xs1 : xs0) : (long long)xs0 + xs1);
             const long long s = 256LL * acc[0][o] + (long long)(uint32_t)acc[0][o + 1] - corr;
-            return (float)s * MM.wsr[row];
+            return (float)s * scale;
         };
-        if (EPI == EPI_STORE) {
-            const float v = val(0, M);
-            const float t = L.res ? v + (float)L.res[M.out_off + row] : v;
-            static_cast<int16_t*>(L.y)[M.out_off + row] = (int16_t)q16_round(t);
+        const float sw = PF ? pick(pw, row_it, hr) : M.wsr[row];
+        const float rv = PF ? (float)pick(pres, row_it, hr) : (L.res ? (float)L.res[M.out_off + row] : 0.0f);
+        if (EPI == EPI_STORE || EPI == EPI_STORE_ARGMAX) {
+            const float v = val(0, sw);
+            const float t = L.res ? v + rv : v;
+            const int q = q16_round(t);
+            static_cast<int16_t*>(L.y)[M.out_off + row] = (int16_t)q;
+            if (EPI == EPI_STORE_ARGMAX) {
+                const unsigned long long k = argmax_key(q, M.out_off + row);
+                akey = k > akey ? k : akey;
+            }
         } else if (EPI == EPI_STORE_F32) {
-            static_cast<float*>(L.y)[M.out_off + row] = val(0, M) * (1.0f / 256.0f);
+            static_cast<float*>(L.y)[M.out_off + row] = val(0, sw) * (1.0f / 256.0f);
         } else if (EPI == EPI_SPLIT) {
-            const float va = val(0, M), vb = val(1, M);
-            const float y1 = (float)q16_round(va + (float)L.res[row]);
+            const float va = val(0, sw), vb = val(1, sw);
+            const float y1 = (float)q16_round(va + rv);
             static_cast<int16_t*>(L.y)[row] = (int16_t)q16_round(vb + y1);
         } else {  // gate
-            const float v1 = val(0, M), v3 = val(1, L.mats2[mi]);
+            const float v1 = val(0, sw), v3 = val(1, PF ? pick(pw3, row_it, hr) : M3.wsr[row]);
             const float g = (float)q16_round(v1), uu = (float)q16_round(v3);
             const float a = g / 256.0f;
             const float e = (float)exp(-(double)a);
@@ -573,6 +708,8 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
             static_cast<int16_t*>(L.y)[row] = (int16_t)q16_round(o * 256.0f);
         }
     }
+    }
+    if (EPI == EPI_STORE_ARGMAX) argmax_tail(L, akey);
 }
 
 // argmax with the first-maximum rule over int16 values, one block.
@@ -628,22 +765,29 @@ __global__ void dequant_kernel(const MatDev M, float* out) {
 // Dispatch tables.
 using KernFn = void (*)(const GemvLaunch);
 
-template <int KIND, int EPI, bool XF32>
+template <int KIND, int EPI, int XM>
 KernFn pick_kernel(int lpr, int ri) {
 #define VGX_K(LP, R) \
-    if (lpr == LP && ri == R) return gemv_kernel<KIND, LP, R, EPI, XF32>;
+    if (lpr == LP && ri == R) return gemv_kernel<KIND, LP, R, EPI, XM>;
     VGX_K(8, 1) VGX_K(8, 4) VGX_K(16, 1) VGX_K(16, 4) VGX_K(32, 1) VGX_K(32, 4) VGX_K(64, 1) VGX_K(64, 4)
 #undef VGX_K
     return nullptr;
 }
 
+// The (epilogue, input) pairs the entry points use.
 template <int KIND>
-KernFn pick_epi(int epi, int lpr, int ri) {
+KernFn pick_epi(int epi, int xm, int lpr, int ri) {
     switch (epi) {
-        case EPI_STORE: return pick_kernel<KIND, EPI_STORE, false>(lpr, ri);
-        case EPI_STORE_F32: return pick_kernel<KIND, EPI_STORE_F32, true>(lpr, ri);
-        case EPI_GATE: return pick_kernel<KIND, EPI_GATE, false>(lpr, ri);
-        case EPI_SPLIT: return pick_kernel<KIND, EPI_SPLIT, false>(lpr, ri);
+        case EPI_STORE:
+            return xm == X_RMS ? pick_kernel<KIND, EPI_STORE, X_RMS>(lpr, ri)
+                               : pick_kernel<KIND, EPI_STORE, X_I16>(lpr, ri);
+        case EPI_STORE_F32: return pick_kernel<KIND, EPI_STORE_F32, X_F32>(lpr, ri);
+        case EPI_GATE:
+            return xm == X_RMS ? pick_kernel<KIND, EPI_GATE, X_RMS>(lpr, ri)
+                               : pick_kernel<KIND, EPI_GATE, X_I16>(lpr, ri);
+        case EPI_SPLIT: return xm == X_I16 ? pick_kernel<KIND, EPI_SPLIT, X_I16>(lpr, ri) : nullptr;
+        case EPI_STORE_ARGMAX:
+            return xm == X_RMS ? pick_kernel<KIND, EPI_STORE_ARGMAX, X_RMS>(lpr, ri) : nullptr;
     }
     return nullptr;
 }
@@ -675,11 +819,16 @@ int vgx_gemv_plan(int kind, int rows, int cols, int num_cu, int* lpr, int* ri, i
 
 int vgx_gemv_launch(const GemvLaunch& L, hipStream_t s) {
     KernFn fn = nullptr;
-    const int epi = L.xf ? EPI_STORE_F32 : (L.mats2 ? EPI_GATE : (L.split_chunk > 0 ? EPI_SPLIT : EPI_STORE));
+    const int epi = L.xf ? EPI_STORE_F32
+                         : L.gate ? EPI_GATE
+                         : L.split_chunk > 0 ? EPI_SPLIT
+                         : L.argmax_out ? EPI_STORE_ARGMAX : EPI_STORE;
+    const int xm = L.xf ? X_F32 : L.rw ? X_RMS : X_I16;
+    if (epi == EPI_STORE_ARGMAX && !L.counter) return vgx_fail(VGX_EINVAL, "gemv: argmax without a counter");
     switch (L.kind) {
-        case VGX_Q8: fn = pick_epi<VGX_Q8>(epi, L.lpr, L.ri); break;
-        case VGX_Q4: fn = pick_epi<VGX_Q4>(epi, L.lpr, L.ri); break;
-        case VGX_T3: fn = pick_epi<VGX_T3>(epi, L.lpr, L.ri); break;
+        case VGX_Q8: fn = pick_epi<VGX_Q8>(epi, xm, L.lpr, L.ri); break;
+        case VGX_Q4: fn = pick_epi<VGX_Q4>(epi, xm, L.lpr, L.ri); break;
+        case VGX_T3: fn = pick_epi<VGX_T3>(epi, xm, L.lpr, L.ri); break;
     }
     if (!fn) return vgx_fail(VGX_EINVAL, "gemv: no kernel for this shape");
     const size_t shm = lds_bytes(L.kind, L.cols);

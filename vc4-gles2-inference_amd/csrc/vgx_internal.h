@@ -6,6 +6,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <string>
+#include <vector>
 
 #include "vgx.h"
 
@@ -70,24 +71,47 @@ struct vgx_group {
     int n = 0, kind = 0, cols = 0, rows = 0, blocks = 0;
     int lpr = 64, ri = 1;
     MatDev* d_dev = nullptr;  // n descriptors with out_off / blk_off filled
+    std::vector<MatDev> host;  // the same descriptors, host copy
+    // fused argmax state, 0 at rest: [0] the finished-workgroup count (u32),
+    // [2..3] the running max key (u64)
+    unsigned* counter = nullptr;
 };
 
 // ---------------------------------------------------------------------------
 // Launch helpers implemented in vgx_gemv.hip.
-enum GemvEpi { EPI_STORE = 0, EPI_STORE_F32 = 1, EPI_GATE = 2, EPI_SPLIT = 3 };
+// EPI_STORE_ARGMAX: EPI_STORE, then the last workgroup to finish (a device
+// counter, reset by that workgroup) takes the first-maximum argmax of the
+// whole output.
+enum GemvEpi { EPI_STORE = 0, EPI_STORE_F32 = 1, EPI_GATE = 2, EPI_SPLIT = 3, EPI_STORE_ARGMAX = 4 };
+// How the activation row reaches the kernel: q16, f32 (host quantisation on
+// the device), or q16 through RMSNorm (every workgroup recomputes the
+// statistics of x and stages rmsnorm(x, rw, eps)).
+enum GemvX { X_I16 = 0, X_F32 = 1, X_RMS = 2 };
+
+// Launches over at most this many matrices carry their descriptors by value in
+// the kernel arguments, so no workgroup waits on a descriptor load.
+constexpr int kInlineMats = 8;
 
 struct GemvLaunch {
-    const MatDev* mats;   // device descriptors
+    MatDev md[kInlineMats];  // descriptors by value (nmat <= kInlineMats)
+    MatDev md3;           // W3 by value (EPI_GATE)
+    const MatDev* mats;   // device descriptors (nmat > kInlineMats)
     int nmat;
     int blocks;           // total blocks
     const int16_t* x;     // q16 input (or nullptr)
     const float* xf;      // f32 input (EPI_STORE_F32)
     const int16_t* res;   // residual (EPI_STORE / EPI_SPLIT)
     void* y;              // int16 or f32 output
-    const MatDev* mats2;  // W3 for EPI_GATE
+    int gate;             // EPI_GATE: the second matrix is md3
     int hs;               // hidden store exponent (EPI_GATE)
     int split_chunk;      // first chunk of the second column half (EPI_SPLIT)
     int kind, cols, lpr, ri;
+    const int16_t* rw;    // RMSNorm weight, q16 (X_RMS)
+    float eps;            // RMSNorm epsilon (X_RMS)
+    int* argmax_out;      // EPI_STORE_ARGMAX: the index
+    unsigned* counter;    // EPI_STORE_ARGMAX: finished-workgroup counter, 0 between launches
+    unsigned long long* argmax_key;  // EPI_STORE_ARGMAX: running max key, 0 between launches
+    int total_rows;       // EPI_STORE_ARGMAX: length of the output
 };
 
 int vgx_gemv_plan(int kind, int rows, int cols, int num_cu, int* lpr, int* ri, int* rows_per_block);

@@ -42,8 +42,8 @@ struct vgx_engine {
     vgx_group* head = nullptr;
     int8_t* emb = nullptr;
     float* emb_scale = nullptr;
-    int16_t *h = nullptr, *x1 = nullptr, *xb = nullptr, *qkv = nullptr, *att = nullptr, *hbuf = nullptr;
-    int16_t *xf = nullptr, *logits = nullptr, *rms_final = nullptr;
+    int16_t *h = nullptr, *x1 = nullptr, *qkv = nullptr, *att = nullptr, *hbuf = nullptr;
+    int16_t *logits = nullptr, *rms_final = nullptr;
     int* toks = nullptr;  // device token slots: [0, seq) prompt/decode history, [seq] the host step's
     int seq = 0, kv_bits = 16, ffn_chunk = 0;
     std::vector<void*> allocs;
@@ -226,8 +226,8 @@ struct vgx_engine {
         }
         if ((st = vgx_attn_create(ctx, &ad, &attn))) return st;
         const int qkv_rows = D + 2 * m.kv_dim();
-        if ((st = dalloc(&h, D)) || (st = dalloc(&x1, D)) || (st = dalloc(&xb, D)) || (st = dalloc(&att, D)) ||
-            (st = dalloc(&xf, D)) || (st = dalloc(&qkv, qkv_rows)) || (st = dalloc(&hbuf, m.hidden)) ||
+        if ((st = dalloc(&h, D)) || (st = dalloc(&x1, D)) || (st = dalloc(&att, D)) ||
+            (st = dalloc(&qkv, qkv_rows)) || (st = dalloc(&hbuf, m.hidden)) ||
             (st = dalloc(&logits, (size_t)m.vocab)) || (st = dalloc(&toks, (size_t)seq + 1)))
             return st;
         hipError_t he = hipDeviceSynchronize();
@@ -236,7 +236,10 @@ struct vgx_engine {
 
     // Session::forward_gpu_hidden for one position; the token is read from
     // device memory.  With want_logits the final RMSNorm, the LM head and the
-    // argmax (into *next_dev) follow.
+    // argmax (into *next_dev) follow.  Each RMSNorm runs inside the GEMV that
+    // consumes it (the attention norm in the qkv draw, the FFN norm in the
+    // gate, the final norm in the LM head with its argmax): five launches a
+    // layer.
     int forward(const int* token_dev, int pos, bool want_logits, int* next_dev) {
         int st;
         const int D = m.dim;
@@ -244,19 +247,16 @@ struct vgx_engine {
         if ((st = vgx_embed_q8(ctx, emb, emb_scale, m.vocab, D, token_dev, h))) return st;
         for (int l = 0; l < m.layers; ++l) {
             Layer& ly = L[l];
-            if ((st = vgx_rmsnorm(ctx, D, h, ly.rms_att, eps, xb))) return st;
-            if ((st = vgx_gemv(ctx, ly.qkv, xb, nullptr, qkv))) return st;
+            if ((st = vgx_gemv_rms(ctx, ly.qkv, h, ly.rms_att, eps, nullptr, qkv))) return st;
             if ((st = vgx_attn_block(attn, l, pos, qkv, att))) return st;
             if ((st = vgx_gemv(ctx, ly.wo, att, h, x1))) return st;
-            if ((st = vgx_rmsnorm(ctx, D, x1, ly.rms_ffn, eps, xb))) return st;
-            if ((st = vgx_ffn_gate(ctx, ly.w1, ly.w3, xb, ly.hs, hbuf))) return st;
+            if ((st = vgx_ffn_gate_rms(ctx, ly.w1, ly.w3, x1, ly.rms_ffn, eps, ly.hs, hbuf))) return st;
             if (ffn_chunk) st = vgx_gemv_add_split(ctx, ly.w2, ffn_chunk, hbuf, x1, h);
             else st = vgx_gemv(ctx, ly.w2, hbuf, x1, h);
             if (st) return st;
         }
         if (!want_logits) return VGX_OK;
-        if ((st = vgx_rmsnorm(ctx, D, h, rms_final, eps, xf))) return st;
-        return vgx_logits_argmax(ctx, head, xf, logits, next_dev);
+        return vgx_logits_argmax_rms(ctx, head, h, rms_final, eps, logits, next_dev);
     }
 };
 

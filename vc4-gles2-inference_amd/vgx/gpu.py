@@ -71,6 +71,20 @@ class Group:
         _l.check(_l.load().vgx_logits_argmax(self.gpu.ctx, self.h, _ptr(x), _ptr(logits), _ptr(token)))
         return logits, token
 
+    def gemv_rms(self, x, rms_w, eps, out=None):
+        """rmsnorm(x, rms_w, eps) then the group GEMV, one launch."""
+        out = out if out is not None else torch.empty(self.rows, dtype=torch.int16, device=x.device)
+        _l.check(_l.load().vgx_gemv_group_rms(self.gpu.ctx, self.h, _ptr(x), _ptr(rms_w), float(eps), _ptr(out)))
+        return out
+
+    def logits_argmax_rms(self, x, rms_w, eps, logits=None, token=None):
+        """The final norm, the logits pass and the argmax in one launch."""
+        logits = logits if logits is not None else torch.empty(self.rows, dtype=torch.int16, device=x.device)
+        token = token if token is not None else torch.empty(1, dtype=torch.int32, device=x.device)
+        _l.check(_l.load().vgx_logits_argmax_rms(self.gpu.ctx, self.h, _ptr(x), _ptr(rms_w), float(eps),
+                                                  _ptr(logits), _ptr(token)))
+        return logits, token
+
     def free(self):
         if self.h:
             _l.load().vgx_group_free(self.h)
@@ -208,6 +222,18 @@ class GPU:
     def rmsnorm(self, x, w, eps=1e-5, out=None):
         out = out if out is not None else torch.empty_like(x)
         _l.check(_l.load().vgx_rmsnorm(self.ctx, x.numel(), _ptr(x), _ptr(w), float(eps), _ptr(out)))
+        return out
+
+    def matvec_rms(self, mat, x, rms_w, eps=1e-5, res=None, out=None):
+        """rmsnorm(x, rms_w, eps) then matvec_add, one launch."""
+        out = out if out is not None else torch.empty(mat.rows, dtype=torch.int16, device=x.device)
+        _l.check(_l.load().vgx_gemv_rms(self.ctx, mat.h, _ptr(x), _ptr(rms_w), float(eps), _ptr(res), _ptr(out)))
+        return out
+
+    def ffn_gate_rms(self, w1, w3, x, rms_w, eps=1e-5, hs=0, out=None):
+        """rmsnorm(x, rms_w, eps) then the fused FFN gate, one launch."""
+        out = out if out is not None else torch.empty(w1.rows, dtype=torch.int16, device=x.device)
+        _l.check(_l.load().vgx_ffn_gate_rms(self.ctx, w1.h, w3.h, _ptr(x), _ptr(rms_w), float(eps), hs, _ptr(out)))
         return out
 
     def embed_q8(self, emb, emb_scale, token, out=None):
