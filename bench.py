@@ -28,9 +28,88 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "dequant-GEMV GB/s (% HBM peak) + decode tokens/s, MiniMind3-64M q8, 1 GPU"
 
 
-def algo_bytes(rows, cols):
-    """body + f32 row plane + f32 x + f32 y for one q8 per-row GEMV."""
+def algo_bytes(rows, cols, kind="q8"):
+    """Weight body + scale planes + f32 x + f32 y for one GEMV: q8 per-row
+    (body + f32 row plane), q4 g32 (nibbles + int16 scale and min per group)."""
+    if kind == "q4":
+        return rows * cols // 2 + rows * (cols // 32) * 4 + cols * 4 + rows * 4
     return rows * cols + rows * 4 + cols * 4 + rows * 4
+
+
+def weight_bytes(rows, cols, kind):
+    return rows * cols // 2 + rows * (cols // 32) * 4 if kind == "q4" else rows * cols + rows * 4
+
+
+def make_matrix(rng, rows, cols, kind):
+    """N(0, 0.02) fp32 weights packed by the container packer (vgx.mmcf)."""
+    import numpy as np
+    from vgx import mmcf
+    w = rng.standard_normal((rows, cols)).astype(np.float32) * np.float32(0.02)
+    if kind == "q4":
+        packed, s16, m16, ps, _ = mmcf.q4mat(w)
+        return mmcf.Matrix("q4", rows, cols, packed.ravel(), ps, s16=s16.ravel(), m16=m16.ravel())
+    q, unit, plane = mmcf.q8_per_row(w)
+    return mmcf.Matrix("q8", rows, cols, (q.view(np.uint8) ^ 0x80).ravel(), unit, True, plane)
+
+
+def pmc_summary(fetch_csv, write_csv, bench_log):
+    """HBM traffic of the cold sweep's launches from two rocprofv3 --pmc runs
+    of `bench.py --only gemv --steps 3 --warmup 1 --copy-mb 1024` (counter
+    FETCH_SIZE, then WRITE_SIZE; KiB per dispatch), each scaled by what the
+    same counter reads for the 1 GiB elementwise copy of that run.  The first
+    four steps (warm-up + 3 timed) are averaged per shape.  `bench_log` is the
+    JSON line of a full bench run (for the algorithmic bytes)."""
+    import csv
+
+    def load(p):
+        with open(p) as f:
+            rows = list(csv.DictReader(f))
+        rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+        return rows
+
+    def scale(rows, known):
+        v = [float(r["Counter_Value"]) for r in rows if "AUnaryFunctor" in r["Kernel_Name"]]
+        return known / (sum(v) / len(v) * 1024.0), v
+
+    fe, wr = load(fetch_csv), load(write_csv)
+    with open(bench_log) as f:
+        bench = [json.loads(line) for line in f if line.startswith("{")][-1]
+    kf, cf = scale(fe, 1 << 30)
+    kw, cw = scale(wr, 1 << 30)
+    names = ["%dx%d" % s for s in SHAPES]
+    algo = {"q8": {x["shape"]: x["bytes_per_launch"] for x in bench["gemv"]},
+            "q4": {x["shape"]: x["bytes_per_launch"] for x in bench["q4"]["gemv"]}}
+    per = {}
+    for kind, kid in (("q8", 1), ("q4", 2)):
+        def cold(rows):
+            return [r for r in rows if r["Kernel_Name"].startswith("void (anonymous namespace)::gemv_kernel<%d," % kid)
+                    and ", 4, 1, 1>" in r["Kernel_Name"]]
+        cfk, cwk = cold(fe), cold(wr)
+        per[kind] = {}
+        for i, s in enumerate(names):
+            fb = sum(float(cfk[k * 5 + i]["Counter_Value"]) for k in range(4)) / 4 * 1024.0 * kf
+            wb = sum(float(cwk[k * 5 + i]["Counter_Value"]) for k in range(4)) / 4 * 1024.0 * kw
+            per[kind][s] = {"fetch_bytes": round(fb), "write_bytes": round(wb), "algorithmic_bytes": algo[kind][s],
+                            "traffic_over_algorithmic": round((fb + wb) / algo[kind][s], 4)}
+    return {"source": "rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE: bench.py --only gemv --steps 3 --warmup 1 "
+                      "--warm-reps 5 --copy-mb 1024",
+            "calibration": {"kernel": "at::native elementwise mul, float32, 1 GiB read + 1 GiB written",
+                            "fetch_KiB": cf, "write_KiB": cw, "fetch_bytes_per_counted_byte": kf,
+                            "write_bytes_per_counted_byte": kw},
+            "per_launch": per,
+            "bytes_per_step": sum(v["fetch_bytes"] + v["write_bytes"] for v in per["q8"].values()),
+            "algorithmic_bytes_per_step": sum(algo["q8"].values())}
+
+
+def traffic_summary():
+    """HBM bytes per launch of the headline kernel from the committed rocprofv3
+    PMC summary (FETCH_SIZE + WRITE_SIZE runs of this script, scaled by the
+    same counters on a copy of known size), or None before one exists."""
+    p = os.path.join(ROOT, "profiles", "gemv_q8_cold_traffic.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f)
 
 
 def cpu_baseline(seconds):
@@ -120,7 +199,12 @@ def main():
     ap.add_argument("--cpu-decode-steps", type=int, default=16)
     ap.add_argument("--only", choices=["gemv", "decode"], default=None,
                     help="run one leg (for profiling); the JSON line then carries that leg only")
+    ap.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "BENCH_LOG"),
+                    help="print the HBM traffic summary of two rocprofv3 --pmc runs and exit (no GPU)")
     args = ap.parse_args()
+    if args.pmc_summary:
+        print(json.dumps(pmc_summary(*args.pmc_summary), indent=1))
+        return
     if args.only == "decode":
         blob, prompt, toks, dec = decode_bench(args.decode_runs)
         print(json.dumps({"decode": dec}))
@@ -136,88 +220,101 @@ def main():
     import torch
 
     from vgx import gpu as vg
-    from vgx import mmcf
 
     torch.cuda.set_device(0)
     g = vg.GPU(0)
-    rng = np.random.default_rng(0)
-    xs, per_shape = {}, []
-    for rows, cols in SHAPES:
-        w = rng.standard_normal((rows, cols)).astype(np.float32) * np.float32(0.02)
-        q, unit, plane = mmcf.q8_per_row(w)
-        m = mmcf.Matrix("q8", rows, cols, (q.view(np.uint8) ^ 0x80).ravel(), unit, True, plane)
-        base = g.upload(m)
-        copies = max(1, (args.cold_mb << 20) // (rows * cols))
-        mats = [base] + [g.clone(base) for _ in range(copies - 1)]
-        grp = g.group(mats)
-        if cols not in xs:
-            xs[cols] = torch.from_numpy(rng.standard_normal(cols).astype(np.float32)).cuda()
-        y = torch.empty(grp.rows, dtype=torch.float32, device="cuda")
-        per_shape.append(dict(rows=rows, cols=cols, copies=copies, mats=mats, grp=grp, y=y,
-                              y1=torch.empty(rows, dtype=torch.float32, device="cuda")))
-    torch.cuda.synchronize()
 
-    def step():
+    def cold_sweep(kind, timed):
+        """One launch per shape over >= --cold-mb MiB of distinct copies (a
+        group sharing x); `timed` steps of the five launches between two
+        events, then per-shape cold and warm launch times."""
+        rng = np.random.default_rng(0 if kind == "q8" else 1)
+        xs, per_shape = {}, []
+        for rows, cols in SHAPES:
+            base = g.upload(make_matrix(rng, rows, cols, kind))
+            copies = max(1, (args.cold_mb << 20) // weight_bytes(rows, cols, kind))
+            mats = [base] + [g.clone(base) for _ in range(copies - 1)]
+            grp = g.group(mats)
+            if cols not in xs:
+                xs[cols] = torch.from_numpy(rng.standard_normal(cols).astype(np.float32)).cuda()
+            y = torch.empty(grp.rows, dtype=torch.float32, device="cuda")
+            per_shape.append(dict(rows=rows, cols=cols, copies=copies, mats=mats, grp=grp, y=y,
+                                  y1=torch.empty(rows, dtype=torch.float32, device="cuda")))
+        torch.cuda.synchronize()
+
+        def step():
+            for s in per_shape:
+                s["grp"].gemv_f32(xs[s["cols"]], s["y"])
+
+        step_bytes = sum(s["copies"] * algo_bytes(s["rows"], s["cols"], kind) for s in per_shape)
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(timed):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ms_step = e0.elapsed_time(e1) / timed
+        shapes_out = []
         for s in per_shape:
-            s["grp"].gemv_f32(xs[s["cols"]], s["y"])
-
-    step_bytes = sum(s["copies"] * algo_bytes(s["rows"], s["cols"]) for s in per_shape)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record()
-    for _ in range(args.steps):
-        step()
-    e1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_step = e0.elapsed_time(e1) / args.steps
-    value = step_bytes / (ms_step * 1e-3) / 1e9
-
-    # per-shape launch durations (cold) and warm single-matrix launches
-    shapes_out = []
-    for s in per_shape:
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(args.steps):
-            s["grp"].gemv_f32(xs[s["cols"]], s["y"])
-        b.record()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(timed):
+                s["grp"].gemv_f32(xs[s["cols"]], s["y"])
+            b.record()
+            torch.cuda.synchronize()
+            cold_us = a.elapsed_time(b) * 1e3 / timed
+            a.record()
+            for _ in range(args.warm_reps):
+                g.matvec_f32(s["mats"][0], xs[s["cols"]], s["y1"])
+            b.record()
+            torch.cuda.synchronize()
+            warm_us = a.elapsed_time(b) * 1e3 / args.warm_reps
+            ab = algo_bytes(s["rows"], s["cols"], kind)
+            shapes_out.append({"shape": "%dx%d" % (s["rows"], s["cols"]), "copies": s["copies"],
+                               "bytes_per_launch": s["copies"] * ab,
+                               "cold_us_per_launch": round(cold_us, 2),
+                               "cold_GBps": round(s["copies"] * ab / (cold_us * 1e-6) / 1e9, 1),
+                               "warm_us_per_gemv": round(warm_us, 3),
+                               "warm_GBps": round(ab / (warm_us * 1e-6) / 1e9, 1)})
+        for s in per_shape:
+            s["grp"].free()
+            for mm in s["mats"]:
+                mm.free()
         torch.cuda.synchronize()
-        cold_us = a.elapsed_time(b) * 1e3 / args.steps
-        a.record()
-        for _ in range(args.warm_reps):
-            g.matvec_f32(s["mats"][0], xs[s["cols"]], s["y1"])
-        b.record()
-        torch.cuda.synchronize()
-        warm_us = a.elapsed_time(b) * 1e3 / args.warm_reps
-        ab = algo_bytes(s["rows"], s["cols"])
-        shapes_out.append({"shape": "%dx%d" % (s["rows"], s["cols"]), "copies": s["copies"],
-                           "cold_us_per_launch": round(cold_us, 2),
-                           "cold_GBps": round(s["copies"] * ab / (cold_us * 1e-6) / 1e9, 1),
-                           "warm_us_per_gemv": round(warm_us, 3),
-                           "warm_GBps": round(ab / (warm_us * 1e-6) / 1e9, 1)})
-    kern_us = sum(x["cold_us_per_launch"] for x in shapes_out)
-    achieved = step_bytes / (kern_us * 1e-6) / 1e9
+        kern_us = sum(x["cold_us_per_launch"] for x in shapes_out)
+        return {"value": step_bytes / (ms_step * 1e-3) / 1e9, "ms_step": ms_step, "wall": wall,
+                "step_bytes": step_bytes, "achieved": step_bytes / (kern_us * 1e-6) / 1e9, "shapes": shapes_out}
+
+    q8 = cold_sweep("q8", args.steps)
+    q4 = cold_sweep("q4", args.steps)
+    traffic = traffic_summary()
     out = {
-        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "int8 weights x q16 activations (exact int32 dot), fp32 scale",
+        "metric": METRIC, "value": round(q8["value"], 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(q8["ms_step"], 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8 weights x q16 activations (exact int32 dot), fp32 scale",
         "data": "synthetic: N(0,0.02) fp32 weights, seed 0, packed q8 per-row; x ~ N(0,1) fp32",
         "config": {"workload": "q8 dequant-GEMV sweep at MiniMind3 shapes, cold weights",
-                   "shapes": [x["shape"] for x in shapes_out], "batch": 1,
-                   "cold_bytes_per_step": step_bytes, "wall_s": round(wall, 3)},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                   "shapes": [x["shape"] for x in q8["shapes"]], "batch": 1,
+                   "cold_bytes_per_step": q8["step_bytes"], "wall_s": round(q8["wall"], 3)},
+        "roofline": {"bound": "hbm", "achieved": round(q8["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(q8["achieved"] / HBM_PEAK_GBS, 4),
+                     "traffic": traffic["bytes_per_step"] if traffic else None,
+                     "algorithmic_bytes": q8["step_bytes"],
+                     "per": "step: one launch per shape, 5 launches; achieved = algorithmic bytes / sum of the "
+                            "5 launches' HIP-event durations",
                      "kernel": "gemv_kernel<q8, EPI_STORE_F32> (one launch per shape per step)"},
-        "gemv": shapes_out,
+        "gemv": q8["shapes"],
+        "q4": {"value": round(q4["value"], 1), "unit": "GB/s", "achieved": round(q4["achieved"], 1),
+               "frac": round(q4["achieved"] / HBM_PEAK_GBS, 4), "ms_per_step": round(q4["ms_step"], 4),
+               "cold_bytes_per_step": q4["step_bytes"], "gemv": q4["shapes"]},
     }
-    for s in per_shape:
-        s["grp"].free()
-        for mm in s["mats"]:
-            mm.free()
+    if traffic:
+        out["roofline"]["traffic_source"] = traffic.get("source")
     g.close()
     torch.cuda.synchronize()
     if args.copy_mb:

@@ -252,6 +252,14 @@ int vgx_dequant(vgx_ctx* ctx, const vgx_mat* m, float* out) {
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Workgroups of a GEMV launch: one per row tile up to 4 per CU; past that each
+// workgroup loops over tiles (x is staged once per workgroup).  4 per CU was
+// the best of 2..16 on HBM-streamed q8 and q4 launches.
+static int gemv_grid(const vgx_ctx* ctx, int tiles) {
+    const int cap = 4 * ctx->num_cu;
+    return tiles < cap ? tiles : cap;
+}
+
 static int launch_single(vgx_ctx* ctx, const vgx_mat* W, const int16_t* x, const float* xf,
                          const int16_t* res, void* y, const vgx_mat* W3, int hs, int split,
                          const int16_t* rw = nullptr, float eps = 0.0f) {
@@ -270,6 +278,7 @@ static int launch_single(vgx_ctx* ctx, const vgx_mat* W, const int16_t* x, const
     L.mats = W->d_dev;
     L.nmat = 1;
     L.blocks = (units + rpb - 1) / rpb;
+    L.grid = gemv_grid(ctx, L.blocks);
     L.x = x;
     L.xf = xf;
     L.res = res;
@@ -370,6 +379,10 @@ int vgx_group_create(vgx_ctx* ctx, int n, const vgx_mat* const* mats, vgx_group*
     g->blocks = blk;
     g->rows = off;
     g->host = ds;
+    // equal row counts: the tile -> matrix lookup is a division
+    bool uniform = true;
+    for (int i = 1; i < n; ++i) uniform = uniform && ds[i].rows == ds[0].rows;
+    g->bpm = uniform ? blk / n : 0;
     hipError_t e = hipMalloc(&g->d_dev, sizeof(MatDev) * (size_t)n);
     if (e == hipSuccess) e = hipMemcpy(g->d_dev, ds.data(), sizeof(MatDev) * (size_t)n, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMalloc(&g->counter, 256);
@@ -403,6 +416,8 @@ static int launch_group(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, cons
     if (g->n <= kInlineMats)
         for (int i = 0; i < g->n; ++i) L.md[i] = g->host[i];
     L.blocks = g->blocks;
+    L.grid = gemv_grid(ctx, g->blocks);
+    L.bpm = g->bpm;
     L.x = x;
     L.xf = xf;
     L.y = y;

@@ -55,6 +55,15 @@ __device__ __forceinline__ T shfl_xor(T v, int o) {
     return __shfl_xor(v, o, 64);
 }
 
+// A 16-byte weight chunk, loaded with the nontemporal hint: every weight byte
+// is read once per GEMV, so it should not displace reused lines (measured:
+// +15% on HBM-streamed q8/q4 launches, no change on cache-resident decode).
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 wload(const uint8_t* p) {
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Which matrix / row block this block works on.
 __device__ __forceinline__ int find_mat(const GemvLaunch& L, int blk) {
     if (L.nmat == 1) return 0;
@@ -303,64 +312,69 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
     const int rs = lane / LPR;
     const int cl = lane % LPR;
 
-    // descriptors: by value in the launch arguments (no dependent load) for
-    // up to kInlineMats matrices, else from the device table
-    const bool inl = L.nmat <= kInlineMats;
-    const int mi = find_mat(L, blockIdx.x);
-    const MatDev M = inl ? L.md[mi] : L.mats[mi];
-    const MatDev M3 = L.md3;  // W3 of the gate epilogue (single-matrix launches)
-    const int K = M.cols;
-    const int units = KIND == VGX_T3 ? (M.rows + 1) / 2 : M.rows;
-    const int unit0 = (blockIdx.x - M.blk_off) * (kWaves * RPI * RI) + wave * (RPI * RI);
+    // Every matrix of a launch has K = L.cols columns and reads the same x.
+    const int K = L.cols;
     constexpr int RPU = KIND == VGX_T3 ? 2 : 1;  // rows per unit
+    const MatDev M3 = L.md3;  // W3 of the gate epilogue (single-matrix launches)
 
     // --- weight chunk geometry
     const int nch = KIND == VGX_Q8 ? (K >> 4) : (K >> 5);
     const size_t ustride = KIND == VGX_Q8 ? (size_t)K : KIND == VGX_Q4 ? (size_t)(K >> 1)
                                                                      : (size_t)(K >> 3) * 4;
-    const uint8_t* body = M.body;
     const uint8_t* body3 = (EPI == EPI_GATE) ? M3.body : nullptr;
     const int niter = (nch + LPR - 1) / LPR;
 
-    // The epilogue's per-row operands (row scales, residual) of every row this
-    // lane may store, loaded now so their latency hides under the main loop --
-    // for one row per lane only: with RI rows the registers they hold across
-    // the loop would cost occupancy, which the streaming launches need more.
+    // A workgroup takes row tiles blockIdx.x, blockIdx.x + gridDim.x, ...;
+    // x is staged once for all of them.  Per tile: the matrix descriptor (by
+    // value in the launch arguments for up to kInlineMats matrices, else from
+    // the device table), the tile's first weight chunk, and -- for one row per
+    // lane only -- the epilogue's per-row operands (row scales, residual), so
+    // their latency hides under the main loop.  With RI rows per lane those
+    // registers would cost occupancy, which the streaming launches need more.
     constexpr bool PF = RI == 1;
+    MatDev M;
+    int units = 0, unit0 = 0;
+    const uint8_t* body = nullptr;
     float pw[RI][RPU], pw3[RI][RPU];
     int pres[RI][RPU];
-#pragma unroll
-    for (int it = 0; it < (PF ? RI : 0); ++it) {
-#pragma unroll
-        for (int hr = 0; hr < RPU; ++hr) {
-            const int row = (unit0 + it * RPI + rs) * RPU + hr;
-            const bool rok = row < M.rows;
-            pw[it][hr] = (KIND != VGX_Q4 && rok) ? M.wsr[row] : 0.0f;
-            pw3[it][hr] = (KIND != VGX_Q4 && EPI == EPI_GATE && rok) ? M3.wsr[row] : 0.0f;
-            const bool has_res = (EPI == EPI_STORE || EPI == EPI_STORE_ARGMAX || EPI == EPI_SPLIT) && L.res;
-            pres[it][hr] = (has_res && rok) ? (int)L.res[M.out_off + row] : 0;
-        }
-    }
-
-    // Issue the first chunk's weight loads before staging x so the two
-    // latencies overlap.
     uint4 w[RI], w3[RI];
     uint32_t smv[RI], smv3[RI];
+    auto begin_tile = [&](int tile) {
+        const int mi = L.bpm > 0 ? tile / L.bpm : find_mat(L, tile);
+        M = L.nmat <= kInlineMats ? L.md[mi] : L.mats[mi];
+        units = KIND == VGX_T3 ? (M.rows + 1) / 2 : M.rows;
+        unit0 = (tile - M.blk_off) * (kWaves * RPI * RI) + wave * (RPI * RI);
+        body = M.body;
 #pragma unroll
-    for (int it = 0; it < RI; ++it) {
-        const int u = unit0 + it * RPI + rs;
-        const int c = cl;
-        const bool ok = u < units && c < nch;
-        w[it] = ok ? *reinterpret_cast<const uint4*>(body + (size_t)u * ustride + (size_t)c * 16)
-                   : make_uint4(0, 0, 0, 0);
-        if (EPI == EPI_GATE)
-            w3[it] = ok ? *reinterpret_cast<const uint4*>(body3 + (size_t)u * ustride + (size_t)c * 16)
-                        : make_uint4(0, 0, 0, 0);
-        if (KIND == VGX_Q4) {
-            smv[it] = ok ? M.sm[(size_t)u * nch + c] : 0u;
-            if (EPI == EPI_GATE) smv3[it] = ok ? M3.sm[(size_t)u * nch + c] : 0u;
+        for (int it = 0; it < (PF ? RI : 0); ++it) {
+#pragma unroll
+            for (int hr = 0; hr < RPU; ++hr) {
+                const int row = (unit0 + it * RPI + rs) * RPU + hr;
+                const bool rok = row < M.rows;
+                pw[it][hr] = (KIND != VGX_Q4 && rok) ? M.wsr[row] : 0.0f;
+                pw3[it][hr] = (KIND != VGX_Q4 && EPI == EPI_GATE && rok) ? M3.wsr[row] : 0.0f;
+                const bool has_res = (EPI == EPI_STORE || EPI == EPI_STORE_ARGMAX || EPI == EPI_SPLIT) && L.res;
+                pres[it][hr] = (has_res && rok) ? (int)L.res[M.out_off + row] : 0;
+            }
         }
-    }
+#pragma unroll
+        for (int it = 0; it < RI; ++it) {
+            const int u = unit0 + it * RPI + rs;
+            const int c = cl;
+            const bool ok = u < units && c < nch;
+            w[it] = ok ? wload(body + (size_t)u * ustride + (size_t)c * 16)
+                       : make_uint4(0, 0, 0, 0);
+            if (EPI == EPI_GATE)
+                w3[it] = ok ? wload(body3 + (size_t)u * ustride + (size_t)c * 16)
+                            : make_uint4(0, 0, 0, 0);
+            if (KIND == VGX_Q4) {
+                smv[it] = ok ? M.sm[(size_t)u * nch + c] : 0u;
+                if (EPI == EPI_GATE) smv3[it] = ok ? M3.sm[(size_t)u * nch + c] : 0u;
+            }
+        }
+    };
+    // the first tile's loads go out before staging x so the latencies overlap
+    begin_tile(blockIdx.x);
 
     // --- stage x planes (and the row-independent sums) in LDS
     // the byte split's bias sums, per column half (the split epilogue adds the
@@ -463,6 +477,8 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
     __syncthreads();
     const int xs0 = KIND == VGX_Q4 ? 0 : s_xsum[0], xs1 = KIND == VGX_Q4 ? 0 : s_xsum[1];
 
+    unsigned long long akey = 0ull;  // EPI_STORE_ARGMAX: this lane's best key
+    for (int tile = blockIdx.x;;) {
     // --- main loop
     if (KIND == VGX_Q4) {
         double acc[RI][NV];
@@ -484,11 +500,11 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
                     const int u = unit0 + it * RPI + rs;
                     const int cn = c + LPR;
                     const bool ok = u < units && cn < nch;
-                    wn[it] = ok ? *reinterpret_cast<const uint4*>(body + (size_t)u * ustride + (size_t)cn * 16)
+                    wn[it] = ok ? wload(body + (size_t)u * ustride + (size_t)cn * 16)
                                 : make_uint4(0, 0, 0, 0);
                     sn[it] = ok ? M.sm[(size_t)u * nch + cn] : 0u;
                     if (EPI == EPI_GATE) {
-                        wn3[it] = ok ? *reinterpret_cast<const uint4*>(body3 + (size_t)u * ustride + (size_t)cn * 16)
+                        wn3[it] = ok ? wload(body3 + (size_t)u * ustride + (size_t)cn * 16)
                                      : make_uint4(0, 0, 0, 0);
                         sn3[it] = ok ? M3.sm[(size_t)u * nch + cn] : 0u;
                     }
@@ -532,7 +548,6 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
             }
         }
         const int row_it = seg_reduce<LPR, RI, NV, double>(acc, cl);
-        unsigned long long akey = 0ull;
         if ((cl % (LPR / RI > 0 ? LPR / RI : 1)) == 0) {
             const int u = unit0 + row_it * RPI + rs;
             if (u < units) {
@@ -543,7 +558,10 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
                     const float t = L.res ? v + rv : v;
                     const int q = q16_round(t);
                     static_cast<int16_t*>(L.y)[M.out_off + u] = (int16_t)q;
-                    if (EPI == EPI_STORE_ARGMAX) akey = argmax_key(q, M.out_off + u);
+                    if (EPI == EPI_STORE_ARGMAX) {
+                        const unsigned long long k = argmax_key(q, M.out_off + u);
+                        akey = k > akey ? k : akey;
+                    }
                 } else if (EPI == EPI_STORE_F32) {
                     static_cast<float*>(L.y)[M.out_off + u] = v * (1.0f / 256.0f);
                 } else if (EPI == EPI_SPLIT) {
@@ -564,10 +582,7 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
                 }
             }
         }
-        if (EPI == EPI_STORE_ARGMAX) argmax_tail(L, akey);
-        return;
-    }
-
+    } else {
     // q8 and t3: exact int32 partial sums.  t3 carries two rows (a pair) per unit.
     constexpr int ROWS_PER_UNIT = KIND == VGX_T3 ? 2 : 1;
     constexpr int NI = 2 * NV * ROWS_PER_UNIT;  // ints per unit: (s1, s2) per row per half
@@ -588,10 +603,10 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
                 const int u = unit0 + it * RPI + rs;
                 const int cn = c + LPR;
                 const bool ok = u < units && cn < nch;
-                wn[it] = ok ? *reinterpret_cast<const uint4*>(body + (size_t)u * ustride + (size_t)cn * 16)
+                wn[it] = ok ? wload(body + (size_t)u * ustride + (size_t)cn * 16)
                             : make_uint4(0, 0, 0, 0);
                 if (EPI == EPI_GATE)
-                    wn3[it] = ok ? *reinterpret_cast<const uint4*>(body3 + (size_t)u * ustride + (size_t)cn * 16)
+                    wn3[it] = ok ? wload(body3 + (size_t)u * ustride + (size_t)cn * 16)
                                  : make_uint4(0, 0, 0, 0);
             }
         }
@@ -664,14 +679,13 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
 
     const int row_it = seg_reduce<LPR, RI, NI, int>(acc, cl);
     const int u = unit0 + row_it * RPI + rs;
-    unsigned long long akey = 0ull;
     if ((cl % (LPR / RI > 0 ? LPR / RI : 1)) == 0 && u < units) {
     // bias of the byte split: q8 -128*sum(xl), t3 -sum(x)
     const long long cmul = KIND == VGX_Q8 ? 128LL : 1LL;
 #pragma unroll
     for (int hr = 0; hr < ROWS_PER_UNIT; ++hr) {
         const int row = u * ROWS_PER_UNIT + hr;
-        if (row >= M.rows) break;
+        if (row < M.rows) {
         // value of (matrix-or-half h) for this row, times the row scale
         auto val = [&](int h, float scale) -> float {
             const int o = KIND == VGX_T3 ? 4 * h + 2 * hr : 2 * h;
@@ -707,7 +721,13 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
             o = o * ldexpf(1.0f, -L.hs);
             static_cast<int16_t*>(L.y)[row] = (int16_t)q16_round(o * 256.0f);
         }
+        }
     }
+    }
+    }
+    tile += gridDim.x;
+    if (tile >= L.blocks) break;
+    begin_tile(tile);
     }
     if (EPI == EPI_STORE_ARGMAX) argmax_tail(L, akey);
 }
@@ -800,17 +820,23 @@ size_t lds_bytes(int kind, int cols) {
 
 }  // namespace
 
-// Lanes per row: enough chunks per lane (about four) to keep several loads in
-// flight, at most one wave per row; rows per lane: 4 when the matrix has
-// enough rows to give every CU several waves anyway, else 1.
+// Rows per lane: 4 when the matrix has enough rows to give every CU several
+// waves anyway (the bandwidth-bound launches), else 1 (the latency-bound
+// decode shapes).  Lanes per row, latency-bound: enough that each lane has
+// about four chunks, at most one wave per row.  Bandwidth-bound, from a sweep
+// of HBM-streamed launches on MI355X: q8 keeps 16 lanes on a row up to 64
+// chunks (K <= 1024) and 8 beyond (more chunks per lane in flight; int32
+// accumulators are cheap); q4 (fp64 group sums, more registers per chunk) and
+// t3 (two rows per chunk) use 8 lanes up to 48 chunks and 16 beyond.
 int vgx_gemv_plan(int kind, int rows, int cols, int num_cu, int* lpr, int* ri, int* rows_per_block) {
     const int nch = kind == VGX_Q8 ? cols / 16 : cols / 32;
     int l = 8;
     while (l < 64 && l * 4 < nch) l <<= 1;
     const int units = kind == VGX_T3 ? (rows + 1) / 2 : rows;
+    const int waves1 = (units + 64 / l - 1) / (64 / l);
+    const int r = waves1 >= 16 * num_cu ? 4 : 1;
+    if (r == 4) l = kind == VGX_Q8 ? (nch <= 64 ? 16 : 8) : (nch <= 48 ? 8 : 16);
     const int rpi = 64 / l;
-    const int waves1 = (units + rpi - 1) / rpi;
-    int r = waves1 >= 16 * num_cu ? 4 : 1;
     *lpr = l;
     *ri = r;
     *rows_per_block = kWaves * rpi * r;  // in units (row pairs for t3)
@@ -833,7 +859,9 @@ int vgx_gemv_launch(const GemvLaunch& L, hipStream_t s) {
     if (!fn) return vgx_fail(VGX_EINVAL, "gemv: no kernel for this shape");
     const size_t shm = lds_bytes(L.kind, L.cols);
     if (shm > 160 * 1024) return vgx_fail(VGX_EINVAL, "gemv: activation row too long for LDS");
-    hipLaunchKernelGGL(fn, dim3(L.blocks), dim3(kThreads), shm, s, L);
+    if (L.blocks <= 0) return vgx_fail(VGX_EINVAL, "gemv: empty launch");
+    const int grid = L.grid > 0 && L.grid < L.blocks ? L.grid : L.blocks;
+    hipLaunchKernelGGL(fn, dim3(grid), dim3(kThreads), shm, s, L);
     VGX_LAUNCH_CHECK("gemv launch");
     return VGX_OK;
 }

@@ -69,6 +69,7 @@ struct vgx_mat {
 struct vgx_group {
     vgx_ctx* ctx = nullptr;
     int n = 0, kind = 0, cols = 0, rows = 0, blocks = 0;
+    int bpm = 0;  // tiles per matrix when all matrices have the same rows, else 0
     int lpr = 64, ri = 1;
     MatDev* d_dev = nullptr;  // n descriptors with out_off / blk_off filled
     std::vector<MatDev> host;  // the same descriptors, host copy
@@ -97,7 +98,9 @@ struct GemvLaunch {
     MatDev md3;           // W3 by value (EPI_GATE)
     const MatDev* mats;   // device descriptors (nmat > kInlineMats)
     int nmat;
-    int blocks;           // total blocks
+    int blocks;           // row tiles (kWaves * 64/lpr * ri units each)
+    int grid;             // workgroups; each takes tiles b, b + grid, ...
+    int bpm;              // tiles per matrix when every matrix has the same rows, else 0
     const int16_t* x;     // q16 input (or nullptr)
     const float* xf;      // f32 input (EPI_STORE_F32)
     const int16_t* res;   // residual (EPI_STORE / EPI_SPLIT)

@@ -7,7 +7,9 @@ import ctypes
 import os
 
 PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(PKG, "lib", "libvgx.so")
+# VGX_LIB names another build of the same library (e.g. one built with other
+# compiler flags); by default the in-tree build.
+LIB_PATH = os.environ.get("VGX_LIB") or os.path.join(PKG, "lib", "libvgx.so")
 
 VGX_OK, VGX_EINVAL, VGX_EHIP, VGX_ENOMEM, VGX_ESTATE, VGX_ERANGE = 0, -1, -2, -3, -4, -5
 Q8, Q4, T3 = 1, 2, 3
