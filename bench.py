@@ -168,6 +168,71 @@ def decode_bench(runs):
         "prefill_ms": round(float(np.median(pf)), 3), "runs": runs}
 
 
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 matrix-core peak, TOPS
+
+
+def prefill_bench(runs):
+    """The C3 workload: MiniMind3-64M-shaped q4, KV q8, SEQ 768.  A 256-token
+    prompt prefilled in one batch (int8 matrix cores) against the serial loop,
+    then 512 greedy tokens; and the prefill GEMMs alone (256 tokens x the
+    layer shapes), their algorithmic int8 ops (2*M*N*K) over kernel time
+    against the matrix-core peak."""
+    import numpy as np
+    import torch
+    from vgx import gpu as vg
+    from vgx import synth
+    from vgx.engine import Engine
+
+    spec = synth.minimind3_spec(seq=768)
+    blob = synth.container(spec, "q4", seed=0)
+    prompt = synth.prompt(256, spec.vocab, seed=0)
+    eng = Engine(blob, kv_bits=8)
+    eng.prefill(prompt, logits=False)
+    batched = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        eng.prefill(prompt, logits=False)
+        batched.append((time.perf_counter() - t0) * 1e3)
+    eng.set_prefill_batch(0)
+    t0 = time.perf_counter()
+    eng.prefill(prompt, logits=False)
+    serial_ms = (time.perf_counter() - t0) * 1e3
+    eng.set_prefill_batch(256)
+    toks, pf_ms, dc_ms = eng.generate(prompt, 512)
+    eng.close()
+
+    # the GEMMs alone, on the stream the wrapper launches on
+    g = vg.GPU(0)
+    rng = np.random.default_rng(0)
+    gemms = []
+    for name, rows, cols in (("qkv", 1536, 768), ("wo", 768, 768), ("w1/w3 chunk", 1216, 768), ("w2", 768, 2432)):
+        W = g.upload(make_matrix(rng, rows, cols, "q4"))
+        x = torch.from_numpy(rng.integers(-3000, 3000, (256, cols)).astype(np.int16)).cuda()
+        y = torch.empty((256, rows), dtype=torch.int16, device="cuda")
+        for _ in range(3):
+            g.gemm(W, x, out=y)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(100):
+            g.gemm(W, x, out=y)
+        b.record()
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / 100
+        tops = 2.0 * 256 * rows * cols / (us * 1e-6) / 1e12
+        gemms.append({"gemm": name, "M_tokens": 256, "N": rows, "K": cols, "kind": "q4", "us": round(us, 2),
+                      "int8_TOPS": round(tops, 2), "frac_of_peak": round(tops / INT8_PEAK_TOPS, 5)})
+        W.free()
+    g.close()
+    med = float(np.median(batched))
+    return {"model": "MiniMind3-64M-shaped, q4 g32, seed 0", "kv": "q8", "seq": 768, "prompt": 256,
+            "batched_prefill_ms": round(med, 3), "batched_prefill_tokens_per_s": round(256 / med * 1e3, 1),
+            "serial_prefill_ms": round(serial_ms, 3), "serial_prefill_tokens_per_s": round(256 / serial_ms * 1e3, 1),
+            "speedup": round(serial_ms / med, 2), "runs": runs,
+            "generate_512": {"prefill_ms": round(pf_ms, 3), "decode_ms": round(dc_ms, 3),
+                             "decode_tokens_per_s": round(511 / dc_ms * 1e3, 1)},
+            "gemm_int8_peak_TOPS": INT8_PEAK_TOPS, "gemms": gemms}
+
+
 def decode_cpu_baseline(blob, prompt, steps):
     """The float CPU path (oracle/model.py FModel: the reference's numpy
     forward semantics on the dequantised container) for `steps` positions."""
@@ -197,24 +262,29 @@ def main():
     ap.add_argument("--skip-decode", action="store_true")
     ap.add_argument("--copy-mb", type=int, default=0, help="also time a device copy of this many MiB")
     ap.add_argument("--cpu-decode-steps", type=int, default=16)
-    ap.add_argument("--only", choices=["gemv", "decode"], default=None,
+    ap.add_argument("--only", choices=["gemv", "decode", "prefill"], default=None,
                     help="run one leg (for profiling); the JSON line then carries that leg only")
+    ap.add_argument("--prefill-runs", type=int, default=5)
+    ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "BENCH_LOG"),
                     help="print the HBM traffic summary of two rocprofv3 --pmc runs and exit (no GPU)")
     args = ap.parse_args()
     if args.pmc_summary:
         print(json.dumps(pmc_summary(*args.pmc_summary), indent=1))
         return
+    if args.gpus != 1:
+        print("bench.py measures one GPU: the decode path runs on a single device; --gpus %d is not measured"
+              % args.gpus, file=sys.stderr)
+        sys.exit(2)
     if args.only == "decode":
         blob, prompt, toks, dec = decode_bench(args.decode_runs)
         print(json.dumps({"decode": dec}))
         return
+    if args.only == "prefill":
+        print(json.dumps({"prefill": prefill_bench(args.prefill_runs)}))
+        return
     if args.only == "gemv":
-        args.skip_decode, args.no_cpu = True, True
-    if args.gpus != 1:
-        print("bench.py runs on one GPU: the decode path is single-device (see DESIGN.md); --gpus %d "
-              "is not measured" % args.gpus, file=sys.stderr)
-        sys.exit(2)
+        args.skip_decode, args.no_cpu, args.skip_prefill = True, True, True
 
     import numpy as np
     import torch
@@ -334,6 +404,8 @@ def main():
         blob, prompt, toks, dec = decode_bench(args.decode_runs)
         out["decode"] = dec
         out["decode_tokens_per_s"] = dec["tokens_per_s"]
+    if not args.skip_prefill:
+        out["prefill"] = prefill_bench(args.prefill_runs)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
         if not args.skip_decode:

@@ -168,6 +168,33 @@ int vgx_gemv_group_rms(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, const
 int vgx_logits_argmax_rms(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, const int16_t* rms_w, float eps,
                           int16_t* logits, int* token);
 
+/* ---- batched prefill: ntok consecutive positions per launch, every row the
+ * exact result of the batch-1 entry point on that token.  Replaces
+ * Session::step_group's per-position draws (engine/src/session.cpp:1741-1795)
+ * and the two-position P2 kernels (matvec_q8_p2 and the pair gate,
+ * engine/src/shaders.cpp:825-1072): the reference's rule for a batched path
+ * is byte-identical logits to the serial one (docs/prefill-batching.md:98-113).
+ * Activations are row-major, ntok rows of cols (x) or rows (y, res, h) q16
+ * values; the GEMMs run on the int8 matrix cores.
+ *   vgx_gemm            per token: vgx_gemv (y = q16(W.x [+ res]))
+ *   vgx_gemm_add_split  per token: vgx_gemv_add_split
+ *   vgx_ffn_gate_batch  per token: vgx_ffn_gate
+ *   vgx_rmsnorm_batch   per token: vgx_rmsnorm (upload_hidden_grp + rmsnorm,
+ *                       engine/src/gpu_upload.cpp:250)
+ *   vgx_embed_q8_batch  per token: vgx_embed_q8; tokens is a device int array
+ *   vgx_kv_append_batch / vgx_attn_decode_batch: positions pos0 .. pos0+ntok-1,
+ *     qkv and out rows consecutive; the KV rows are written first, then every
+ *     position attends to its prefix (att_stage, att_scores_batch,
+ *     att_stats_row, att_v_row: engine/src/gpu_attn.cpp:433-532). */
+int vgx_gemm(vgx_ctx* ctx, const vgx_mat* W, int ntok, const int16_t* x, const int16_t* res, int16_t* y);
+int vgx_gemm_add_split(vgx_ctx* ctx, const vgx_mat* W, int split, int ntok, const int16_t* x, const int16_t* res,
+                       int16_t* y);
+int vgx_ffn_gate_batch(vgx_ctx* ctx, const vgx_mat* W1, const vgx_mat* W3, int ntok, const int16_t* x, int hs,
+                       int16_t* h);
+int vgx_rmsnorm_batch(vgx_ctx* ctx, int ntok, int dim, const int16_t* x, const int16_t* w, float eps, int16_t* y);
+int vgx_embed_q8_batch(vgx_ctx* ctx, const int8_t* emb, const float* emb_scale, int vocab, int dim, int ntok,
+                       const int* tokens, int16_t* x);
+
 /* Session::embedding (engine/src/session.cpp:342-371), q8 rows: x = the
  * host-grid q16 of emb[token]*emb_scale[token].  emb: vocab x dim signed
  * bytes (device), emb_scale: vocab f32 (device), token: device int. */
@@ -196,6 +223,11 @@ int vgx_kv_append(vgx_attn* a, int layer, int pos, const int16_t* qkv);
 int vgx_attn_decode(vgx_attn* a, int layer, int pos, const int16_t* qkv, int16_t* out);
 /* vgx_kv_append then vgx_attn_decode in one launch. */
 int vgx_attn_block(vgx_attn* a, int layer, int pos, const int16_t* qkv, int16_t* out);
+/* Batched forms for positions pos0 .. pos0+ntok-1 (see the batched prefill
+ * block above; engine/src/gpu_attn.cpp:433-532): qkv holds ntok consecutive
+ * rows of dim + 2*kv_dim, out ntok rows of dim.  Append all rows first. */
+int vgx_kv_append_batch(vgx_attn* a, int layer, int pos0, int ntok, const int16_t* qkv);
+int vgx_attn_decode_batch(vgx_attn* a, int layer, int pos0, int ntok, const int16_t* qkv, int16_t* out);
 /* The packed KV rows in the reference's texel byte layout (K values then V
  * values; q16 big-endian, q8 two's-complement bytes) -- what MMKV1 persists
  * (engine/src/prefix_cache.cpp:59-67).  Host buffers; these block. */

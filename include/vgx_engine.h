@@ -37,6 +37,16 @@ int vgx_engine_step(vgx_engine* e, int token, int pos, int16_t* logits_host, int
  * the n_gen-1 steps after it.  Either timing pointer may be NULL. */
 int vgx_engine_generate(vgx_engine* e, const int* prompt, int n_prompt, int n_gen, int* out,
                         double* prefill_ms, double* decode_ms);
+/* Prompt positions pos0 .. pos0+n-1 in batches: Session::step_group
+ * (engine/src/session.cpp:1741-1795) on the int8 matrix cores.  Every
+ * position's result equals vgx_engine_step's, so logits_host (vocab int16 of
+ * the last position, may be NULL) and next are what n serial steps give. */
+int vgx_engine_prefill(vgx_engine* e, const int* tokens, int n, int pos0, int16_t* logits_host, int* next);
+/* Largest batch a prompt is prefilled in (the reference's PREFILL_BATCH,
+ * docs/prefill-batching.md): 0 or 1 = one position at a time; at most
+ * min(seq, 512), which is also the default.  Applies to vgx_engine_prefill
+ * and to vgx_engine_generate's prompt. */
+int vgx_engine_set_prefill_batch(vgx_engine* e, int n);
 /* The message of the last failed engine call on this thread. */
 const char* vgx_engine_last_error(void);
 

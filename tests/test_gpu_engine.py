@@ -96,6 +96,61 @@ def test_minimind3_q4_kv8(gpu):
     eng.close()
 
 
+@pytest.mark.parametrize("scheme", ["q8", "q4", "t3"])
+def test_prefill_batches_equal_serial(gpu, scheme):
+    """The reference's acceptance for a batched prefill: the logits after the
+    prompt are byte-identical to the serial loop's (docs/prefill-batching.md:
+    98-113), for one batch, uneven batches, and a prompt continued at pos0 > 0."""
+    spec = synth.tiny_spec(seq=48, hidden=2112 if scheme != "t3" else 96)
+    blob = synth.container(spec, scheme, seed=4)
+    prompt = synth.prompt(29, spec.vocab, seed=3)
+    ser = Engine(blob)
+    ser.set_prefill_batch(0)
+    want, wn = ser.prefill(prompt)
+    ref = QModel(blob)
+    for pos in range(len(prompt)):
+        lq = ref.step(int(prompt[pos]), pos, want_logits=pos == len(prompt) - 1)
+    assert np.array_equal(want, lq)
+    for batch in (48, 8, 5):
+        eng = Engine(blob)
+        eng.set_prefill_batch(batch)
+        got, gn = eng.prefill(prompt)
+        assert np.array_equal(got, want), batch
+        assert gn == wn
+        if batch == 48:
+            # decode continues identically from the batched KV
+            a, _ = eng.step(gn, len(prompt))
+            b, _ = ser.step(wn, len(prompt))
+            assert np.array_equal(a, b)
+        eng.close()
+    # prompt split over two calls: positions 0..11, then 12..28
+    eng = Engine(blob)
+    eng.prefill(prompt[:12], 0, logits=False)
+    got, _ = eng.prefill(prompt[12:], 12)
+    assert np.array_equal(got, want)
+    eng.close()
+    ser.close()
+
+
+def test_minimind3_q4_prefill_256_kv8(gpu):
+    """The C3 shape: MiniMind3 q4, KV q8, SEQ 768, a 256-token prompt in one
+    batch against the serial loop, then greedy decode from both."""
+    spec = synth.minimind3_spec(seq=768)
+    blob = synth.container(spec, "q4", seed=0)
+    prompt = synth.prompt(256, spec.vocab, seed=0)
+    a, b = Engine(blob, kv_bits=8), Engine(blob, kv_bits=8)
+    b.set_prefill_batch(0)
+    la, ta = a.prefill(prompt)
+    lb, tb = b.prefill(prompt)
+    assert np.array_equal(la, lb) and ta == tb
+    for pos in range(256, 264):
+        la, ta = a.step(ta, pos)
+        lb, tb = b.step(tb, pos)
+        assert np.array_equal(la, lb) and ta == tb, pos
+    a.close()
+    b.close()
+
+
 def test_engine_refusals(gpu):
     from vgx import lib as vl
     spec = synth.tiny_spec(seq=8)

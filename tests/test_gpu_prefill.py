@@ -1,0 +1,139 @@
+"""Batched prefill (int8 matrix cores) against the batch-1 path: every row of
+every batched op must equal the oracle's batch-1 result on that token, bit
+for bit -- the reference's acceptance rule for a batched path
+(docs/prefill-batching.md:98-113)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as o
+from test_gpu_kernels import dev, host, oracle_rowval, q4_matrix, q8_matrix, rand_x, t3_matrix
+
+pytestmark = pytest.mark.gpu
+
+MK = {"q8": q8_matrix, "q4": q4_matrix, "t3": t3_matrix}
+
+
+def x_rows(rng, ntok, cols, full=False):
+    if full:
+        return rng.integers(-32768, 32768, (ntok, cols)).astype(np.int16)
+    return np.stack([rand_x(rng, cols) for _ in range(ntok)])
+
+
+@pytest.mark.parametrize("kind,rows,cols", [("q8", 1536, 768), ("q8", 768, 2432), ("q8", 33, 96), ("q8", 7, 48),
+                                            ("q4", 1536, 768), ("q4", 768, 2432), ("q4", 33, 96),
+                                            ("t3", 1280, 1024), ("t3", 33, 96)])
+@pytest.mark.parametrize("ntok", [1, 5, 37, 64])
+def test_gemm_rows_equal_gemv(gpu, kind, rows, cols, ntok):
+    rng = np.random.default_rng(rows + 7 * cols + ntok)
+    m = MK[kind](rng, rows, cols)
+    W = gpu.upload(m)
+    x = x_rows(rng, ntok, cols)
+    res = x_rows(rng, ntok, rows)
+    got = host(gpu.gemm(W, dev(x)))
+    got_r = host(gpu.gemm(W, dev(x), res=dev(res)))
+    for t in range(ntok):
+        v = oracle_rowval(m, x[t])
+        assert np.array_equal(got[t], o.store(v)), t
+        assert np.array_equal(got_r[t], o.store(v, res[t])), t
+
+
+@pytest.mark.parametrize("kind", ["q8", "t3"])
+def test_gemm_full_range(gpu, kind):
+    # int16 extremes and every weight byte: the byte-plane split and its
+    # -128 offset stay exact
+    rng = np.random.default_rng(3)
+    m = q8_matrix(rng, 96, 512, full=True) if kind == "q8" else t3_matrix(rng, 96, 512)
+    W = gpu.upload(m)
+    x = x_rows(rng, 40, 512, full=True)
+    x[0, :] = -32768
+    x[1, :] = 32767
+    got = host(gpu.gemm(W, dev(x)))
+    for t in range(40):
+        assert np.array_equal(got[t], o.store(oracle_rowval(m, x[t]))), t
+
+
+@pytest.mark.parametrize("kind,rows,cols,split", [("q8", 768, 2432, 1216), ("q8", 40, 96, 48),
+                                                  ("q4", 768, 2432, 1216), ("t3", 256, 1024, 512)])
+def test_gemm_add_split(gpu, kind, rows, cols, split):
+    # split 48 of 96 falls in the middle of a 32-column matrix-core step
+    rng = np.random.default_rng(cols + split)
+    m = MK[kind](rng, rows, cols)
+    m.scale_mul = 4.0
+    W = gpu.upload(m)
+    ntok = 33
+    x = x_rows(rng, ntok, cols)
+    res = x_rows(rng, ntok, rows)
+    got = host(gpu.gemm_add_split(W, split, dev(x), dev(res)))
+    a, b = m.slice_cols(0, split), m.slice_cols(split, cols)
+    for t in range(ntok):
+        y1 = o.store(oracle_rowval(a, x[t, :split]), res[t])
+        assert np.array_equal(got[t], o.store(oracle_rowval(b, x[t, split:]), y1)), t
+
+
+@pytest.mark.parametrize("kind,rows,cols", [("q8", 2432, 768), ("q4", 1216, 768), ("t3", 512, 1024)])
+def test_ffn_gate_batch(gpu, kind, rows, cols):
+    rng = np.random.default_rng(rows)
+    m1, m3 = MK[kind](rng, rows, cols), MK[kind](rng, rows, cols)
+    W1, W3 = gpu.upload(m1), gpu.upload(m3)
+    x = x_rows(rng, 37, cols)
+    for hs in (0, 2):
+        got = host(gpu.ffn_gate_batch(W1, W3, dev(x), hs))
+        for t in range(37):
+            want = o.gate(oracle_rowval(m1, x[t]), oracle_rowval(m3, x[t]), hs)
+            assert np.array_equal(got[t], want), (hs, t)
+
+
+def test_rmsnorm_and_embed_batch(gpu):
+    rng = np.random.default_rng(5)
+    x = np.clip(rng.standard_normal((19, 768)) * 900, -32768, 32767).astype(np.int16)
+    w = o.quantize_act(rng.uniform(0.5, 1.5, 768).astype(np.float32))
+    got = host(gpu.rmsnorm_batch(dev(x), dev(w), 1e-5))
+    for t in range(19):
+        assert np.array_equal(got[t], o.rmsnorm(x[t], w, 1e-5)), t
+    emb = rng.integers(-127, 128, (6400, 768)).astype(np.int8)
+    es = rng.uniform(1e-4, 1e-2, 6400).astype(np.float32)
+    toks = np.array([0, 17, 6399, 17, 5], np.int32)
+    got = host(gpu.embed_q8_batch(dev(emb), dev(es), dev(toks)))
+    for t, tk in enumerate(toks):
+        assert np.array_equal(got[t], o.embed_q8(emb, es, int(tk))), t
+
+
+@pytest.mark.parametrize("kv_bits", [16, 8])
+def test_attention_batch_equals_serial(gpu, kv_bits):
+    # MiniMind3 heads: 20 positions one at a time against batches of 7 and 13
+    dim, heads, kvh, hd, seq = 768, 8, 4, 96, 64
+    rc, rs = o.rope_cos_sin(1e6, hd, seq)
+    rng = np.random.default_rng(kv_bits)
+    qn = rng.uniform(0.5, 1.5, (1, hd)).astype(np.float32)
+    kn = rng.uniform(0.5, 1.5, (1, hd)).astype(np.float32)
+
+    def make():
+        return gpu.attention(dim=dim, heads=heads, kv_heads=kvh, head_dim=hd, seq=seq, layers=1, kv_bits=kv_bits,
+                             rope_half=1, qk_norm=1, rope_cos=rc, rope_sin=rs, q_norm=qn, k_norm=kn)
+
+    A1, A2 = make(), make()
+    qkv = np.clip(rng.standard_normal((20, dim + 2 * kvh * hd)) * 300, -32768, 32767).astype(np.int16)
+    serial = np.stack([host(A1.block(0, p, dev(qkv[p]))) for p in range(20)])
+    b1 = host(A2.block_batch(0, 0, dev(qkv[:7])))
+    b2 = host(A2.block_batch(0, 7, dev(qkv[7:])))
+    assert np.array_equal(np.concatenate([b1, b2]), serial)
+    assert np.array_equal(A1.read_rows(0, 0, 20), A2.read_rows(0, 0, 20))
+    A1.free()
+    A2.free()
+
+
+def test_batch_refusals(gpu):
+    from vgx.lib import VgxError
+    rng = np.random.default_rng(9)
+    W = gpu.upload(q8_matrix(rng, 64, 64))
+    with pytest.raises(VgxError):
+        gpu.gemm(W, torch.empty((0, 64), dtype=torch.int16, device="cuda"))
+    with pytest.raises(VgxError):
+        gpu.gemm_add_split(W, 40, dev(x_rows(rng, 3, 64)), dev(x_rows(rng, 3, 64)))  # not a multiple of 16
+    rc, rs = o.rope_cos_sin(1e6, 64, 8)
+    A = gpu.attention(dim=128, heads=2, kv_heads=1, head_dim=64, seq=8, layers=1, kv_bits=16, rope_half=1,
+                      qk_norm=0, rope_cos=rc, rope_sin=rs)
+    with pytest.raises(VgxError):
+        A.block_batch(0, 5, dev(np.zeros((4, 256), np.int16)))  # positions 5..8 past the cache
+    A.free()

@@ -144,12 +144,17 @@ __device__ __forceinline__ long long dot_row(const int* q, const uint8_t* k, int
 template <int KVB>
 __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t* kv, const int32_t* rtab,
                                                         const int16_t* qn, const int16_t* kn,
-                                                        const int16_t* qkv, int16_t* out, int pos,
+                                                        const int16_t* qkv, int16_t* out, int pos0,
                                                         int do_write, int do_attend) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int kvh = blockIdx.x;
     const int hd = A.hd, G = A.group, kv_dim = A.kv_heads * hd, GH = G * hd, seq = A.seq;
     const int tid = threadIdx.x;
+    // blockIdx.y: the position's offset in a batch of consecutive positions,
+    // whose qkv and output rows are consecutive rows
+    const int pos = pos0 + blockIdx.y;
+    qkv += (size_t)blockIdx.y * (A.dim + 2 * kv_dim);
+    if (out) out += (size_t)blockIdx.y * A.dim;
     const int npos = pos + 1;
     const int nch = (npos + kChunk - 1) / kChunk;
 
@@ -378,22 +383,29 @@ size_t attn_layout(AttnDev& A) {
     return off;
 }
 
-int launch(vgx_attn* at, int layer, int pos, const int16_t* qkv, int16_t* out, int w, int att) {
+// Positions pos .. pos + ntok - 1 (their qkv and output rows consecutive).
+// With ntok > 1 the KV write and the attention must be separate launches: a
+// position reads the rows the others write.
+int launch(vgx_attn* at, int layer, int pos, int ntok, const int16_t* qkv, int16_t* out, int w, int att) {
     if (!at) return vgx_fail(VGX_EINVAL, "attention: NULL handle");
     if (layer < 0 || layer >= at->layers || !at->kv[layer])
         return vgx_fail(VGX_ERANGE, "attention: layer " + std::to_string(layer) + " has no KV cache");
-    if (pos < 0 || pos >= at->a.seq)
-        return vgx_fail(VGX_ERANGE, "attention: pos " + std::to_string(pos) + " outside the KV length");
+    if (ntok <= 0 || ntok > 65535) return vgx_fail(VGX_EINVAL, "attention: ntok outside 1..65535");
+    if (pos < 0 || pos > at->a.seq - ntok)
+        return vgx_fail(VGX_ERANGE, "attention: positions " + std::to_string(pos) + ".." +
+                                        std::to_string(pos + ntok - 1) + " outside the KV length");
     if (!qkv || (att && !out)) return vgx_fail(VGX_EINVAL, "attention: NULL buffer");
+    if (ntok > 1 && w && att) return vgx_fail(VGX_EINVAL, "attention: a batch writes its KV rows first");
     VGX_HIP(hipSetDevice(at->ctx->device));
     const AttnDev& A = at->a;
     const int16_t* qn = at->qn ? at->qn + (size_t)layer * A.hd : nullptr;
     const int16_t* kn = at->kn ? at->kn + (size_t)layer * A.hd : nullptr;
+    const dim3 grid(A.kv_heads, ntok);
     if (A.kv_bits == 16)
-        hipLaunchKernelGGL(attn_kernel<16>, dim3(A.kv_heads), dim3(kThreads), at->lds, at->ctx->stream, A,
+        hipLaunchKernelGGL(attn_kernel<16>, grid, dim3(kThreads), at->lds, at->ctx->stream, A,
                            at->kv[layer], at->rtab, qn, kn, qkv, out, pos, w, att);
     else
-        hipLaunchKernelGGL(attn_kernel<8>, dim3(A.kv_heads), dim3(kThreads), at->lds, at->ctx->stream, A,
+        hipLaunchKernelGGL(attn_kernel<8>, grid, dim3(kThreads), at->lds, at->ctx->stream, A,
                            at->kv[layer], at->rtab, qn, kn, qkv, out, pos, w, att);
     VGX_LAUNCH_CHECK("attention launch");
     return VGX_OK;
@@ -481,15 +493,23 @@ int vgx_attn_free(vgx_attn* at) {
 }
 
 int vgx_kv_append(vgx_attn* a, int layer, int pos, const int16_t* qkv) {
-    return launch(a, layer, pos, qkv, nullptr, 1, 0);
+    return launch(a, layer, pos, 1, qkv, nullptr, 1, 0);
 }
 
 int vgx_attn_decode(vgx_attn* a, int layer, int pos, const int16_t* qkv, int16_t* out) {
-    return launch(a, layer, pos, qkv, out, 0, 1);
+    return launch(a, layer, pos, 1, qkv, out, 0, 1);
 }
 
 int vgx_attn_block(vgx_attn* a, int layer, int pos, const int16_t* qkv, int16_t* out) {
-    return launch(a, layer, pos, qkv, out, 1, 1);
+    return launch(a, layer, pos, 1, qkv, out, 1, 1);
+}
+
+int vgx_kv_append_batch(vgx_attn* a, int layer, int pos0, int ntok, const int16_t* qkv) {
+    return launch(a, layer, pos0, ntok, qkv, nullptr, 1, 0);
+}
+
+int vgx_attn_decode_batch(vgx_attn* a, int layer, int pos0, int ntok, const int16_t* qkv, int16_t* out) {
+    return launch(a, layer, pos0, ntok, qkv, out, 0, 1);
 }
 
 int vgx_kv_row_bytes(const vgx_attn* a) { return a ? a->a.row_bytes : 0; }

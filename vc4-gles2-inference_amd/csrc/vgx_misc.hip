@@ -18,11 +18,13 @@ __device__ __forceinline__ int q16_round(float v) {
 // rms_stats_split's 32 partial sums of v^2 over contiguous slices of
 // ceil(dim/32) values, each on the 1/4096 grid (P = sum x^2 in Q units, stored
 // value floor(P/16 + 1/2)), their total ss, inv = inversesqrt(ss/dim + eps),
-// y = q16(x * inv * w).
+// y = q16(x * inv * w).  One workgroup per row of x (rows `dim` apart).
 __global__ void __launch_bounds__(256) rmsnorm_kernel(const int16_t* x, const int16_t* w, int dim,
                                                        float eps, int16_t* y) {
     __shared__ long long part[32];
     __shared__ float s_inv;
+    x += (size_t)blockIdx.x * dim;
+    y += (size_t)blockIdx.x * dim;
     const int per = (dim + 31) / 32;
     const int tid = threadIdx.x;
     // 8 threads per partial slice
@@ -53,10 +55,12 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const int16_t* x, const in
     }
 }
 
-// Session::embedding, q8 rows (engine/src/session.cpp:362-365).
+// Session::embedding, q8 rows (engine/src/session.cpp:362-365).  Row
+// blockIdx.y of x takes token[blockIdx.y].
 __global__ void embed_q8_kernel(const int8_t* emb, const float* scale, int vocab, int dim,
                                 const int* token, int16_t* x) {
-    int tok = *token;
+    x += (size_t)blockIdx.y * dim;
+    int tok = token[blockIdx.y];
     if (tok < 0) tok = 0;
     if (tok >= vocab) tok = vocab - 1;
     const float s = scale[tok];
@@ -87,6 +91,29 @@ int vgx_embed_q8(vgx_ctx* ctx, const int8_t* emb, const float* emb_scale, int vo
     if (vocab <= 0 || dim <= 0) return vgx_fail(VGX_EINVAL, "vgx_embed_q8: empty shape");
     VGX_HIP(hipSetDevice(ctx->device));
     hipLaunchKernelGGL(embed_q8_kernel, dim3(1), dim3(256), 0, ctx->stream, emb, emb_scale, vocab, dim, token, x);
+    VGX_LAUNCH_CHECK("embed launch");
+    return VGX_OK;
+}
+
+int vgx_rmsnorm_batch(vgx_ctx* ctx, int ntok, int dim, const int16_t* x, const int16_t* w, float eps,
+                      int16_t* y) {
+    if (!ctx || !x || !w || !y) return vgx_fail(VGX_EINVAL, "vgx_rmsnorm_batch: NULL argument");
+    if (dim <= 0 || dim > 65536) return vgx_fail(VGX_EINVAL, "vgx_rmsnorm_batch: dim outside 1..65536");
+    if (ntok <= 0 || ntok > 65535) return vgx_fail(VGX_EINVAL, "vgx_rmsnorm_batch: ntok outside 1..65535");
+    VGX_HIP(hipSetDevice(ctx->device));
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(ntok), dim3(256), 0, ctx->stream, x, w, dim, eps, y);
+    VGX_LAUNCH_CHECK("rmsnorm launch");
+    return VGX_OK;
+}
+
+int vgx_embed_q8_batch(vgx_ctx* ctx, const int8_t* emb, const float* emb_scale, int vocab, int dim, int ntok,
+                       const int* tokens, int16_t* x) {
+    if (!ctx || !emb || !emb_scale || !tokens || !x) return vgx_fail(VGX_EINVAL, "vgx_embed_q8_batch: NULL argument");
+    if (vocab <= 0 || dim <= 0) return vgx_fail(VGX_EINVAL, "vgx_embed_q8_batch: empty shape");
+    if (ntok <= 0 || ntok > 65535) return vgx_fail(VGX_EINVAL, "vgx_embed_q8_batch: ntok outside 1..65535");
+    VGX_HIP(hipSetDevice(ctx->device));
+    hipLaunchKernelGGL(embed_q8_kernel, dim3(1, ntok), dim3(256), 0, ctx->stream, emb, emb_scale, vocab, dim, tokens,
+                       x);
     VGX_LAUNCH_CHECK("embed launch");
     return VGX_OK;
 }

@@ -1,0 +1,371 @@
+// Batched prefill on the int8 matrix cores: Y[t] = W . X[t] for ntok token
+// rows at once, the same exact integer sums as the batch-1 GEMV, so every
+// output row is bit-identical to vgx_gemv on that token (the reference's
+// acceptance rule for a batched path: the logits of a grouped prefill equal
+// the serial ones byte for byte, docs/prefill-batching.md:98-113;
+// Session::step_group, engine/src/session.cpp:1741-1795).
+//
+// v_mfma_i32_32x32x32_i8: one wave multiplies a 32 x 32 int8 tile of A by a
+// 32 x 32 tile of B into 32 x 32 int32.  Lane l supplies
+//   A[m = l % 32][k = 16*(l/32) .. +15]   (16 int8)
+//   B[k = 16*(l/32) .. +15][n = l % 32]   (16 int8)
+// and holds C[8*(r/4) + 4*(l/32) + r%4][l % 32] in accumulator r (0..15).
+// Here A = activation tokens x columns and B^T = weight rows x columns, so a
+// lane's B operand is 16 consecutive weight columns of one row: one 16-byte
+// (q8) or 8-byte (q4, t3) load.  The q16 activations are split in registers
+// into two int8 planes,
+//   x = 256*xh + (xl - 128) + 128,   xh = signed high byte, xl = low byte,
+// so  sum w*x = 256*sum w*xh + sum w*(xl - 128) + 128*sum w, every term an
+// exact integer (|partial| <= 128*128*K < 2^31 for K <= 32768).
+//
+// A wave owns a 32-token x 32-row output tile; a workgroup is 4 waves over 128
+// consecutive weight rows.  Epilogues restate the batch-1 GEMV's fp32
+// expressions: q16 store (+ residual, one rounding), the SwiGLU gate over W1
+// and W3, and the two-half residual add of the split w2.  q4 applies its
+// per-group fp32 terms after each 32-column group (one MFMA k-step = one
+// group) and sums them in double in group order, as the oracle does.
+#include <cmath>
+#include <string>
+
+#include "vgx_internal.h"
+
+#pragma clang fp contract(off)
+
+namespace {
+
+typedef signed char i8x16 __attribute__((ext_vector_type(16)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kTile = 32;  // tokens and weight rows per wave tile
+
+enum BatchEpi { BEPI_STORE = 0, BEPI_GATE = 1, BEPI_SPLIT = 2 };
+
+struct GemmLaunch {
+    MatDev M, M3;           // W (and W3 for the gate)
+    int ntok, cols;
+    const int16_t* x;       // ntok rows of cols q16 values, row stride ldx
+    int ldx;
+    const int16_t* res;     // residual rows (stride ldy) or nullptr
+    int16_t* y;             // ntok rows of M.rows q16 values, row stride ldy
+    int ldy;
+    int hs;                 // gate: hidden store exponent
+    int split;              // split: first column of the second half
+};
+
+union Op {
+    i8x16 v;
+    uint32_t d[4];
+};
+
+__device__ __forceinline__ int q16_round(float v) {
+    float f = floorf(v + 0.5f);
+    f = fminf(fmaxf(f, -32768.0f), 32767.0f);
+    return (int)f;
+}
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+__device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) {
+    return __builtin_amdgcn_perm(s0, s1, sel);
+}
+
+__device__ __forceinline__ i32x16 mfma(const Op& a, const Op& b, const i32x16& c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a.v, b.v, c, 0, 0, 0);
+}
+
+// A operands: 16 q16 activations at columns k0..k0+15 of one token row, as the
+// high-byte plane and the low-byte plane minus 128; xsum = their exact sum.
+__device__ __forceinline__ void x_operands(const int16_t* xrow, int k0, bool ok, Op& xh, Op& xl, int& xsum) {
+    if (!ok) {
+        for (int i = 0; i < 4; ++i) { xh.d[i] = 0u; xl.d[i] = 0u; }
+        xsum = 0;
+        return;
+    }
+    const uint4* p = reinterpret_cast<const uint4*>(xrow + k0);
+    const uint4 a = p[0], b = p[1];
+    const uint32_t d[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    int sh = 0;
+    uint32_t sl = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t lo = perm(d[2 * k + 1], d[2 * k], 0x06040200u);  // low bytes of 4k..4k+3
+        const uint32_t hi = perm(d[2 * k + 1], d[2 * k], 0x07050301u);
+        xh.d[k] = hi;
+        xl.d[k] = lo ^ 0x80808080u;
+        sh = sdot4(hi, 0x01010101u, sh);
+        sl = __builtin_amdgcn_udot4(lo, 0x01010101u, sl, false);
+    }
+    xsum = 256 * sh + (int)sl;
+}
+
+// Four 2-bit t3 codes (one byte) as four int8 levels: bit 0 = |level|,
+// bit 1 = sign (engine/tools/mmcf_hf.py:168-199).
+__device__ __forceinline__ uint32_t t3_levels(uint32_t b) {
+    uint32_t r = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t c = (b >> (2 * j)) & 3u;
+        const uint32_t lv = c == 1u ? 0x01u : (c == 3u ? 0xFFu : 0x00u);
+        r |= lv << (8 * j);
+    }
+    return r;
+}
+
+// B operand: weight row n, columns k0..k0+15, as int8 levels; wsum = their sum.
+template <int KIND>
+__device__ __forceinline__ void w_operand(const MatDev& M, int n, int k0, int K, bool ok, Op& w, int& wsum) {
+    if (!ok) {
+        for (int i = 0; i < 4; ++i) w.d[i] = 0u;
+        wsum = 0;
+        return;
+    }
+    if (KIND == VGX_Q8) {
+        const uint4 v = *reinterpret_cast<const uint4*>(M.body + (size_t)n * K + k0);
+        w.d[0] = v.x ^ 0x80808080u;
+        w.d[1] = v.y ^ 0x80808080u;
+        w.d[2] = v.z ^ 0x80808080u;
+        w.d[3] = v.w ^ 0x80808080u;
+    } else if (KIND == VGX_Q4) {
+        const uint2 v = *reinterpret_cast<const uint2*>(M.body + (size_t)n * (K >> 1) + (k0 >> 1));
+        const uint32_t lo0 = v.x & 0x0F0F0F0Fu, hi0 = (v.x >> 4) & 0x0F0F0F0Fu;
+        const uint32_t lo1 = v.y & 0x0F0F0F0Fu, hi1 = (v.y >> 4) & 0x0F0F0F0Fu;
+        // low nibble = even column: interleave (lo.b0, hi.b0, lo.b1, hi.b1), ...
+        w.d[0] = perm(hi0, lo0, 0x05010400u);
+        w.d[1] = perm(hi0, lo0, 0x07030602u);
+        w.d[2] = perm(hi1, lo1, 0x05010400u);
+        w.d[3] = perm(hi1, lo1, 0x07030602u);
+    } else {
+        // texel (c, u): b0 b1 = row 2u columns 8c..8c+7, b2 b3 = row 2u+1
+        const size_t ustride = (size_t)(K >> 3) * 4;
+        const uint2 v = *reinterpret_cast<const uint2*>(M.body + (size_t)(n >> 1) * ustride + (size_t)(k0 >> 3) * 4);
+        const int sh = (n & 1) * 16;
+        w.d[0] = t3_levels((v.x >> sh) & 0xFFu);
+        w.d[1] = t3_levels((v.x >> (sh + 8)) & 0xFFu);
+        w.d[2] = t3_levels((v.y >> sh) & 0xFFu);
+        w.d[3] = t3_levels((v.y >> (sh + 8)) & 0xFFu);
+    }
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s = sdot4(w.d[i], 0x01010101u, s);
+    wsum = s;
+}
+
+__device__ __forceinline__ float gate_value(float v1, float v3, int hs) {
+    const float g = (float)q16_round(v1), uu = (float)q16_round(v3);
+    const float a = g / 256.0f;
+    const float e = (float)exp(-(double)a);
+    const float dn = 1.0f + e;
+    const float r = a / dn;
+    float o = r * (uu / 256.0f);
+    o = o * ldexpf(1.0f, -hs);
+    return o * 256.0f;
+}
+
+template <int KIND, int EPI>
+__global__ void __launch_bounds__(kThreads) gemm_kernel(const GemmLaunch G) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int half = lane >> 5;
+    const int li = lane & 31;
+    const int n0 = (blockIdx.x * kWaves + wave) * kTile;
+    const int t0 = blockIdx.y * kTile;
+    const int K = G.cols;
+    const MatDev& M = G.M;
+    const int n = n0 + li;  // this lane's weight row (B operand) and output column
+    const int t = t0 + li;  // this lane's token row (A operand)
+    const bool nok = n < M.rows;
+    const bool tok = t < G.ntok;
+    const int16_t* xrow = G.x + (size_t)(tok ? t : 0) * G.ldx;
+    const int nsteps = (K + kTile - 1) / kTile;
+    constexpr int NA = EPI == BEPI_STORE ? 1 : 2;  // accumulator sets: W1/W3 or the two halves
+
+    i32x16 ch[NA], cl[NA];
+    double dacc[NA][16];
+    int wsum[NA];
+#pragma unroll
+    for (int a = 0; a < NA; ++a) {
+        ch[a] = (i32x16){};
+        cl[a] = (i32x16){};
+        wsum[a] = 0;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dacc[a][r] = 0.0;
+    }
+    const float ps = M.ps, ps3 = G.M3.ps;
+
+    for (int s = 0; s < nsteps; ++s) {
+        const int k0 = s * kTile + half * 16;
+        const bool kok = k0 < K;
+        Op xh, xl, w, w3;
+        int xs, ws, ws3 = 0;
+        x_operands(xrow, k0, tok && kok, xh, xl, xs);
+        w_operand<KIND>(M, n, k0, K, nok && kok, w, ws);
+        if (EPI == BEPI_GATE) w_operand<KIND>(G.M3, n, k0, K, nok && kok, w3, ws3);
+        if (KIND != VGX_Q4) {
+            if (EPI == BEPI_SPLIT) {
+                // a lane's 16 columns lie on one side of the split (split % 16 == 0)
+                const bool lo_side = k0 < G.split;
+                Op zh, zl;
+                for (int i = 0; i < 4; ++i) { zh.d[i] = 0u; zl.d[i] = 0u; }
+                const Op& ah = lo_side ? xh : zh;
+                const Op& al = lo_side ? xl : zl;
+                const Op& bh = lo_side ? zh : xh;
+                const Op& bl = lo_side ? zl : xl;
+                ch[0] = mfma(ah, w, ch[0]);
+                cl[0] = mfma(al, w, cl[0]);
+                ch[NA - 1] = mfma(bh, w, ch[NA - 1]);
+                cl[NA - 1] = mfma(bl, w, cl[NA - 1]);
+                if (lo_side) wsum[0] += ws; else wsum[NA - 1] += ws;
+            } else {
+                ch[0] = mfma(xh, w, ch[0]);
+                cl[0] = mfma(xl, w, cl[0]);
+                wsum[0] += ws;
+                if (EPI == BEPI_GATE) {
+                    ch[NA - 1] = mfma(xh, w3, ch[NA - 1]);
+                    cl[NA - 1] = mfma(xl, w3, cl[NA - 1]);
+                    wsum[NA - 1] += ws3;
+                }
+            }
+        } else {
+            // one step = one 32-column group g = s: D = sum n*x exactly, then
+            // the shader's fp32 term (s16*ps)*D + (m16*ps)*X, summed in double
+            const i32x16 zero = {};
+            const int xg = xs + __shfl_xor(xs, 32, 64);  // token li's group sum (both halves)
+            const int nmat = EPI == BEPI_GATE ? 2 : 1;
+            const int side = (EPI == BEPI_SPLIT && s * kTile >= G.split) ? 1 : 0;
+#pragma unroll
+            for (int mm = 0; mm < nmat; ++mm) {
+                const Op& wv = mm == 0 ? w : w3;
+                const MatDev& MM = mm == 0 ? M : G.M3;
+                const float pss = mm == 0 ? ps : ps3;
+                const i32x16 dh = mfma(xh, wv, zero);
+                const i32x16 dl = mfma(xl, wv, zero);
+                const int wl = mm == 0 ? ws : ws3;
+                const int wg = wl + __shfl_xor(wl, 32, 64);
+                const uint32_t sm = nok ? MM.sm[(size_t)n * (K >> 5) + s] : 0u;
+                const float sa = (float)(int16_t)(sm & 0xFFFFu) * pss;
+                const float ma = (float)(int16_t)(sm >> 16) * pss;
+                const int slot = EPI == BEPI_GATE ? mm : side;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = 8 * (r >> 2) + 4 * half + (r & 3);
+                    const int X = __shfl(xg, m, 64);
+                    const long long D = 256LL * dh[r] + (long long)dl[r] + 128LL * wg;
+                    const float t1 = sa * (float)D;
+                    const float t2 = ma * (float)X;
+                    const float tt = t1 + t2;
+                    dacc[slot][r] += (double)tt;
+                }
+            }
+        }
+    }
+
+    // epilogue: this lane holds column n for 16 token rows
+    int wtot[NA];
+#pragma unroll
+    for (int a = 0; a < NA; ++a) wtot[a] = wsum[a] + __shfl_xor(wsum[a], 32, 64);
+    const float wsr = (KIND != VGX_Q4 && nok) ? M.wsr[n] : 0.0f;
+    const float wsr3 = (KIND != VGX_Q4 && EPI == BEPI_GATE && nok) ? G.M3.wsr[n] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int m = 8 * (r >> 2) + 4 * half + (r & 3);
+        const int tt = t0 + m;
+        if (!nok || tt >= G.ntok) continue;
+        float v[NA];
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+            if (KIND == VGX_Q4) {
+                v[a] = (float)dacc[a][r];
+            } else {
+                const long long S = 256LL * ch[a][r] + (long long)cl[a][r] + 128LL * wtot[a];
+                const float sc = (EPI == BEPI_GATE && a == 1) ? wsr3 : wsr;
+                v[a] = (float)S * sc;
+            }
+        }
+        int16_t* yo = G.y + (size_t)tt * G.ldy + n;
+        if (EPI == BEPI_STORE) {
+            const float o = G.res ? v[0] + (float)G.res[(size_t)tt * G.ldy + n] : v[0];
+            *yo = (int16_t)q16_round(o);
+        } else if (EPI == BEPI_SPLIT) {
+            const float y1 = (float)q16_round(v[0] + (float)G.res[(size_t)tt * G.ldy + n]);
+            *yo = (int16_t)q16_round(v[NA - 1] + y1);
+        } else {
+            *yo = (int16_t)q16_round(gate_value(v[0], v[NA - 1], G.hs));
+        }
+    }
+}
+
+using GemmFn = void (*)(const GemmLaunch);
+
+template <int EPI>
+GemmFn pick(int kind) {
+    switch (kind) {
+        case VGX_Q8: return gemm_kernel<VGX_Q8, EPI>;
+        case VGX_Q4: return gemm_kernel<VGX_Q4, EPI>;
+        case VGX_T3: return gemm_kernel<VGX_T3, EPI>;
+    }
+    return nullptr;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int launch(vgx_ctx* ctx, const vgx_mat* W, const vgx_mat* W3, int ntok, const int16_t* x, const int16_t* res,
+           int16_t* y, int epi, int hs, int split, const char* who) {
+    if (!ctx || !W || !x || !y) return vgx_fail(VGX_EINVAL, std::string(who) + ": NULL argument");
+    if (ntok <= 0 || ntok > 65535 * kTile) return vgx_fail(VGX_EINVAL, std::string(who) + ": ntok outside 1..2097120");
+    if (!aligned16(x)) return vgx_fail(VGX_EINVAL, std::string(who) + ": x must be 16-byte aligned");
+    const MatDev& M = W->d;
+    if (M.kind == VGX_Q8 && M.cols % 16)
+        return vgx_fail(VGX_EINVAL, std::string(who) + ": q8 cols must be a multiple of 16");
+    VGX_HIP(hipSetDevice(ctx->device));
+    GemmLaunch L{};
+    L.M = M;
+    if (W3) L.M3 = W3->d;
+    L.ntok = ntok;
+    L.cols = M.cols;
+    L.x = x;
+    L.ldx = M.cols;
+    L.res = res;
+    L.y = y;
+    L.ldy = M.rows;
+    L.hs = hs;
+    L.split = split;
+    GemmFn fn = epi == BEPI_STORE ? pick<BEPI_STORE>(M.kind)
+              : epi == BEPI_GATE ? pick<BEPI_GATE>(M.kind) : pick<BEPI_SPLIT>(M.kind);
+    if (!fn) return vgx_fail(VGX_EINVAL, std::string(who) + ": unknown weight kind");
+    const dim3 grid((M.rows + kWaves * kTile - 1) / (kWaves * kTile), (ntok + kTile - 1) / kTile);
+    hipLaunchKernelGGL(fn, grid, dim3(kThreads), 0, ctx->stream, L);
+    VGX_LAUNCH_CHECK("gemm launch");
+    return VGX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int vgx_gemm(vgx_ctx* ctx, const vgx_mat* W, int ntok, const int16_t* x, const int16_t* res, int16_t* y) {
+    return launch(ctx, W, nullptr, ntok, x, res, y, BEPI_STORE, 0, 0, "vgx_gemm");
+}
+
+int vgx_gemm_add_split(vgx_ctx* ctx, const vgx_mat* W, int split, int ntok, const int16_t* x, const int16_t* res,
+                       int16_t* y) {
+    if (!W || !res) return vgx_fail(VGX_EINVAL, "vgx_gemm_add_split: NULL argument");
+    const int unit = W->d.kind == VGX_Q8 ? 16 : 32;
+    if (split <= 0 || split >= W->d.cols || split % unit)
+        return vgx_fail(VGX_EINVAL, "vgx_gemm_add_split: split must be inside cols and a multiple of " +
+                                        std::to_string(unit));
+    return launch(ctx, W, nullptr, ntok, x, res, y, BEPI_SPLIT, 0, split, "vgx_gemm_add_split");
+}
+
+int vgx_ffn_gate_batch(vgx_ctx* ctx, const vgx_mat* W1, const vgx_mat* W3, int ntok, const int16_t* x, int hs,
+                       int16_t* h) {
+    if (!W1 || !W3) return vgx_fail(VGX_EINVAL, "vgx_ffn_gate_batch: NULL matrix");
+    if (W1->d.kind != W3->d.kind || W1->d.rows != W3->d.rows || W1->d.cols != W3->d.cols)
+        return vgx_fail(VGX_EINVAL, "vgx_ffn_gate_batch: W1 and W3 differ in kind or shape");
+    if (hs < 0 || hs > 5) return vgx_fail(VGX_EINVAL, "vgx_ffn_gate_batch: hs outside 0..5");
+    return launch(ctx, W1, W3, ntok, x, nullptr, h, BEPI_GATE, hs, 0, "vgx_ffn_gate_batch");
+}
+
+}  // extern "C"

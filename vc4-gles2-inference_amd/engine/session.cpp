@@ -46,6 +46,10 @@ struct vgx_engine {
     int16_t *logits = nullptr, *rms_final = nullptr;
     int* toks = nullptr;  // device token slots: [0, seq) prompt/decode history, [seq] the host step's
     int seq = 0, kv_bits = 16, ffn_chunk = 0;
+    // batched prefill: row buffers for up to pcap positions; prompts run in
+    // batches of pbatch (serial steps when pbatch < 2)
+    int pcap = 0, pbatch = 0;
+    int16_t *bh = nullptr, *bx1 = nullptr, *bxn = nullptr, *bqkv = nullptr, *batt = nullptr, *bhid = nullptr;
     std::vector<void*> allocs;
 
     ~vgx_engine() {
@@ -230,6 +234,12 @@ struct vgx_engine {
             (st = dalloc(&qkv, qkv_rows)) || (st = dalloc(&hbuf, m.hidden)) ||
             (st = dalloc(&logits, (size_t)m.vocab)) || (st = dalloc(&toks, (size_t)seq + 1)))
             return st;
+        pcap = seq < 512 ? seq : 512;
+        pbatch = pcap;
+        const size_t P = (size_t)pcap;
+        if ((st = dalloc(&bh, P * D)) || (st = dalloc(&bx1, P * D)) || (st = dalloc(&bxn, P * D)) ||
+            (st = dalloc(&batt, P * D)) || (st = dalloc(&bqkv, P * qkv_rows)) || (st = dalloc(&bhid, P * m.hidden)))
+            return st;
         hipError_t he = hipDeviceSynchronize();
         return he == hipSuccess ? VGX_OK : fail(VGX_EHIP, hipGetErrorString(he));
     }
@@ -257,6 +267,51 @@ struct vgx_engine {
         }
         if (!want_logits) return VGX_OK;
         return vgx_logits_argmax_rms(ctx, head, h, rms_final, eps, logits, next_dev);
+    }
+
+    // Batched prefill of positions pos0 .. pos0+n-1 (Session::step_group,
+    // engine/src/session.cpp:1741-1795): the same layer sequence as forward()
+    // over n rows at once -- GEMMs on the int8 matrix cores, the KV rows of all
+    // n positions appended before any of them attends.  Every row is the exact
+    // result of forward() on that position, so the logits of the last one are
+    // identical to the serial loop's.
+    int prefill(const int* toks_dev, int pos0, int n, bool want_logits, int* next_dev) {
+        int st;
+        const int D = m.dim;
+        const float eps = m.rms_eps;
+        if (n <= 0 || n > pcap) return fail(VGX_EINVAL, "prefill: batch outside 1.." + std::to_string(pcap));
+        if ((st = vgx_embed_q8_batch(ctx, emb, emb_scale, m.vocab, D, n, toks_dev, bh))) return st;
+        for (int l = 0; l < m.layers; ++l) {
+            Layer& ly = L[l];
+            if ((st = vgx_rmsnorm_batch(ctx, n, D, bh, ly.rms_att, eps, bxn))) return st;
+            if ((st = vgx_gemm(ctx, ly.qkv, n, bxn, nullptr, bqkv))) return st;
+            if ((st = vgx_kv_append_batch(attn, l, pos0, n, bqkv))) return st;
+            if ((st = vgx_attn_decode_batch(attn, l, pos0, n, bqkv, batt))) return st;
+            if ((st = vgx_gemm(ctx, ly.wo, n, batt, bh, bx1))) return st;
+            if ((st = vgx_rmsnorm_batch(ctx, n, D, bx1, ly.rms_ffn, eps, bxn))) return st;
+            if ((st = vgx_ffn_gate_batch(ctx, ly.w1, ly.w3, n, bxn, ly.hs, bhid))) return st;
+            if (ffn_chunk) st = vgx_gemm_add_split(ctx, ly.w2, ffn_chunk, n, bhid, bx1, bh);
+            else st = vgx_gemm(ctx, ly.w2, n, bhid, bx1, bh);
+            if (st) return st;
+        }
+        if (!want_logits) return VGX_OK;
+        return vgx_logits_argmax_rms(ctx, head, bh + (size_t)(n - 1) * D, rms_final, eps, logits, next_dev);
+    }
+
+    // The prompt tokens at toks_dev[0..n) for positions pos0.., in batches of
+    // up to pbatch (one position at a time when pbatch < 2).
+    int run_prompt(const int* toks_dev, int pos0, int n, int* next_dev) {
+        int st;
+        if (pbatch < 2) {
+            for (int p = 0; p < n; ++p)
+                if ((st = forward(toks_dev + p, pos0 + p, p == n - 1, next_dev))) return st;
+            return VGX_OK;
+        }
+        for (int p = 0; p < n; p += pbatch) {
+            const int b = n - p < pbatch ? n - p : pbatch;
+            if ((st = prefill(toks_dev + p, pos0 + p, b, p + b == n, next_dev))) return st;
+        }
+        return VGX_OK;
     }
 };
 
@@ -343,8 +398,7 @@ int vgx_engine_generate(vgx_engine* e, const int* prompt, int n_prompt, int n_ge
     if (hipDeviceSynchronize() != hipSuccess) return fail(VGX_EHIP, "sync");
     auto t0 = std::chrono::steady_clock::now();
     int st;
-    for (int p = 0; p < n_prompt; ++p)
-        if ((st = e->forward(e->toks + p, p, p == n_prompt - 1, gen))) return st;
+    if ((st = e->run_prompt(e->toks, 0, n_prompt, gen))) return st;
     if (hipStreamSynchronize(s) != hipSuccess) return fail(VGX_EHIP, "prefill sync");
     auto t1 = std::chrono::steady_clock::now();
     for (int i = 1; i < n_gen; ++i)
@@ -355,6 +409,38 @@ int vgx_engine_generate(vgx_engine* e, const int* prompt, int n_prompt, int n_ge
         return fail(VGX_EHIP, "token readback");
     if (prefill_ms) *prefill_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
     if (decode_ms) *decode_ms = std::chrono::duration<double, std::milli>(t2 - t1).count();
+    return VGX_OK;
+}
+
+int vgx_engine_set_prefill_batch(vgx_engine* e, int n) {
+    g_err.clear();
+    if (!e) return fail(VGX_EINVAL, "vgx_engine_set_prefill_batch: NULL engine");
+    if (n < 0 || n > e->pcap)
+        return fail(VGX_EINVAL, "vgx_engine_set_prefill_batch: batch outside 0.." + std::to_string(e->pcap));
+    e->pbatch = n;
+    return VGX_OK;
+}
+
+int vgx_engine_prefill(vgx_engine* e, const int* tokens, int n, int pos0, int16_t* logits_host, int* next) {
+    g_err.clear();
+    if (!e || !tokens) return fail(VGX_EINVAL, "vgx_engine_prefill: NULL argument");
+    if (n <= 0 || pos0 < 0 || pos0 > e->seq - n)
+        return fail(VGX_ERANGE, "vgx_engine_prefill: positions outside the KV length");
+    for (int i = 0; i < n; ++i)
+        if (tokens[i] < 0 || tokens[i] >= e->m.vocab) return fail(VGX_EINVAL, "vgx_engine_prefill: token outside the vocabulary");
+    hipStream_t s = static_cast<hipStream_t>(vgx_ctx_stream(e->ctx));
+    int* dst = e->toks + pos0;
+    int* slot = e->toks + e->seq;
+    if (hipMemcpyAsync(dst, tokens, (size_t)n * sizeof(int), hipMemcpyHostToDevice, s) != hipSuccess)
+        return fail(VGX_EHIP, "token upload");
+    int st = e->run_prompt(dst, pos0, n, slot);
+    if (st) return st;
+    if (logits_host && hipMemcpyAsync(logits_host, e->logits, (size_t)e->m.vocab * 2, hipMemcpyDeviceToHost, s) != hipSuccess)
+        return fail(VGX_EHIP, "logits readback");
+    int nx = 0;
+    if (hipMemcpyAsync(&nx, slot, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess) return fail(VGX_EHIP, "token readback");
+    if (hipStreamSynchronize(s) != hipSuccess) return fail(VGX_EHIP, "prefill sync");
+    if (next) *next = nx;
     return VGX_OK;
 }
 

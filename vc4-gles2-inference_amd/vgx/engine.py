@@ -19,6 +19,8 @@ _SIGS = {
     "vgx_engine_step": (_I, [_P, _I, _I, _P, ctypes.POINTER(_I)]),
     "vgx_engine_generate": (_I, [_P, _P, _I, _I, _P, ctypes.POINTER(ctypes.c_double),
                                  ctypes.POINTER(ctypes.c_double)]),
+    "vgx_engine_prefill": (_I, [_P, _P, _I, _I, _P, ctypes.POINTER(_I)]),
+    "vgx_engine_set_prefill_batch": (_I, [_P, _I]),
     "vgx_engine_last_error": (ctypes.c_char_p, []),
 }
 _lib = None
@@ -71,6 +73,19 @@ class Engine:
         _check(load().vgx_engine_step(self.h, int(token), int(pos),
                                       ctypes.c_void_p(out.ctypes.data if logits else 0), ctypes.byref(nx)))
         return out, nx.value
+
+    def prefill(self, tokens, pos0=0, logits=True):
+        """Positions pos0.. of `tokens` in batches; the last one's logits and argmax."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        out = np.empty(self.vocab, np.int16) if logits else None
+        nx = ctypes.c_int()
+        _check(load().vgx_engine_prefill(self.h, t.ctypes.data, t.size, int(pos0),
+                                         ctypes.c_void_p(out.ctypes.data if logits else 0), ctypes.byref(nx)))
+        return out, nx.value
+
+    def set_prefill_batch(self, n):
+        """Largest prompt batch (0 or 1: one position at a time)."""
+        _check(load().vgx_engine_set_prefill_batch(self.h, int(n)))
 
     def generate(self, prompt, n_gen):
         p = np.ascontiguousarray(prompt, np.int32)

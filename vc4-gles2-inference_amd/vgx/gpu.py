@@ -128,6 +128,16 @@ class Attention:
         _l.check(_l.load().vgx_attn_block(self.h, layer, pos, _ptr(qkv), _ptr(out)))
         return out
 
+    def block_batch(self, layer, pos0, qkv, out=None):
+        """Positions pos0 .. pos0 + n - 1 for the n rows of qkv: the KV rows
+        are appended first, then every position attends to its prefix."""
+        n = qkv.shape[0]
+        out = out if out is not None else torch.empty((n, self.dim), dtype=torch.int16, device=qkv.device)
+        L = _l.load()
+        _l.check(L.vgx_kv_append_batch(self.h, layer, pos0, n, _ptr(qkv)))
+        _l.check(L.vgx_attn_decode_batch(self.h, layer, pos0, n, _ptr(qkv), _ptr(out)))
+        return out
+
     def read_rows(self, layer, row0, nrows):
         buf = np.empty(nrows * self.row_bytes, np.uint8)
         _l.check(_l.load().vgx_kv_read_rows(self.h, layer, row0, nrows, _np_ptr(buf)))
@@ -222,6 +232,39 @@ class GPU:
     def rmsnorm(self, x, w, eps=1e-5, out=None):
         out = out if out is not None else torch.empty_like(x)
         _l.check(_l.load().vgx_rmsnorm(self.ctx, x.numel(), _ptr(x), _ptr(w), float(eps), _ptr(out)))
+        return out
+
+    # -- batched prefill: x is (ntok, cols), outputs (ntok, rows)
+    def gemm(self, mat, x, res=None, out=None):
+        n = x.shape[0]
+        out = out if out is not None else torch.empty((n, mat.rows), dtype=torch.int16, device=x.device)
+        _l.check(_l.load().vgx_gemm(self.ctx, mat.h, n, _ptr(x), _ptr(res), _ptr(out)))
+        return out
+
+    def gemm_add_split(self, mat, split, x, res, out=None):
+        n = x.shape[0]
+        out = out if out is not None else torch.empty((n, mat.rows), dtype=torch.int16, device=x.device)
+        _l.check(_l.load().vgx_gemm_add_split(self.ctx, mat.h, split, n, _ptr(x), _ptr(res), _ptr(out)))
+        return out
+
+    def ffn_gate_batch(self, w1, w3, x, hs=0, out=None):
+        n = x.shape[0]
+        out = out if out is not None else torch.empty((n, w1.rows), dtype=torch.int16, device=x.device)
+        _l.check(_l.load().vgx_ffn_gate_batch(self.ctx, w1.h, w3.h, n, _ptr(x), hs, _ptr(out)))
+        return out
+
+    def rmsnorm_batch(self, x, w, eps=1e-5, out=None):
+        out = out if out is not None else torch.empty_like(x)
+        _l.check(_l.load().vgx_rmsnorm_batch(self.ctx, x.shape[0], x.shape[1], _ptr(x), _ptr(w), float(eps),
+                                             _ptr(out)))
+        return out
+
+    def embed_q8_batch(self, emb, emb_scale, tokens, out=None):
+        vocab, dim = emb.shape
+        n = tokens.numel()
+        out = out if out is not None else torch.empty((n, dim), dtype=torch.int16, device=emb.device)
+        _l.check(_l.load().vgx_embed_q8_batch(self.ctx, _ptr(emb), _ptr(emb_scale), vocab, dim, n, _ptr(tokens),
+                                              _ptr(out)))
         return out
 
     def matvec_rms(self, mat, x, rms_w, eps=1e-5, res=None, out=None):

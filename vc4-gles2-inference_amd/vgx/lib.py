@@ -69,6 +69,13 @@ _SIGS = {
     "vgx_ffn_gate_rms": (_I, [_P, _P, _P, _P, _P, ctypes.c_float, _I, _P]),
     "vgx_gemv_group_rms": (_I, [_P, _P, _P, _P, ctypes.c_float, _P]),
     "vgx_logits_argmax_rms": (_I, [_P, _P, _P, _P, ctypes.c_float, _P, _P]),
+    "vgx_gemm": (_I, [_P, _P, _I, _P, _P, _P]),
+    "vgx_gemm_add_split": (_I, [_P, _P, _I, _I, _P, _P, _P]),
+    "vgx_ffn_gate_batch": (_I, [_P, _P, _P, _I, _P, _I, _P]),
+    "vgx_rmsnorm_batch": (_I, [_P, _I, _I, _P, _P, ctypes.c_float, _P]),
+    "vgx_embed_q8_batch": (_I, [_P, _P, _P, _I, _I, _I, _P, _P]),
+    "vgx_kv_append_batch": (_I, [_P, _I, _I, _I, _P]),
+    "vgx_attn_decode_batch": (_I, [_P, _I, _I, _I, _P, _P]),
     "vgx_embed_q8": (_I, [_P, _P, _P, _I, _I, _P, _P]),
     "vgx_attn_create": (_I, [_P, ctypes.POINTER(AttnDesc), ctypes.POINTER(_P)]),
     "vgx_attn_free": (_I, [_P]),
