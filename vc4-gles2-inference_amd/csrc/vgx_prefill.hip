@@ -18,8 +18,10 @@
 // so  sum w*x = 256*sum w*xh + sum w*(xl - 128) + 128*sum w, every term an
 // exact integer (|partial| <= 128*128*K < 2^31 for K <= 32768).
 //
-// A wave owns a 32-token x 32-row output tile; a workgroup is 4 waves over 128
-// consecutive weight rows.  Epilogues restate the batch-1 GEMV's fp32
+// A workgroup owns a 32-token x 32-row output tile; its 4 waves take a
+// contiguous quarter of the k-steps each, load each step's operands one step
+// ahead, and wave 0 adds the other waves' partial sums (exact integers; for
+// q4 doubles, in wave order) before the epilogue.  Epilogues restate the batch-1 GEMV's fp32
 // expressions: q16 store (+ residual, one rounding), the SwiGLU gate over W1
 // and W3, and the two-half residual add of the split w2.  q4 applies its
 // per-group fp32 terms after each 32-column group (one MFMA k-step = one
@@ -166,11 +168,20 @@ __device__ __forceinline__ float gate_value(float v1, float v3, int hs) {
 
 template <int KIND, int EPI>
 __global__ void __launch_bounds__(kThreads) gemm_kernel(const GemmLaunch G) {
+    constexpr int NA = EPI == BEPI_STORE ? 1 : 2;  // accumulator sets: W1/W3 or the two halves
+    // Waves 1..3 hand their partial sums to wave 0 through LDS, lane-major:
+    // q8/t3 [wave-1][set][ch 0..15, cl 0..15][lane] int32 plus the weight
+    // sums; q4 [wave-1][set][r][lane] double.
+    constexpr int kRedInts = (kWaves - 1) * NA * 32 * 64 + (kWaves - 1) * NA * 64;
+    constexpr int kRedBytes = KIND == VGX_Q4 ? (kWaves - 1) * NA * 16 * 64 * 8 : kRedInts * 4;
+    __shared__ __align__(16) unsigned char s_red[kRedBytes];
+    __shared__ int s_xg[kWaves][kTile];  // q4: this step's group sum of x per token
+
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int half = lane >> 5;
     const int li = lane & 31;
-    const int n0 = (blockIdx.x * kWaves + wave) * kTile;
+    const int n0 = blockIdx.x * kTile;
     const int t0 = blockIdx.y * kTile;
     const int K = G.cols;
     const MatDev& M = G.M;
@@ -180,7 +191,9 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(const GemmLaunch G) {
     const bool tok = t < G.ntok;
     const int16_t* xrow = G.x + (size_t)(tok ? t : 0) * G.ldx;
     const int nsteps = (K + kTile - 1) / kTile;
-    constexpr int NA = EPI == BEPI_STORE ? 1 : 2;  // accumulator sets: W1/W3 or the two halves
+    // the four waves of a workgroup share one 32 x 32 output tile and take a
+    // contiguous quarter of the k-steps each
+    const int s_beg = (nsteps * wave) / kWaves, s_end = (nsteps * (wave + 1)) / kWaves;
 
     i32x16 ch[NA], cl[NA];
     double dacc[NA][16];
@@ -195,69 +208,133 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(const GemmLaunch G) {
     }
     const float ps = M.ps, ps3 = G.M3.ps;
 
-    for (int s = 0; s < nsteps; ++s) {
+    // a step's operands, loaded one step ahead of the multiply
+    struct Ops {
+        Op xh, xl, w, w3;
+        int xs, ws, ws3;
+        uint32_t sm, sm3;
+    };
+    auto load = [&](int s, Ops& o) {
         const int k0 = s * kTile + half * 16;
         const bool kok = k0 < K;
-        Op xh, xl, w, w3;
-        int xs, ws, ws3 = 0;
-        x_operands(xrow, k0, tok && kok, xh, xl, xs);
-        w_operand<KIND>(M, n, k0, K, nok && kok, w, ws);
-        if (EPI == BEPI_GATE) w_operand<KIND>(G.M3, n, k0, K, nok && kok, w3, ws3);
+        x_operands(xrow, k0, tok && kok, o.xh, o.xl, o.xs);
+        w_operand<KIND>(M, n, k0, K, nok && kok, o.w, o.ws);
+        o.ws3 = 0;
+        if (EPI == BEPI_GATE) w_operand<KIND>(G.M3, n, k0, K, nok && kok, o.w3, o.ws3);
+        if (KIND == VGX_Q4) {
+            o.sm = nok ? M.sm[(size_t)n * (K >> 5) + s] : 0u;
+            o.sm3 = (EPI == BEPI_GATE && nok) ? G.M3.sm[(size_t)n * (K >> 5) + s] : 0u;
+        }
+    };
+    Ops cur;
+    if (s_beg < s_end) load(s_beg, cur);
+    for (int s = s_beg; s < s_end; ++s) {
+        Ops nxt;
+        const bool more = s + 1 < s_end;
+        if (more) load(s + 1, nxt);
+        const int k0 = s * kTile + half * 16;
         if (KIND != VGX_Q4) {
             if (EPI == BEPI_SPLIT) {
                 // a lane's 16 columns lie on one side of the split (split % 16 == 0)
                 const bool lo_side = k0 < G.split;
                 Op zh, zl;
                 for (int i = 0; i < 4; ++i) { zh.d[i] = 0u; zl.d[i] = 0u; }
-                const Op& ah = lo_side ? xh : zh;
-                const Op& al = lo_side ? xl : zl;
-                const Op& bh = lo_side ? zh : xh;
-                const Op& bl = lo_side ? zl : xl;
-                ch[0] = mfma(ah, w, ch[0]);
-                cl[0] = mfma(al, w, cl[0]);
-                ch[NA - 1] = mfma(bh, w, ch[NA - 1]);
-                cl[NA - 1] = mfma(bl, w, cl[NA - 1]);
-                if (lo_side) wsum[0] += ws; else wsum[NA - 1] += ws;
+                ch[0] = mfma(lo_side ? cur.xh : zh, cur.w, ch[0]);
+                cl[0] = mfma(lo_side ? cur.xl : zl, cur.w, cl[0]);
+                ch[NA - 1] = mfma(lo_side ? zh : cur.xh, cur.w, ch[NA - 1]);
+                cl[NA - 1] = mfma(lo_side ? zl : cur.xl, cur.w, cl[NA - 1]);
+                if (lo_side) wsum[0] += cur.ws; else wsum[NA - 1] += cur.ws;
             } else {
-                ch[0] = mfma(xh, w, ch[0]);
-                cl[0] = mfma(xl, w, cl[0]);
-                wsum[0] += ws;
+                ch[0] = mfma(cur.xh, cur.w, ch[0]);
+                cl[0] = mfma(cur.xl, cur.w, cl[0]);
+                wsum[0] += cur.ws;
                 if (EPI == BEPI_GATE) {
-                    ch[NA - 1] = mfma(xh, w3, ch[NA - 1]);
-                    cl[NA - 1] = mfma(xl, w3, cl[NA - 1]);
-                    wsum[NA - 1] += ws3;
+                    ch[NA - 1] = mfma(cur.xh, cur.w3, ch[NA - 1]);
+                    cl[NA - 1] = mfma(cur.xl, cur.w3, cl[NA - 1]);
+                    wsum[NA - 1] += cur.ws3;
                 }
             }
         } else {
-            // one step = one 32-column group g = s: D = sum n*x exactly, then
-            // the shader's fp32 term (s16*ps)*D + (m16*ps)*X, summed in double
+            // one step = one 32-column group g = s: D = sum n*x exactly (|D| <
+            // 2^24), then the shader's fp32 term (s16*ps)*D + (m16*ps)*X,
+            // summed in double
             const i32x16 zero = {};
-            const int xg = xs + __shfl_xor(xs, 32, 64);  // token li's group sum (both halves)
+            const int xg = cur.xs + __shfl_xor(cur.xs, 32, 64);  // token li's group sum
+            if (half == 0) s_xg[wave][li] = xg;
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            int X[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) X[r] = s_xg[wave][8 * (r >> 2) + 4 * half + (r & 3)];
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
             const int nmat = EPI == BEPI_GATE ? 2 : 1;
             const int side = (EPI == BEPI_SPLIT && s * kTile >= G.split) ? 1 : 0;
 #pragma unroll
             for (int mm = 0; mm < nmat; ++mm) {
-                const Op& wv = mm == 0 ? w : w3;
-                const MatDev& MM = mm == 0 ? M : G.M3;
+                const Op& wv = mm == 0 ? cur.w : cur.w3;
                 const float pss = mm == 0 ? ps : ps3;
-                const i32x16 dh = mfma(xh, wv, zero);
-                const i32x16 dl = mfma(xl, wv, zero);
-                const int wl = mm == 0 ? ws : ws3;
+                const i32x16 dh = mfma(cur.xh, wv, zero);
+                const i32x16 dl = mfma(cur.xl, wv, zero);
+                const int wl = mm == 0 ? cur.ws : cur.ws3;
                 const int wg = wl + __shfl_xor(wl, 32, 64);
-                const uint32_t sm = nok ? MM.sm[(size_t)n * (K >> 5) + s] : 0u;
+                const uint32_t sm = mm == 0 ? cur.sm : cur.sm3;
                 const float sa = (float)(int16_t)(sm & 0xFFFFu) * pss;
                 const float ma = (float)(int16_t)(sm >> 16) * pss;
                 const int slot = EPI == BEPI_GATE ? mm : side;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int m = 8 * (r >> 2) + 4 * half + (r & 3);
-                    const int X = __shfl(xg, m, 64);
-                    const long long D = 256LL * dh[r] + (long long)dl[r] + 128LL * wg;
+                    const int D = 256 * dh[r] + dl[r] + 128 * wg;
                     const float t1 = sa * (float)D;
-                    const float t2 = ma * (float)X;
+                    const float t2 = ma * (float)X[r];
                     const float tt = t1 + t2;
                     dacc[slot][r] += (double)tt;
                 }
+            }
+        }
+        if (more) cur = nxt;
+    }
+
+    // waves 1..3 hand over; wave 0 adds the partials in wave order and stores
+    if (wave > 0) {
+        if (KIND == VGX_Q4) {
+            double* p = reinterpret_cast<double*>(s_red) + (size_t)(wave - 1) * NA * 16 * 64;
+#pragma unroll
+            for (int a = 0; a < NA; ++a)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) p[(a * 16 + r) * 64 + lane] = dacc[a][r];
+        } else {
+            int* p = reinterpret_cast<int*>(s_red) + (size_t)(wave - 1) * NA * 32 * 64;
+            int* pw = reinterpret_cast<int*>(s_red) + (size_t)(kWaves - 1) * NA * 32 * 64 + (wave - 1) * NA * 64;
+#pragma unroll
+            for (int a = 0; a < NA; ++a) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    p[(a * 32 + r) * 64 + lane] = ch[a][r];
+                    p[(a * 32 + 16 + r) * 64 + lane] = cl[a][r];
+                }
+                pw[a * 64 + lane] = wsum[a];
+            }
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    for (int wv = 1; wv < kWaves; ++wv) {
+        if (KIND == VGX_Q4) {
+            const double* p = reinterpret_cast<const double*>(s_red) + (size_t)(wv - 1) * NA * 16 * 64;
+#pragma unroll
+            for (int a = 0; a < NA; ++a)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) dacc[a][r] += p[(a * 16 + r) * 64 + lane];
+        } else {
+            const int* p = reinterpret_cast<const int*>(s_red) + (size_t)(wv - 1) * NA * 32 * 64;
+            const int* pw = reinterpret_cast<const int*>(s_red) + (size_t)(kWaves - 1) * NA * 32 * 64 + (wv - 1) * NA * 64;
+#pragma unroll
+            for (int a = 0; a < NA; ++a) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    ch[a][r] += p[(a * 32 + r) * 64 + lane];
+                    cl[a][r] += p[(a * 32 + 16 + r) * 64 + lane];
+                }
+                wsum[a] += pw[a * 64 + lane];
             }
         }
     }
@@ -335,7 +412,7 @@ int launch(vgx_ctx* ctx, const vgx_mat* W, const vgx_mat* W3, int ntok, const in
     GemmFn fn = epi == BEPI_STORE ? pick<BEPI_STORE>(M.kind)
               : epi == BEPI_GATE ? pick<BEPI_GATE>(M.kind) : pick<BEPI_SPLIT>(M.kind);
     if (!fn) return vgx_fail(VGX_EINVAL, std::string(who) + ": unknown weight kind");
-    const dim3 grid((M.rows + kWaves * kTile - 1) / (kWaves * kTile), (ntok + kTile - 1) / kTile);
+    const dim3 grid((M.rows + kTile - 1) / kTile, (ntok + kTile - 1) / kTile);
     hipLaunchKernelGGL(fn, grid, dim3(kThreads), 0, ctx->stream, L);
     VGX_LAUNCH_CHECK("gemm launch");
     return VGX_OK;
