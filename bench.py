@@ -142,30 +142,53 @@ def cpu_baseline(seconds):
                       "%.1f s, oracle exact-integer q8 GEMV with OpenMP" % (passes, dt)}
 
 
-def decode_bench(runs):
-    """MiniMind3-64M q8 (per-row scales), KV q16, SEQ 256: 32 prompt tokens
-    then 64 greedy tokens through the engine; decode tokens/s over the 63
-    steps after the prompt, median of `runs` after one warm-up run."""
+def model_decode(name, spec, scheme, kv_bits, n_prompt, n_gen, runs):
+    """A seeded synthetic model through the engine: n_prompt prompt tokens
+    (batched prefill) then n_gen greedy tokens; decode tokens/s over the
+    n_gen - 1 steps after the prompt, median of `runs` after a warm-up run."""
     import numpy as np
     from vgx import synth
     from vgx.engine import Engine
 
-    spec = synth.minimind3_spec(seq=256)
-    blob = synth.container(spec, "q8", seed=0, q8_row=True)
-    prompt = synth.prompt(32, spec.vocab, seed=0)
-    eng = Engine(blob, kv_bits=16)
-    eng.generate(prompt, 64)
+    blob = synth.container(spec, scheme, seed=0, q8_row=True)
+    prompt = synth.prompt(n_prompt, spec.vocab, seed=0)
+    eng = Engine(blob, kv_bits=kv_bits)
+    eng.generate(prompt, n_gen)
     pf, dc, toks = [], [], None
     for _ in range(runs):
-        toks, p, d = eng.generate(prompt, 64)
+        toks, p, d = eng.generate(prompt, n_gen)
         pf.append(p)
         dc.append(d)
     eng.close()
-    ms_tok = float(np.median(dc)) / 63
+    ms_tok = float(np.median(dc)) / (n_gen - 1)
     return blob, prompt, toks, {
-        "model": "MiniMind3-64M-shaped, q8 per-row, seed 0", "prompt": 32, "gen": 64, "seq": 256, "kv": "q16",
+        "model": name, "prompt": n_prompt, "gen": n_gen, "seq": spec.seq, "kv": "q%d" % kv_bits,
         "tokens_per_s": round(1000.0 / ms_tok, 1), "ms_per_token": round(ms_tok, 4),
         "prefill_ms": round(float(np.median(pf)), 3), "runs": runs}
+
+
+def decode_bench(runs):
+    """C1: MiniMind3-64M q8 (per-row scales), KV q16, SEQ 256, 32 prompt
+    tokens then 64 greedy tokens."""
+    from vgx import synth
+    return model_decode("MiniMind3-64M-shaped, q8 per-row, seed 0", synth.minimind3_spec(seq=256), "q8", 16,
+                        32, 64, runs)
+
+
+def hybrid_decode_bench(runs):
+    """C4: LFM2.5-230M-shaped hybrid q8 (8 conv + 6 attention layers), KV q16,
+    SEQ 256, 64 prompt tokens then 128 greedy tokens."""
+    from vgx import synth
+    return model_decode("LFM2.5-230M-shaped hybrid, q8 per-row, seed 0", synth.lfm2_spec(seq=256), "q8", 16,
+                        64, 128, runs)
+
+
+def ternary_decode_bench(runs):
+    """C5 at batch 1: the 0.5B Llama-shaped ternary (t3) body, KV q16, SEQ 512,
+    128 prompt tokens then 256 greedy tokens."""
+    from vgx import synth
+    return model_decode("0.5B Llama-shaped t3 (per-row ternary P(0)=0.4), seed 0", synth.bitcpm_spec(seq=512),
+                        "t3", 16, 128, 256, runs)
 
 
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 matrix-core peak, TOPS
@@ -246,7 +269,7 @@ def decode_cpu_baseline(blob, prompt, steps):
         f.step(int(prompt[pos % len(prompt)]), pos)
     dt = time.perf_counter() - t0
     return {"tokens_per_s": round(steps / dt, 2), "cores": o.threads(),
-            "sample": "%d positions of the float path (numpy fp32 BLAS, dequantised q8 weights)" % steps}
+            "sample": "%d positions of the float path (numpy fp32 BLAS, dequantised container weights)" % steps}
 
 
 def main():
@@ -262,10 +285,11 @@ def main():
     ap.add_argument("--skip-decode", action="store_true")
     ap.add_argument("--copy-mb", type=int, default=0, help="also time a device copy of this many MiB")
     ap.add_argument("--cpu-decode-steps", type=int, default=16)
-    ap.add_argument("--only", choices=["gemv", "decode", "prefill"], default=None,
+    ap.add_argument("--only", choices=["gemv", "decode", "prefill", "hybrid", "ternary"], default=None,
                     help="run one leg (for profiling); the JSON line then carries that leg only")
     ap.add_argument("--prefill-runs", type=int, default=5)
     ap.add_argument("--skip-prefill", action="store_true")
+    ap.add_argument("--skip-models", action="store_true", help="skip the C4 hybrid and C5 ternary decode legs")
     ap.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "BENCH_LOG"),
                     help="print the HBM traffic summary of two rocprofv3 --pmc runs and exit (no GPU)")
     args = ap.parse_args()
@@ -283,8 +307,12 @@ def main():
     if args.only == "prefill":
         print(json.dumps({"prefill": prefill_bench(args.prefill_runs)}))
         return
+    if args.only in ("hybrid", "ternary"):
+        fn = hybrid_decode_bench if args.only == "hybrid" else ternary_decode_bench
+        print(json.dumps({args.only: fn(args.decode_runs)[3]}))
+        return
     if args.only == "gemv":
-        args.skip_decode, args.no_cpu, args.skip_prefill = True, True, True
+        args.skip_decode, args.no_cpu, args.skip_prefill, args.skip_models = True, True, True, True
 
     import numpy as np
     import torch
@@ -406,10 +434,18 @@ def main():
         out["decode_tokens_per_s"] = dec["tokens_per_s"]
     if not args.skip_prefill:
         out["prefill"] = prefill_bench(args.prefill_runs)
+    others = []
+    if not args.skip_models:
+        others = [("decode_c4", hybrid_decode_bench(args.decode_runs), 8),
+                  ("decode_c5_batch1", ternary_decode_bench(args.decode_runs), 4)]
+        for key, (_b, _p, _t, res), _n in others:
+            out[key] = res
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
         if not args.skip_decode:
             out["decode"]["cpu_float_path"] = decode_cpu_baseline(blob, prompt, args.cpu_decode_steps)
+        for key, (b, p, _t, _r), n in others:
+            out[key]["cpu_float_path"] = decode_cpu_baseline(b, p, n)
     print(json.dumps(out))
 
 

@@ -48,6 +48,7 @@ typedef struct vgx_ctx vgx_ctx;
 typedef struct vgx_mat vgx_mat;
 typedef struct vgx_group vgx_group;
 typedef struct vgx_attn vgx_attn;
+typedef struct vgx_conv vgx_conv;
 
 int vgx_abi_version(void);
 const char* vgx_strerror(int status);
@@ -228,6 +229,29 @@ int vgx_attn_block(vgx_attn* a, int layer, int pos, const int16_t* qkv, int16_t*
  * rows of dim + 2*kv_dim, out ntok rows of dim.  Append all rows first. */
 int vgx_kv_append_batch(vgx_attn* a, int layer, int pos0, int ntok, const int16_t* qkv);
 int vgx_attn_decode_batch(vgx_attn* a, int layer, int pos0, int ntok, const int16_t* qkv, int16_t* out);
+
+/* ---- LFM2 gated short convolution: replaces GPU::init_conv, set_conv_kernel,
+ * conv_block's gate/conv3/gate passes and clear_conv_state
+ * (engine/src/gpu_conv.cpp:10-225), between the in_proj GEMV (3*dim rows:
+ * B, C, x) and the out_proj GEMV.
+ * vgx_conv_create: w = host f32 [layers][dim][kernel] (the container's
+ *   depthwise kernel records, engine/src/model.cpp:1143-1158), kernel must be
+ *   3; layer_is_conv = host [layers] (key 14) or NULL = every layer.
+ * vgx_conv_step: positions in order, ntok of them: bcx = ntok rows of 3*dim
+ *   q16 (the in_proj output), y = ntok rows of dim q16; the per-layer state
+ *   (the last two gated vectors) advances by ntok.
+ * vgx_conv_reset: every layer's state to zero (Session::zero_conv_state,
+ *   engine/src/session.cpp:320-325).
+ * vgx_conv_state_read / write: one layer's state, 2*dim int16 (the gated
+ *   vectors of positions pos-2 and pos-1), what the prefix cache persists for
+ *   a hybrid model (read_conv_state / write_conv_state, gpu_conv.cpp:24-58). */
+int vgx_conv_create(vgx_ctx* ctx, int dim, int layers, int kernel, const float* w, const uint8_t* layer_is_conv,
+                    vgx_conv** out);
+int vgx_conv_free(vgx_conv* c);
+int vgx_conv_reset(vgx_conv* c);
+int vgx_conv_step(vgx_conv* c, int layer, int ntok, const int16_t* bcx, int16_t* y);
+int vgx_conv_state_read(vgx_conv* c, int layer, int16_t* host);
+int vgx_conv_state_write(vgx_conv* c, int layer, const int16_t* host);
 /* The packed KV rows in the reference's texel byte layout (K values then V
  * values; q16 big-endian, q8 two's-complement bytes) -- what MMKV1 persists
  * (engine/src/prefix_cache.cpp:59-67).  Host buffers; these block. */

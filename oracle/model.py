@@ -93,9 +93,18 @@ class _Base:
         self.kv_dim = self.kv_heads * self.hd
         self.kv_bits = kv_bits
         self.chunk = (self.hidden + 1) // 2 if self.hidden > 2048 else 0
+        # key 14: nonzero = an LFM2 conv layer (in_proj 0x17, f32 depthwise
+        # kernel 0x18, out_proj 0x19; engine/src/model.cpp:1142-1160)
+        self.is_conv = list(meta.get(14, b"")) or [0] * self.layers
+        self.conv_w = [None] * self.layers
         self.mats = []
         for l in range(self.layers):
-            L = {"qkv": self.mat(0x10, l), "wo": self.mat(0x11, l)}
+            if self.is_conv[l]:
+                L = {"conv_in": self.mat(0x17, l), "conv_out": self.mat(0x19, l)}
+                _dt, rows, cols, _s, body = self.recs[0x18 | l << 8]
+                self.conv_w[l] = body.view(np.float32).reshape(rows, cols)
+            else:
+                L = {"qkv": self.mat(0x10, l), "wo": self.mat(0x11, l)}
             if (0x14 | l << 8) in self.recs:
                 w13 = self.mat(0x14, l)
                 L["w1"], L["w3"] = self.rows_of(w13, 0, self.hidden), self.rows_of(w13, self.hidden, 2 * self.hidden)
@@ -170,15 +179,26 @@ class QModel(_Base):
         if self.chunk:
             self.w2ab = [(L["w2"].cols_slice(0, self.chunk), L["w2"].cols_slice(self.chunk, self.hidden))
                          for L in self.mats]
+        self.taps = [o.conv_taps(w) if w is not None else None for w in self.conv_w]
+        self.conv_state = [np.zeros((2, self.dim), np.int16) for _ in range(self.layers)]
 
     def step(self, token, pos, want_logits=True):
+        if pos == 0:  # a new sequence starts with an empty conv history
+            for st in self.conv_state:
+                st[:] = 0
         h = o.embed_q8(self.emb, self.es, token)
         for l, L in enumerate(self.mats):
             xb = o.rmsnorm(h, self.w_att[l], self.eps)
-            qkv = o.store(L["qkv"].rowval(xb))
-            att = o.attn_block(self.cfg, qkv, self.qnq[l] if self.qnq else None,
-                               self.knq[l] if self.knq else None, self.rtab, pos, self.kv[l])
-            x1 = o.store(L["wo"].rowval(att), h)
+            if self.is_conv[l]:
+                # GPU::conv_block (engine/src/gpu_conv.cpp:165-225)
+                bcx = o.store(L["conv_in"].rowval(xb))
+                y = o.conv_step(bcx, self.taps[l], self.conv_state[l])
+                x1 = o.store(L["conv_out"].rowval(y), h)
+            else:
+                qkv = o.store(L["qkv"].rowval(xb))
+                att = o.attn_block(self.cfg, qkv, self.qnq[l] if self.qnq else None,
+                                   self.knq[l] if self.knq else None, self.rtab, pos, self.kv[l])
+                x1 = o.store(L["wo"].rowval(att), h)
             xb = o.rmsnorm(x1, self.w_ffn[l], self.eps)
             hb = o.gate(L["w1"].rowval(xb), L["w3"].rowval(xb), self.hid[l])
             if self.chunk:
@@ -208,6 +228,7 @@ class FModel(_Base):
         self.head = np.concatenate([t.dequant() for t in self.tiles])
         self.kc = np.zeros((self.layers, self.seq, self.kv_heads, self.hd), np.float32)
         self.vc = np.zeros_like(self.kc)
+        self.cstate = np.zeros((self.layers, 2, self.dim), np.float32)  # B*x of pos-2, pos-1
 
     def _rope(self, x, pos):
         c, s = self.rcos[pos], self.rsin[pos]
@@ -223,10 +244,32 @@ class FModel(_Base):
     def _rms(x, w, eps):
         return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps) * w
 
+    def _conv(self, l, W, xn):
+        """LFM2 ShortConv in float: B, C, x = in_proj(xn); Bx = B*x; a causal
+        depthwise conv over the last three Bx (tap 0 on pos-2); C * conv;
+        out_proj (the CPU form of Session, engine/src/session.cpp:383-418,
+        without its q16 stores)."""
+        bcx = W["conv_in"] @ xn
+        b, c, xx = bcx[:self.dim], bcx[self.dim:2 * self.dim], bcx[2 * self.dim:]
+        bx = b * xx
+        w = self.conv_w[l]
+        st = self.cstate[l]
+        cv = w[:, 0] * st[0] + w[:, 1] * st[1] + w[:, 2] * bx
+        st[0], st[1] = st[1], bx
+        return W["conv_out"] @ (c * cv)
+
     def step(self, token, pos):
+        if pos == 0:
+            self.cstate[:] = 0
         x = self.emb[token].astype(np.float32) * self.es[token]
         for l, W in enumerate(self.W):
             xn = self._rms(x, self.rms_att[l], self.eps)
+            if self.is_conv[l]:
+                x = x + self._conv(l, W, xn)
+                xn = self._rms(x, self.rms_ffn[l], self.eps)
+                g, u = W["w1"] @ xn, W["w3"] @ xn
+                x = x + W["w2"] @ ((g / (1 + np.exp(-g))) * u)
+                continue
             qkv = W["qkv"] @ xn
             q = qkv[:self.dim].reshape(self.heads, self.hd)
             k = qkv[self.dim:self.dim + self.kv_dim].reshape(self.kv_heads, self.hd)

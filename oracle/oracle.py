@@ -78,6 +78,8 @@ def _load():
         "vgxo_attn_block": (None, [ctypes.POINTER(AttnCfg), _c_i16, _vp, _vp, _c_i32, _i, _c_u8, _c_i16]),
         "vgxo_kv_decode": (_f, [ctypes.POINTER(AttnCfg), _c_u8, _i]),
         "vgxo_embed_q8": (None, [_c_i8, _c_f32, _i, _i, _c_i16]),
+        "vgxo_conv_taps": (None, [_c_f32, _i, _i, _c_i16]),
+        "vgxo_conv_step": (None, [_i, _c_i16, _c_i16, _c_i16, _c_i16, _c_i16]),
         "vgxo_argmax_i16": (_i, [_c_i16, _i]),
         "vgxo_matvec_f32": (None, [_c_f32, _i, _i, _c_f32, _c_f32]),
         "vgxo_rms_f32": (None, [_c_f32, _vp, _i, _f, _c_f32]),
@@ -366,6 +368,28 @@ def attn_parts(cfg, qrot, kv, pos):
 
 
 # ---- embedding / argmax / float path ------------------------------------------------
+def conv_taps(w):
+    """q16 taps [k][dim] of an f32 depthwise kernel w [dim][k]."""
+    w = _c(w, np.float32)
+    dim, k = w.shape
+    out = np.empty((k, dim), np.int16)
+    lib.vgxo_conv_taps(w, dim, k, out)
+    return out
+
+
+def conv_step(bcx, taps, state):
+    """One position of the conv block: bcx [3*dim] q16, taps [3][dim] q16,
+    state [2][dim] q16 (gated values of pos-2, pos-1; updated in place).
+    Returns y [dim] q16."""
+    dim = taps.shape[1]
+    if state.dtype != np.int16 or not state.flags["C_CONTIGUOUS"] or state.shape != (2, dim):
+        raise ValueError("state must be a contiguous int16 [2][dim] array")
+    y = np.empty(dim, np.int16)
+    s2, s1 = state[0], state[1]
+    lib.vgxo_conv_step(dim, _c(bcx, np.int16), _c(taps, np.int16), s2, s1, y)
+    return y
+
+
 def embed_q8(emb, emb_scale, token):
     emb = _c(emb, np.int8)
     out = np.empty(emb.shape[1], np.int16)

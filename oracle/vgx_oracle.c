@@ -804,6 +804,40 @@ void vgxo_attn_block(const vgxo_attn_cfg* c, const int16_t* qkv, const int16_t* 
 }
 
 /* ======================================================================
+ * LFM2 conv block (GPU::conv_block, engine/src/gpu_conv.cpp:165-225)
+ * ====================================================================== */
+
+/* GPU::set_conv_kernel (engine/src/gpu_conv.cpp:84-101): the f32 depthwise
+ * kernel w[i*k + t] as q16 taps lrintf(w*256), clamped; taps[t*dim + i]. */
+void vgxo_conv_taps(const float* w, int dim, int k, int16_t* taps) {
+    for (int t = 0; t < k; ++t)
+        for (int i = 0; i < dim; ++i) taps[(size_t)t * dim + i] = vgxo_quantize_act(w[(size_t)i * k + t]);
+}
+
+/* One position of the conv block after in_proj.  bcx = the q16 in_proj
+ * output (matvec_to stores x_i24encq, which clamps to the q16 range,
+ * engine/src/shaders.cpp:61; rows B, C, x in that order, model.cpp:1314-1316);
+ * s2 / s1 = the gated values of positions pos-2 / pos-1 (q16), updated in
+ * place; y = the q16 input of out_proj.  Per channel:
+ *   gated = x_st2(b/256 * x/256)                        (mul_act, shaders.cpp:2011)
+ *   cv    = x_st2q(((k0*s2 + k1*s1) + k2*gated) * 2^-8) (conv3_act, :2025-2051;
+ *           every operand in q16 units, fp32, left to right)
+ *   y     = x_st2(c/256 * cv/256)                       (mul_act) */
+void vgxo_conv_step(int dim, const int16_t* bcx, const int16_t* taps, int16_t* s2, int16_t* s1, int16_t* y) {
+    for (int i = 0; i < dim; ++i) {
+        const float bv = (float)bcx[i] / 256.0f, cvv = (float)bcx[dim + i] / 256.0f;
+        const float xv = (float)bcx[2 * dim + i] / 256.0f;
+        const int16_t g = vgxo_q16_store(bv * xv);
+        const float k0 = (float)taps[i], k1 = (float)taps[dim + i], k2 = (float)taps[2 * dim + i];
+        const float acc = ((k0 * (float)s2[i] + k1 * (float)s1[i]) + k2 * (float)g) * 0.00390625f;
+        const int16_t cq = vgxo_q16_round(acc);
+        y[i] = vgxo_q16_store(cvv * ((float)cq / 256.0f));
+        s2[i] = s1[i];
+        s1[i] = g;
+    }
+}
+
+/* ======================================================================
  * Embedding, argmax
  * ====================================================================== */
 

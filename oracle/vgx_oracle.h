@@ -104,6 +104,10 @@ void vgxo_attn_block(const vgxo_attn_cfg* c, const int16_t* qkv, const int16_t* 
                      const int32_t* rtab, int pos, uint8_t* kv, int16_t* out);
 float vgxo_kv_decode(const vgxo_attn_cfg* c, const uint8_t* row, int idx);
 
+/* ---- LFM2 conv block (engine/src/gpu_conv.cpp:165-225) -------------------- */
+void vgxo_conv_taps(const float* w, int dim, int k, int16_t* taps);
+void vgxo_conv_step(int dim, const int16_t* bcx, const int16_t* taps, int16_t* s2, int16_t* s1, int16_t* y);
+
 /* ---- embedding and argmax (engine/src/session.cpp:342-371, sampling.cpp) -- */
 void vgxo_embed_q8(const int8_t* emb, const float* emb_scale, int dim, int token, int16_t* x);
 int vgxo_argmax_i16(const int16_t* v, int n);

@@ -151,6 +151,89 @@ def test_minimind3_q4_prefill_256_kv8(gpu):
     b.close()
 
 
+@pytest.mark.parametrize("scheme", ["q8", "q4", "t3"])
+def test_hybrid_engine_bit_exact(gpu, scheme):
+    """An LFM2-structured hybrid (conv, attn, conv): every step's logits equal
+    the oracle's, and a batched prompt equals the serial loop."""
+    spec = synth.tiny_hybrid_spec(seq=48, hidden=2112 if scheme != "t3" else 96)
+    w = (synth.ternary_weights if scheme == "t3" else synth.dense_weights)(spec, seed=6)
+    if scheme == "t3":
+        rng = np.random.default_rng(6)
+        w["conv_w"] = [rng.standard_normal((spec.dim, 3)).astype(np.float32) * np.float32(0.5)
+                       if t == "conv" else None for t in spec.layer_types]
+        w["conv_in"] = [synth.ternary_matrix(rng, 3 * spec.dim, spec.dim) if t == "conv" else None
+                        for t in spec.layer_types]
+        w["conv_out"] = [synth.ternary_matrix(rng, spec.dim, spec.dim) if t == "conv" else None
+                         for t in spec.layer_types]
+    else:
+        w = synth.dense_weights(spec, seed=6, std=0.05, conv_std=0.5)
+    blob = synth.container(spec, scheme, weights=w)
+    ref, eng = QModel(blob), Engine(blob)
+    prompt = synth.prompt(7, spec.vocab, seed=2)
+    tok = None
+    for pos in range(16):
+        t = int(prompt[pos]) if pos < len(prompt) else tok
+        want = ref.step(t, pos)
+        got, nxt = eng.step(t, pos)
+        assert np.array_equal(got, want), (scheme, pos)
+        tok = nxt
+    # a new sequence at position 0 starts from an empty conv history
+    got, _ = eng.step(int(prompt[0]), 0)
+    assert np.array_equal(got, QModel(blob).step(int(prompt[0]), 0))
+    eng.close()
+    a, b = Engine(blob), Engine(blob)
+    b.set_prefill_batch(0)
+    la, ta = a.prefill(prompt)
+    lb, tb = b.prefill(prompt)
+    assert np.array_equal(la, lb) and ta == tb
+    la, _ = a.step(ta, len(prompt))
+    lb, _ = b.step(tb, len(prompt))
+    assert np.array_equal(la, lb)
+    a.close()
+    b.close()
+
+
+def test_lfm2_230m_shape(gpu):
+    """The C4 shape (LFM2.5-230M-shaped q8: 8 conv + 6 attention layers, dim
+    1024, vocab 64402): bit-exact against the oracle over a batched prompt and
+    greedy steps, and within the stated tolerance of the float path.
+
+    The tolerance for this shape: max |logit difference| <= 1.5 and mean <=
+    0.25 (the float logits' std is 0.64), and at every step the q16 path's
+    greedy token within the float path's top 64 of 64402.  The gap is the
+    reference's own q16 activation grid on a residual of order 0.02 over 14
+    layers, which the reference documents for LFM2.5 (2-3 significant bits per
+    component after the embedding, engine/src/session.cpp:328-333); measured
+    on seed 0: max 0.78-1.18, mean 0.14-0.21, ranks 0-52."""
+    spec = synth.lfm2_spec(seq=256)
+    blob = synth.container(spec, "q8", seed=0, q8_row=True)
+    prompt = synth.prompt(6, spec.vocab, seed=4)
+    eng = Engine(blob)
+    ref, f = QModel(blob), FModel(blob)
+    got, tok = eng.prefill(prompt)
+    for pos in range(len(prompt)):
+        lq = ref.step(int(prompt[pos]), pos, want_logits=pos == len(prompt) - 1)
+        lf = f.step(int(prompt[pos]), pos)
+    assert np.array_equal(got, lq)
+
+    def gap(lq, lf):
+        d = np.abs(lq / 256.0 - lf)
+        rank = int((lf > lf[int(np.argmax(lq))]).sum())
+        return d.max(), d.mean(), rank
+
+    gaps = [gap(lq, lf)]
+    for pos in range(len(prompt), len(prompt) + 4):
+        got, nxt = eng.step(tok, pos)
+        lq, lf = ref.step(tok, pos), f.step(tok, pos)
+        assert np.array_equal(got, lq), pos
+        gaps.append(gap(lq, lf))
+        tok = nxt
+    assert max(g[0] for g in gaps) <= 1.5, gaps
+    assert max(g[1] for g in gaps) <= 0.25, gaps
+    assert max(g[2] for g in gaps) < 64, gaps
+    eng.close()
+
+
 def test_engine_refusals(gpu):
     from vgx import lib as vl
     spec = synth.tiny_spec(seq=8)

@@ -305,6 +305,60 @@ def test_attention_relative_position_invariance():
         assert np.max(np.abs(s - base)) <= 3
 
 
+def test_conv_taps_grid():
+    # set_conv_kernel (engine/src/gpu_conv.cpp:84-101): lrintf(w*256), the
+    # int16 rail, tap-major from the channel-major f32 kernel
+    rng = np.random.default_rng(12)
+    w = (rng.standard_normal((40, 3)) * 0.7).astype(np.float32)
+    w[0, 0], w[1, 1], w[2, 2], w[3, 0] = 200.0, 2.5 / 256, 3.5 / 256, -200.0
+    taps = o.conv_taps(w)
+    assert taps.shape == (3, 40)
+    want = np.clip(np.rint(w.T * np.float32(256)), -32768, 32767)
+    assert np.array_equal(taps, want)
+    assert (taps[0, 0], taps[1, 1], taps[2, 2], taps[0, 3]) == (32767, 2, 4, -32768)  # half-even ties
+
+
+def _conv_run(taps, xs, b=256, c=256):
+    dim = taps.shape[1]
+    state = np.zeros((2, dim), np.int16)
+    ys = []
+    for x in xs:
+        bcx = np.concatenate([np.full(dim, b), np.full(dim, c), x]).astype(np.int16)
+        ys.append(o.conv_step(bcx, taps, state))
+    return np.array(ys, np.int64), state
+
+
+def test_conv_step_closed_forms():
+    # With B = C = 1.0 the two gates pass x and cv through unchanged, so the
+    # block is the causal depthwise convolution itself: taps (0, 0, 1) give
+    # y_t = x_t, (0, 1, 0) y_t = x_{t-1}, (1, 0, 0) y_t = x_{t-2} (zero
+    # history), and integer taps give the exact integer convolution
+    # (conv3_act's operand order: tap 0 on pos-2, tap 2 on pos; Session's CPU
+    # form engine/src/session.cpp:394-401 has the same order).
+    rng = np.random.default_rng(13)
+    dim, T = 64, 9
+    xs = [rng.integers(-3000, 3001, dim).astype(np.int16) for _ in range(T)]
+    X = np.array(xs, np.int64)
+    Z = np.zeros((2, dim), np.int64)
+    Xp = np.concatenate([Z, X])  # Xp[t + 2] = x_t
+    for tap, shift in ((2, 0), (1, 1), (0, 2)):
+        taps = np.zeros((3, dim), np.int16)
+        taps[tap] = 256
+        y, st = _conv_run(taps, xs)
+        assert np.array_equal(y, Xp[2 - shift:2 - shift + T]), tap
+        assert np.array_equal(st, X[-2:])  # the state holds the last two gated values
+    a = rng.integers(-2, 3, (3, dim))
+    y, _ = _conv_run((a * 256).astype(np.int16), xs)
+    want = a[0] * Xp[0:T] + a[1] * Xp[1:T + 1] + a[2] * Xp[2:T + 2]
+    assert np.array_equal(y, np.clip(want, -32768, 32767))
+    # B = 2.0 doubles the gated value up to the int16 rail
+    taps = np.zeros((3, dim), np.int16)
+    taps[2] = 256
+    big = [np.full(dim, 20000, np.int16), np.full(dim, -100, np.int16)]
+    y, _ = _conv_run(taps, big, b=512)
+    assert (y[0] == 32767).all() and (y[1] == -200).all()
+
+
 def test_embed_and_argmax():
     rng = np.random.default_rng(11)
     emb = rng.integers(-127, 128, (10, 16)).astype(np.int8)

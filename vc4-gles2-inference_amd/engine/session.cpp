@@ -32,8 +32,10 @@ struct vgx_engine {
     vgxe::ModelMeta m;
     vgx_ctx* ctx = nullptr;
     vgx_attn* attn = nullptr;
+    vgx_conv* conv = nullptr;  // LFM2 conv-layer state (hybrid models only)
     struct Layer {
         vgx_mat *qkv = nullptr, *wo = nullptr, *w1 = nullptr, *w3 = nullptr, *w2 = nullptr;
+        vgx_mat *conv_in = nullptr, *conv_out = nullptr;  // conv layers instead of qkv / wo
         int16_t *rms_att = nullptr, *rms_ffn = nullptr;
         int hs = 0;
     };
@@ -55,10 +57,12 @@ struct vgx_engine {
     ~vgx_engine() {
         for (auto& l : L) {
             vgx_mat_free(l.qkv); vgx_mat_free(l.wo); vgx_mat_free(l.w1); vgx_mat_free(l.w3); vgx_mat_free(l.w2);
+            vgx_mat_free(l.conv_in); vgx_mat_free(l.conv_out);
         }
         vgx_group_free(head);
         for (vgx_mat* t : head_tiles) vgx_mat_free(t);
         vgx_attn_free(attn);
+        vgx_conv_free(conv);
         for (void* p : allocs) (void)hipFree(p);
         vgx_ctx_destroy(ctx);
     }
@@ -131,11 +135,12 @@ struct vgx_engine {
         return vgx_mat_upload(ctx, &d, out);
     }
 
+    bool is_conv(int l) const { return !m.layer_conv.empty() && m.layer_conv[l]; }
+
     int init(int device, int seq_req, int kv_req) {
         m = c.meta();
-        if (!m.layer_conv.empty())
-            for (uint8_t t : m.layer_conv)
-                if (t) return fail(VGX_EINVAL, "conv (hybrid) layers are not supported by this engine yet");
+        if (!m.layer_conv.empty() && (int)m.layer_conv.size() != m.layers)
+            return fail(VGX_EINVAL, "layer types (key 14) do not match the layer count");
         seq = seq_req > 0 ? seq_req : m.seq;
         kv_bits = kv_req;
         if (kv_bits != 16 && kv_bits != 8) return fail(VGX_EINVAL, "kv_bits must be 16 or 8");
@@ -151,11 +156,34 @@ struct vgx_engine {
         const vgxe::Record* rfin = c.find(vgxe::T_RMS_FINAL);
         if (ra->bytes != (uint64_t)m.layers * D * 4 || rf->bytes != ra->bytes || rfin->bytes != (uint64_t)D * 4)
             return fail(VGX_EINVAL, "rms weight shapes");
+        // LFM2 conv layers (key 14): in_proj 3*dim x dim, the f32 depthwise
+        // kernel dim x 3, out_proj dim x dim (engine/src/model.cpp:1142-1160,
+        // 1480-1500)
+        std::vector<float> conv_w;
+        std::vector<uint8_t> conv_flag((size_t)m.layers, 0);
+        bool hybrid = false;
         for (int l = 0; l < m.layers; ++l) {
             Layer& ly = L[l];
             ly.hs = m.hid_scale.empty() ? 0 : m.hid_scale[l];
-            if ((st = upload_mat(vgxe::T_QKV, l, 0, -1, 0.0f, &ly.qkv))) return st;
-            if ((st = upload_mat(vgxe::T_WO, l, 0, -1, 0.0f, &ly.wo))) return st;
+            if (is_conv(l)) {
+                const vgxe::Record* kw = c.find(vgxe::T_CONV_W, l);
+                if (!kw || kw->dtype != vgxe::DT_F32 || kw->rows != (uint32_t)D || kw->cols != 3)
+                    return fail(VGX_EINVAL, "layer " + std::to_string(l) + ": the conv kernel must be f32 dim x 3");
+                if ((st = upload_mat(vgxe::T_CONV_IN, l, 0, -1, 0.0f, &ly.conv_in))) return st;
+                if ((st = upload_mat(vgxe::T_CONV_OUT, l, 0, -1, 0.0f, &ly.conv_out))) return st;
+                int kind, rows, cols;
+                vgx_mat_shape(ly.conv_in, &kind, &rows, &cols);
+                if (rows != 3 * D || cols != D) return fail(VGX_EINVAL, "conv in_proj must be 3*dim x dim");
+                vgx_mat_shape(ly.conv_out, &kind, &rows, &cols);
+                if (rows != D || cols != D) return fail(VGX_EINVAL, "conv out_proj must be dim x dim");
+                conv_w.resize((size_t)m.layers * D * 3, 0.0f);
+                std::memcpy(conv_w.data() + (size_t)l * D * 3, kw->body, (size_t)D * 3 * 4);
+                conv_flag[l] = 1;
+                hybrid = true;
+            } else {
+                if ((st = upload_mat(vgxe::T_QKV, l, 0, -1, 0.0f, &ly.qkv))) return st;
+                if ((st = upload_mat(vgxe::T_WO, l, 0, -1, 0.0f, &ly.wo))) return st;
+            }
             if (c.find(vgxe::T_W13, l)) {
                 if ((st = upload_mat(vgxe::T_W13, l, 0, m.hidden, 0.0f, &ly.w1))) return st;
                 if ((st = upload_mat(vgxe::T_W13, l, m.hidden, 2 * m.hidden, 0.0f, &ly.w3))) return st;
@@ -173,6 +201,10 @@ struct vgx_engine {
         }
         vgx_quantize_act(reinterpret_cast<const float*>(rfin->body), D, q16.data());
         if ((st = upload(&rms_final, q16.data(), D))) return st;
+        if (hybrid) {
+            conv_w.resize((size_t)m.layers * D * 3, 0.0f);
+            if ((st = vgx_conv_create(ctx, D, m.layers, 3, conv_w.data(), conv_flag.data(), &conv))) return st;
+        }
         // embedding (signed q8 rows + f32 row scales)
         const vgxe::Record* e = c.find(vgxe::T_EMB);
         const vgxe::Record* es = c.find(vgxe::T_EMB_SCALE);
@@ -228,8 +260,12 @@ struct vgx_engine {
             ad.q_norm = reinterpret_cast<const float*>(qn->body);
             ad.k_norm = reinterpret_cast<const float*>(kn->body);
         }
+        std::vector<uint8_t> attn_flag((size_t)m.layers);
+        for (int l = 0; l < m.layers; ++l) attn_flag[l] = is_conv(l) ? 0 : 1;
+        ad.layer_is_attn = attn_flag.data();
         if ((st = vgx_attn_create(ctx, &ad, &attn))) return st;
-        const int qkv_rows = D + 2 * m.kv_dim();
+        // the qkv rows, or a conv layer's in_proj rows (B, C, x)
+        const int qkv_rows = D + 2 * m.kv_dim() > (hybrid ? 3 * D : 0) ? D + 2 * m.kv_dim() : 3 * D;
         if ((st = dalloc(&h, D)) || (st = dalloc(&x1, D)) || (st = dalloc(&att, D)) ||
             (st = dalloc(&qkv, qkv_rows)) || (st = dalloc(&hbuf, m.hidden)) ||
             (st = dalloc(&logits, (size_t)m.vocab)) || (st = dalloc(&toks, (size_t)seq + 1)))
@@ -254,12 +290,21 @@ struct vgx_engine {
         int st;
         const int D = m.dim;
         const float eps = m.rms_eps;
+        if (pos == 0 && conv && (st = vgx_conv_reset(conv))) return st;  // a new sequence
         if ((st = vgx_embed_q8(ctx, emb, emb_scale, m.vocab, D, token_dev, h))) return st;
         for (int l = 0; l < m.layers; ++l) {
             Layer& ly = L[l];
-            if ((st = vgx_gemv_rms(ctx, ly.qkv, h, ly.rms_att, eps, nullptr, qkv))) return st;
-            if ((st = vgx_attn_block(attn, l, pos, qkv, att))) return st;
-            if ((st = vgx_gemv(ctx, ly.wo, att, h, x1))) return st;
+            if (is_conv(l)) {
+                // GPU::conv_block (engine/src/gpu_conv.cpp:165-225): in_proj,
+                // the gated short conv, out_proj + residual
+                if ((st = vgx_gemv_rms(ctx, ly.conv_in, h, ly.rms_att, eps, nullptr, qkv))) return st;
+                if ((st = vgx_conv_step(conv, l, 1, qkv, att))) return st;
+                if ((st = vgx_gemv(ctx, ly.conv_out, att, h, x1))) return st;
+            } else {
+                if ((st = vgx_gemv_rms(ctx, ly.qkv, h, ly.rms_att, eps, nullptr, qkv))) return st;
+                if ((st = vgx_attn_block(attn, l, pos, qkv, att))) return st;
+                if ((st = vgx_gemv(ctx, ly.wo, att, h, x1))) return st;
+            }
             if ((st = vgx_ffn_gate_rms(ctx, ly.w1, ly.w3, x1, ly.rms_ffn, eps, ly.hs, hbuf))) return st;
             if (ffn_chunk) st = vgx_gemv_add_split(ctx, ly.w2, ffn_chunk, hbuf, x1, h);
             else st = vgx_gemv(ctx, ly.w2, hbuf, x1, h);
@@ -280,14 +325,22 @@ struct vgx_engine {
         const int D = m.dim;
         const float eps = m.rms_eps;
         if (n <= 0 || n > pcap) return fail(VGX_EINVAL, "prefill: batch outside 1.." + std::to_string(pcap));
+        if (pos0 == 0 && conv && (st = vgx_conv_reset(conv))) return st;  // a new sequence
         if ((st = vgx_embed_q8_batch(ctx, emb, emb_scale, m.vocab, D, n, toks_dev, bh))) return st;
         for (int l = 0; l < m.layers; ++l) {
             Layer& ly = L[l];
             if ((st = vgx_rmsnorm_batch(ctx, n, D, bh, ly.rms_att, eps, bxn))) return st;
-            if ((st = vgx_gemm(ctx, ly.qkv, n, bxn, nullptr, bqkv))) return st;
-            if ((st = vgx_kv_append_batch(attn, l, pos0, n, bqkv))) return st;
-            if ((st = vgx_attn_decode_batch(attn, l, pos0, n, bqkv, batt))) return st;
-            if ((st = vgx_gemm(ctx, ly.wo, n, batt, bh, bx1))) return st;
+            if (is_conv(l)) {
+                // the conv over the batch walks its positions in order
+                if ((st = vgx_gemm(ctx, ly.conv_in, n, bxn, nullptr, bqkv))) return st;
+                if ((st = vgx_conv_step(conv, l, n, bqkv, batt))) return st;
+                if ((st = vgx_gemm(ctx, ly.conv_out, n, batt, bh, bx1))) return st;
+            } else {
+                if ((st = vgx_gemm(ctx, ly.qkv, n, bxn, nullptr, bqkv))) return st;
+                if ((st = vgx_kv_append_batch(attn, l, pos0, n, bqkv))) return st;
+                if ((st = vgx_attn_decode_batch(attn, l, pos0, n, bqkv, batt))) return st;
+                if ((st = vgx_gemm(ctx, ly.wo, n, batt, bh, bx1))) return st;
+            }
             if ((st = vgx_rmsnorm_batch(ctx, n, D, bx1, ly.rms_ffn, eps, bxn))) return st;
             if ((st = vgx_ffn_gate_batch(ctx, ly.w1, ly.w3, n, bxn, ly.hs, bhid))) return st;
             if (ffn_chunk) st = vgx_gemm_add_split(ctx, ly.w2, ffn_chunk, n, bhid, bx1, bh);

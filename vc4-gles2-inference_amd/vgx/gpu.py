@@ -97,6 +97,51 @@ class Group:
             pass
 
 
+class Conv:
+    """LFM2 conv-block state and taps (GPU::init_conv / set_conv_kernel)."""
+
+    def __init__(self, gpu, w, layer_is_conv=None):
+        L = _l.load()
+        self._w = np.ascontiguousarray(w, np.float32)  # [layers][dim][3]
+        layers, dim, k = self._w.shape
+        self._types = None if layer_is_conv is None else np.ascontiguousarray(layer_is_conv, np.uint8)
+        h = ctypes.c_void_p()
+        _l.check(L.vgx_conv_create(gpu.ctx, dim, layers, k, _np_ptr(self._w), _np_ptr(self._types),
+                                   ctypes.byref(h)))
+        self.gpu, self.h, self.dim = gpu, h, dim
+
+    def step(self, layer, bcx, out=None):
+        """bcx: (ntok, 3*dim) or (3*dim,) q16; returns y of the same leading shape."""
+        n = 1 if bcx.dim() == 1 else bcx.shape[0]
+        shape = (self.dim,) if bcx.dim() == 1 else (n, self.dim)
+        out = out if out is not None else torch.empty(shape, dtype=torch.int16, device=bcx.device)
+        _l.check(_l.load().vgx_conv_step(self.h, layer, n, _ptr(bcx), _ptr(out)))
+        return out
+
+    def reset(self):
+        _l.check(_l.load().vgx_conv_reset(self.h))
+
+    def state(self, layer):
+        buf = np.empty((2, self.dim), np.int16)
+        _l.check(_l.load().vgx_conv_state_read(self.h, layer, _np_ptr(buf)))
+        return buf
+
+    def set_state(self, layer, st):
+        st = np.ascontiguousarray(st, np.int16)
+        _l.check(_l.load().vgx_conv_state_write(self.h, layer, _np_ptr(st)))
+
+    def free(self):
+        if self.h:
+            _l.load().vgx_conv_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 class Attention:
     """GPU::init_attention's state: KV cache, RoPE table, q/k norm weights."""
 
@@ -287,6 +332,9 @@ class GPU:
 
     def attention(self, **kw):
         return Attention(self, **kw)
+
+    def conv(self, w, layer_is_conv=None):
+        return Conv(self, w, layer_is_conv)
 
     def close(self):
         if self.ctx:

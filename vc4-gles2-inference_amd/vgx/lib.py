@@ -75,6 +75,12 @@ _SIGS = {
     "vgx_rmsnorm_batch": (_I, [_P, _I, _I, _P, _P, ctypes.c_float, _P]),
     "vgx_embed_q8_batch": (_I, [_P, _P, _P, _I, _I, _I, _P, _P]),
     "vgx_kv_append_batch": (_I, [_P, _I, _I, _I, _P]),
+    "vgx_conv_create": (_I, [_P, _I, _I, _I, _P, _P, ctypes.POINTER(_P)]),
+    "vgx_conv_free": (_I, [_P]),
+    "vgx_conv_reset": (_I, [_P]),
+    "vgx_conv_step": (_I, [_P, _I, _I, _P, _P]),
+    "vgx_conv_state_read": (_I, [_P, _I, _P]),
+    "vgx_conv_state_write": (_I, [_P, _I, _P]),
     "vgx_attn_decode_batch": (_I, [_P, _I, _I, _I, _P, _P]),
     "vgx_embed_q8": (_I, [_P, _P, _P, _I, _I, _P, _P]),
     "vgx_attn_create": (_I, [_P, ctypes.POINTER(AttnDesc), ctypes.POINTER(_P)]),

@@ -2,8 +2,9 @@
 
 There are no checkpoints to download: weights are random with the stated
 distribution from numpy's PCG64 (`default_rng(seed)`), float32, generated in a
-fixed order (embedding, then per layer wq, wk, wv, wo, w1, w3, w2), and packed
-by vgx.mmcf exactly as the reference packer would pack real float weights.
+fixed order (embedding, then per layer wq, wk, wv, wo -- or conv_in, the conv
+kernel, conv_out for a conv layer -- then w1, w3, w2), and packed by vgx.mmcf
+exactly as the reference packer would pack real float weights.
 """
 import numpy as np
 
@@ -30,21 +31,52 @@ def tiny_spec(seq=64, qk_norm=True, hidden=96):
                           theta=10000.0, rope_half=True, qk_norm=qk_norm)
 
 
-def dense_weights(spec, seed=0, std=0.02):
-    """N(0, std) projections and embedding, unit norm weights, tied head."""
+LFM2_LAYERS = ["conv", "conv", "attn", "conv", "conv", "attn", "conv", "attn",
+               "conv", "attn", "conv", "attn", "conv", "attn"]
+
+
+def lfm2_spec(seq=256):
+    """LFM2.5-230M-shaped hybrid: dim 1024, 8 gated short-conv layers (kernel 3)
+    interleaved with 6 GQA attention layers (16 Q / 8 KV heads of 64, per-head
+    q/k RMSNorm), SwiGLU 4608, vocab 64402, tied head, RoPE theta 1e6."""
+    return mmcf.ModelSpec(dim=1024, hidden=4608, layers=14, heads=16, kv_heads=8, vocab=64402, seq=seq,
+                          theta=1e6, rope_half=True, qk_norm=True, layer_types=list(LFM2_LAYERS))
+
+
+def tiny_hybrid_spec(seq=48, hidden=96):
+    """A small hybrid (conv, attn, conv) for fast parity tests."""
+    return mmcf.ModelSpec(dim=64, hidden=hidden, layers=3, heads=4, kv_heads=2, vocab=80, seq=seq,
+                          theta=10000.0, rope_half=True, qk_norm=True, layer_types=["conv", "attn", "conv"])
+
+
+def dense_weights(spec, seed=0, std=0.02, conv_std=None):
+    """N(0, std) projections and embedding, unit norm weights, tied head.
+    Per layer, in this order: wq, wk, wv, wo for an attention layer, or
+    conv_in (3*dim x dim), the depthwise kernel (dim x 3, N(0, conv_std),
+    default std) and conv_out for a conv layer; then w1, w3, w2."""
     rng = np.random.default_rng(seed)
 
-    def n(*shape):
-        return rng.standard_normal(shape, dtype=np.float32) * np.float32(std)
+    def n(*shape, s=std):
+        return rng.standard_normal(shape, dtype=np.float32) * np.float32(s)
 
     w = {"emb": n(spec.vocab, spec.dim)}
-    for k in ("wq", "wk", "wv", "wo", "w1", "w3", "w2"):
+    for k in ("wq", "wk", "wv", "wo", "w1", "w3", "w2", "conv_in", "conv_w", "conv_out"):
         w[k] = []
-    for _ in range(spec.layers):
-        w["wq"].append(n(spec.dim, spec.dim))
-        w["wk"].append(n(spec.kv_dim, spec.dim))
-        w["wv"].append(n(spec.kv_dim, spec.dim))
-        w["wo"].append(n(spec.dim, spec.dim))
+    types = spec.layer_types or ["attn"] * spec.layers
+    for l in range(spec.layers):
+        if types[l] == "conv":
+            for k in ("wq", "wk", "wv", "wo"):
+                w[k].append(None)
+            w["conv_in"].append(n(3 * spec.dim, spec.dim))
+            w["conv_w"].append(n(spec.dim, 3, s=std if conv_std is None else conv_std))
+            w["conv_out"].append(n(spec.dim, spec.dim))
+        else:
+            for k in ("conv_in", "conv_w", "conv_out"):
+                w[k].append(None)
+            w["wq"].append(n(spec.dim, spec.dim))
+            w["wk"].append(n(spec.kv_dim, spec.dim))
+            w["wv"].append(n(spec.kv_dim, spec.dim))
+            w["wo"].append(n(spec.dim, spec.dim))
         w["w1"].append(n(spec.hidden, spec.dim))
         w["w3"].append(n(spec.hidden, spec.dim))
         w["w2"].append(n(spec.dim, spec.hidden))
