@@ -81,3 +81,35 @@ def test_attention_range_errors(gpu):
     with pytest.raises(vl.VgxError):
         A.block(1, 0, qkv)  # no such layer
     A.free()
+
+
+@pytest.mark.parametrize("bits,hd", [(16, 256), (16, 64), (8, 256), (8, 96)])
+def test_attention_rails(gpu, bits, hd):
+    """Scores at the int16 / int8 rails: every cached K value at the grid's
+    minimum or maximum and the rotated query saturated, with head_dim up to
+    256 -- the widest exact integer sums the score dot product forms."""
+    heads, kvh, seq = 2, 1, 40
+    dim = heads * hd
+    rng = np.random.default_rng(bits * 1000 + hd)
+    rc, rs = o.rope_cos_sin(10000.0, hd, seq)
+    rtab = o.rope_table(rc, rs)
+    A = gpu.attention(dim=dim, heads=heads, kv_heads=kvh, head_dim=hd, seq=seq, layers=1, kv_bits=bits,
+                      rope_half=1, qk_norm=0, rope_cos=rc, rope_sin=rs)
+    c = o.attn_cfg(dim, heads, kvh, hd, seq, bits, 1, 0)
+    rb = o.kv_row_bytes(c)
+    n = 33
+    vals = rng.choice([-32768, 32767] if bits == 16 else [-128, 127], size=(n, rb // (bits // 8)))
+    if bits == 16:  # the texel layout: big-endian int16
+        rows = vals.astype(">i2").view(np.uint8).reshape(-1)
+    else:
+        rows = vals.astype(np.int8).view(np.uint8).reshape(-1)
+    kv = np.zeros(seq * rb, np.uint8)
+    kv[:n * rb] = rows
+    A.write_rows(0, 0, rows)
+    for pos in (n, n + 1):
+        qkv = rng.choice([-32768, 32767], size=dim + 2 * kvh * hd).astype(np.int16)
+        want = o.attn_block(c, qkv, None, None, rtab, pos, kv)
+        got = A.block(0, pos, dev(qkv))
+        torch.cuda.synchronize()
+        assert np.array_equal(got.cpu().numpy(), want), pos
+    A.free()

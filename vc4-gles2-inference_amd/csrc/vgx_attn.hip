@@ -1,12 +1,14 @@
 // Decode attention over the packed KV cache, with the KV pack (append).
 //
-// One workgroup of 1024 threads per KV head: it packs this position's K
-// (qk-norm, RoPE) and V into the layer's KV row, prepares the GROUP query
-// heads that read this KV head (q-norm factor on its 1/65536 grid, RoPE, q16),
-// scores every position 0..pos (exact integer dot products, 1/1024 grid), forms
-// the per-head (max, sum) statistics on their q16 grids and the weighted V sum.
-// Scores and exponentials run one (head, position) per thread; the K row of a
-// position is read as 16-byte vectors.  The two double-precision sums (sum of
+// One workgroup of 1024 threads per query head: it prepares the head's query
+// (q-norm factor on its 1/65536 grid, RoPE, q16), scores every position
+// 0..pos (exact integer dot products, 1/1024 grid), forms the (max, sum)
+// statistics on their q16 grids and the weighted V sum.  In a launch that also
+// appends, the first query head of each KV head's group packs this position's
+// K (qk-norm, RoPE) and V into the layer's KV row, and every head of the group
+// rebuilds the same packed values in LDS for its own position.  Scores and
+// exponentials run one position per thread; the K row of a position is read
+// as 16-byte vectors.  The two double-precision sums (sum of
 // exp, sum over t of p*v) use a fixed order -- chunks of kChunk positions,
 // each summed in position order, then the chunk sums in chunk order -- and the
 // oracle sums in the same order, so the output is reproducible bit for bit.
@@ -26,18 +28,26 @@
 
 namespace {
 
-constexpr int kThreads = 1024;
+constexpr int kThreads = 512;
 constexpr int kChunk = 32;  // positions per chunk of the summation order
+// 16-byte K vectors a lane holds for one scored position (int16 / int8 cache)
+template <int KVB>
+constexpr int kKPre = KVB == 16 ? 8 : 4;
+// 16-byte V vectors a thread stages per round (vR*vW <= kThreads words per
+// row position, kChunk positions per chunk)
+constexpr int kVPre = kChunk / 4;
 
 }  // namespace
 
 struct AttnDev {
     int dim, heads, kv_heads, hd, seq, kv_bits, rope_half, qk_norm, group;
     int row_bytes;
+    int lpp;     // lanes per scored position (a power of two)
+    int vW;      // 32-bit words per V row slice of one head
     int vR;      // chunks per round of the weighted-V pass
     int nchmax;  // chunks of a full cache
     // LDS byte offsets
-    int o_ssk, o_mx, o_invs, o_newk, o_newv, o_qrot, o_sc, o_ep, o_csum, o_vpart, o_acc;
+    int o_wmax, o_newv, o_kpk, o_qhw, o_qlw, o_sc, o_ep, o_csum, o_vpart, o_acc, o_vst;
 };
 
 struct vgx_attn {
@@ -96,49 +106,95 @@ __device__ __forceinline__ void rope_pair(int rope_half, int hd, int i, int& j, 
     }
 }
 
+typedef short short2_t __attribute__((ext_vector_type(2)));
+// A native 4-word vector: arrays of it stay in registers where arrays of the
+// HIP uint4 struct were demoted to scratch.
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ int lo16(unsigned w) { return (int)(short)(w & 0xffffu); }
 __device__ __forceinline__ int hi16(unsigned w) { return (int)w >> 16; }
 __device__ __forceinline__ int byte_s(unsigned w, int k) { return ((int)(w << (24 - 8 * k))) >> 24; }
 
-// Exact q . k over one head: q from LDS (int32 per element), k one cache row's
-// head slice read as 16-byte vectors (hd*KVB/8 bytes, 16-byte aligned).
+// The query split into bytes for the packed integer dot products: q = 256*qh
+// + ql with qh in [-128, 127] and ql in [0, 255].  Word w of qhw / qlw holds
+// the elements of K word w: two int16 halves (KVB 16) or four int8 bytes
+// (KVB 8, low byte stored as ql - 128).
 template <int KVB>
-__device__ __forceinline__ long long dot_row(const int* q, const uint8_t* k, int hd) {
-    const uint4* kv4 = reinterpret_cast<const uint4*>(k);
-    const int4* q4 = reinterpret_cast<const int4*>(q);
-    long long d = 0;
+__device__ __forceinline__ void q_split(int q, int i, int* qhw, int* qlw) {
+    const int qh = q >> 8, ql = q & 255;
     if (KVB == 16) {
-        const int nv = hd / 8;
-#pragma unroll 4
-        for (int v = 0; v < nv; ++v) {
-            const uint4 w = kv4[v];
-            const int4 a = q4[2 * v], b = q4[2 * v + 1];
-            d += (long long)a.x * lo16(w.x);
-            d += (long long)a.y * hi16(w.x);
-            d += (long long)a.z * lo16(w.y);
-            d += (long long)a.w * hi16(w.y);
-            d += (long long)b.x * lo16(w.z);
-            d += (long long)b.y * hi16(w.z);
-            d += (long long)b.z * lo16(w.w);
-            d += (long long)b.w * hi16(w.w);
-        }
+        reinterpret_cast<int16_t*>(qhw)[i] = (int16_t)qh;
+        reinterpret_cast<int16_t*>(qlw)[i] = (int16_t)ql;
     } else {
-        const int nv = hd / 16;
-#pragma unroll 2
-        for (int v = 0; v < nv; ++v) {
-            const uint4 w = kv4[v];
-            const unsigned ws[4] = {w.x, w.y, w.z, w.w};
+        reinterpret_cast<int8_t*>(qhw)[i] = (int8_t)qh;
+        reinterpret_cast<int8_t*>(qlw)[i] = (int8_t)(ql - 128);
+    }
+}
+
+// Exact partial sums of q . k over one 16-byte vector v of a K row (words
+// 4v..4v+3).  KVB 16: sh += sum qh*k, sl += sum ql*k over int16 pairs; for
+// head_dim <= 256 neither leaves int32 (|sh| <= 2^7*2^15*2^8 = 2^30, |sl| <=
+// 255*2^15*2^8 < 2^31).  KVB 8: sh += sum qh*k, sl += sum (ql-128)*k,
+// sk += sum k over int8 quads (each below 2^23).  q . k = 256*sh + sl
+// (+ 128*sk for KVB 8).
+template <int KVB>
+__device__ __forceinline__ void dot_vec(const int* qhw, const int* qlw, int v, const uint4 w, int& sh, int& sl,
+                                        int& sk) {
+    const int4 a = reinterpret_cast<const int4*>(qhw)[v];
+    const int4 b = reinterpret_cast<const int4*>(qlw)[v];
+    const unsigned ws[4] = {w.x, w.y, w.z, w.w};
+    const int as[4] = {a.x, a.y, a.z, a.w}, bs[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int4 a = q4[4 * v + u];
-                d += (long long)a.x * byte_s(ws[u], 0);
-                d += (long long)a.y * byte_s(ws[u], 1);
-                d += (long long)a.z * byte_s(ws[u], 2);
-                d += (long long)a.w * byte_s(ws[u], 3);
-            }
+    for (int u = 0; u < 4; ++u) {
+        if (KVB == 16) {
+            sh = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, as[u]), __builtin_bit_cast(short2_t, ws[u]), sh,
+                                        false);
+            sl = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, bs[u]), __builtin_bit_cast(short2_t, ws[u]), sl,
+                                        false);
+        } else {
+            sh = __builtin_amdgcn_sdot4(as[u], (int)ws[u], sh, false);
+            sl = __builtin_amdgcn_sdot4(bs[u], (int)ws[u], sl, false);
+            sk = __builtin_amdgcn_sdot4(0x01010101, (int)ws[u], sk, false);
         }
     }
-    return d;
+}
+
+// Value e of a 32-bit word of a V row: int16 (KVB 16) or int8 (KVB 8).
+template <int KVB>
+__device__ __forceinline__ int v_field(unsigned w, int e) {
+    if (KVB == 16) return e == 0 ? lo16(w) : hi16(w);
+    return byte_s(w, e);
+}
+
+// The V rows of one round of the weighted-V pass (chunks c0 .. c0+vR-1),
+// staged through LDS in 16-byte vectors: vector g = tid + k*kThreads of the
+// round is vector g % (vW/4) of row g / (vW/4).  Rows at or past npos are
+// clamped to row npos-1 (their values are never used).
+__device__ __forceinline__ void v_stage_load(const AttnDev& A, const uint8_t* vhead, int c0, int npos,
+                                             u32x4_t (&v)[kVPre]) {
+    const int W4 = A.vW / 4;
+#pragma unroll
+    for (int k = 0; k < kVPre; ++k) {
+        const int g = (int)threadIdx.x + k * kThreads;
+        const int t = g / W4, e4 = g - t * W4;
+        const int row = min(c0 * kChunk + t, npos - 1);
+        v[k] = *reinterpret_cast<const u32x4_t*>(vhead + (size_t)row * A.row_bytes + 16 * e4);
+    }
+}
+
+// ... and into the V pass's order: row r*kChunk + u, 32-bit word w of the
+// round at vstage[u*kThreads + r*vW + w].
+__device__ __forceinline__ void v_stage_store(const AttnDev& A, unsigned* vstage, const u32x4_t (&v)[kVPre]) {
+    const int W4 = A.vW / 4;
+#pragma unroll
+    for (int k = 0; k < kVPre; ++k) {
+        const int g = (int)threadIdx.x + k * kThreads;
+        const int t = g / W4, e4 = g - t * W4;
+        if (t < A.vR * kChunk) {
+            const int r = t / kChunk, u = t - r * kChunk;
+            *reinterpret_cast<u32x4_t*>(vstage + u * kThreads + r * A.vW + 4 * e4) = v[k];
+        }
+    }
 }
 
 template <int KVB>
@@ -147,9 +203,16 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
                                                         const int16_t* qkv, int16_t* out, int pos0,
                                                         int do_write, int do_attend) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const int kvh = blockIdx.x;
-    const int hd = A.hd, G = A.group, kv_dim = A.kv_heads * hd, GH = G * hd, seq = A.seq;
-    const int tid = threadIdx.x;
+    constexpr int E = KVB == 16 ? 2 : 4;  // values per 32-bit word
+    constexpr int KP = kKPre<KVB>;
+    const int hd = A.hd, G = A.group, kv_dim = A.kv_heads * hd;
+    // An attending launch has one workgroup per query head; a write-only
+    // launch one per KV head.  The first query head of a KV head's group packs
+    // the KV row; the others rebuild the same values in LDS.
+    const int h = do_attend ? (int)blockIdx.x : (int)blockIdx.x * G;
+    const int kvh = h / G;
+    const bool writer = do_write && h == kvh * G;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     // blockIdx.y: the position's offset in a batch of consecutive positions,
     // whose qkv and output rows are consecutive rows
     const int pos = pos0 + blockIdx.y;
@@ -157,229 +220,321 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     if (out) out += (size_t)blockIdx.y * A.dim;
     const int npos = pos + 1;
     const int nch = (npos + kChunk - 1) / kChunk;
+    const bool own_row = do_write != 0;  // row pos comes from LDS, not from HBM
 
-    unsigned long long* ssk = reinterpret_cast<unsigned long long*>(smem + A.o_ssk);  // 1 + G
-    float* mxs = reinterpret_cast<float*>(smem + A.o_mx);                             // G
-    float* invs = reinterpret_cast<float*>(smem + A.o_invs);                          // G
-    int* newk = reinterpret_cast<int*>(smem + A.o_newk);                              // hd
-    int* newv = reinterpret_cast<int*>(smem + A.o_newv);                              // hd
-    int* qrot = reinterpret_cast<int*>(smem + A.o_qrot);                              // G*hd
-    int16_t* sc = reinterpret_cast<int16_t*>(smem + A.o_sc);                          // G*seq
-    float* ep = reinterpret_cast<float*>(smem + A.o_ep);                              // G*seq
-    double* csum = reinterpret_cast<double*>(smem + A.o_csum);                        // G*nchmax
-    double* vpart = reinterpret_cast<double*>(smem + A.o_vpart);                      // vR*G*hd
-    double* acc = reinterpret_cast<double*>(smem + A.o_acc);                          // G*hd
+    int* wmax = reinterpret_cast<int*>(smem + A.o_wmax);        // kThreads/64
+    int* newv = reinterpret_cast<int*>(smem + A.o_newv);        // hd
+    uint8_t* kpk = smem + A.o_kpk;                              // row pos's packed K slice
+    int* qhw = reinterpret_cast<int*>(smem + A.o_qhw);          // hd/E words
+    int* qlw = reinterpret_cast<int*>(smem + A.o_qlw);          // hd/E words
+    int16_t* sc = reinterpret_cast<int16_t*>(smem + A.o_sc);    // seq
+    float* ep = reinterpret_cast<float*>(smem + A.o_ep);        // nchmax*kChunk
+    double* csum = reinterpret_cast<double*>(smem + A.o_csum);  // nchmax
+    double* vpart = reinterpret_cast<double*>(smem + A.o_vpart);  // vR*hd
+    double* acc = reinterpret_cast<double*>(smem + A.o_acc);    // hd
+    unsigned* vstage = reinterpret_cast<unsigned*>(smem + A.o_vst);  // kChunk*kThreads
 
-    if (tid <= G) ssk[tid] = 0ull;
-    __syncthreads();
-
-    const int16_t* kq = qkv + A.dim + kvh * hd;           // this head's K (q16)
+    const uint8_t* khead = kv + (size_t)kvh * hd * (KVB / 8);
+    const uint8_t* vhead = kv + (size_t)(kv_dim + kvh * hd) * (KVB / 8);
+    const int16_t* kq = qkv + A.dim + kvh * hd;           // this group's K (q16)
     const int16_t* vq = qkv + A.dim + kv_dim + kvh * hd;  // and V
-    uint8_t* row = kv + (size_t)pos * A.row_bytes;
+    const int16_t* qh = qkv + h * hd;                     // this head's q
     const int32_t* rt = rtab + (size_t)pos * (hd / 2) * 2;
 
-    // sums of squares: K head (slot 0) and the G query heads (slots 1..G)
-    if (A.qk_norm) {
-        if (do_write && tid < hd) atomicAdd(&ssk[0], (unsigned long long)(long long)(kq[tid] * kq[tid]));
-        if (do_attend) {
-            for (int idx = tid; idx < GH; idx += kThreads) {
-                const int g = idx / hd, i = idx - g * hd;
-                const int v = qkv[(kvh * G + g) * hd + i];
-                atomicAdd(&ssk[1 + g], (unsigned long long)(long long)(v * v));
-            }
-        }
+    // --- every global read of the launch is issued here, before any store,
+    // so that their latencies overlap: this thread's element i = tid of q, K,
+    // V with its RoPE partner j, the rotation, the norm weights; the elements
+    // of the sums of squares; the K vectors of its first scored position (lpp
+    // lanes per position, vectors sj, sj+lpp, ...) and its share of the
+    // first round's V rows (16-byte vectors, row-major), which go to LDS in
+    // the V pass's order (vstage slot u*kThreads + r*W + w: row r*kChunk + u,
+    // 32-bit word w).  The loads are unconditional, from clamped in-range
+    // addresses, and unused values are discarded afterwards: a predicated
+    // load would be waited for before the next one is issued.
+    const bool el = tid < hd;
+    const int ie = min(tid, hd - 1);
+    int j, ti;
+    bool first;
+    rope_pair(A.rope_half, hd, ie, j, ti, first);
+    const int16_t* knp = A.qk_norm ? kn : kq;
+    const int16_t* qnp = A.qk_norm ? qn : qh;
+    const int rc = rt[2 * ti], rs = rt[2 * ti + 1];
+    const int kqi = kq[ie], kqj = kq[j], vqi = vq[ie], qhi = qh[ie], qhj = qh[j];
+    const int kni = knp[ie], knj = knp[j], qni = qnp[ie], qnj = qnp[j];
+    int ke[4], qe[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int l = min(lane + 64 * c, hd - 1);
+        ke[c] = kq[l];
+        qe[c] = qh[l];
     }
-    __syncthreads();
+    const int nv = hd * KVB / 128;  // 16-byte vectors per K row slice
+    const int lpp = A.lpp, sj = tid & (lpp - 1), P = kThreads / lpp;
+    const int W = hd / E, vr = tid / W, vw = tid - vr * W;
+    uint4 kreg[KP];
+    u32x4_t vreg[kVPre];
+    {
+        const int t = tid / lpp;
+        const int tk = t < npos ? t : 0;
+        const uint4* src = reinterpret_cast<const uint4*>(khead + (size_t)tk * A.row_bytes);
+#pragma unroll
+        for (int k = 0; k < KP; ++k) kreg[k] = src[min(sj + k * lpp, nv - 1)];
+    }
+    v_stage_load(A, vhead, 0, npos, vreg);
+
+    // sums of squares of the K head and the query head (exact), whole in
+    // every lane: lane l holds elements l, l+64, l+128, l+192
+    long long ssk = 0, ssq = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const bool in = lane + 64 * c < hd;
+        const int kc = in ? ke[c] : 0, qc = in ? qe[c] : 0;
+        ssk += (long long)(kc * kc);
+        ssq += (long long)(qc * qc);
+    }
+    for (int o = 32; o >= 1; o >>= 1) {
+        ssk += __shfl_xor(ssk, o, 64);
+        ssq += __shfl_xor(ssq, o, 64);
+    }
+    const float co = (float)rc / 4096.0f, sn = (float)rs / 4096.0f;
 
     // --- KV pack of position pos (att_kv_rope)
-    if (do_write && tid < hd) {
+    if (do_write && el) {
         float rk = 1.0f;
         if (A.qk_norm) {
-            const float ss = (float)(long long)ssk[0] * (1.0f / 65536.0f);
+            const float ss = (float)ssk * (1.0f / 65536.0f);
             rk = rsqrt_d(ss / (float)hd + 1e-6f);
         }
-        const int i = tid;
-        int j, ti;
-        bool first;
-        rope_pair(A.rope_half, hd, i, j, ti, first);
-        float vv = (float)kq[i] / 256.0f, bb = (float)kq[j] / 256.0f;
+        float vv = (float)kqi / 256.0f, bb = (float)kqj / 256.0f;
         if (A.qk_norm) {
-            vv = (vv * rk) * ((float)kn[i] / 256.0f);
-            bb = (bb * rk) * ((float)kn[j] / 256.0f);
+            vv = (vv * rk) * ((float)kni / 256.0f);
+            bb = (bb * rk) * ((float)knj / 256.0f);
         }
-        const float co = (float)rt[2 * ti] / 4096.0f, sn = (float)rt[2 * ti + 1] / 4096.0f;
         const float o = first ? (vv * co) - (bb * sn) : (bb * sn) + (vv * co);
         const int q = kv_enc<KVB>(o);
-        kv_put<KVB>(row, kvh * hd + i, q);
-        newk[i] = q;
-        const int qv = kv_enc<KVB>((float)vq[i] / 256.0f);
-        kv_put<KVB>(row, kv_dim + kvh * hd + i, qv);
-        newv[i] = qv;
+        const int qv = kv_enc<KVB>((float)vqi / 256.0f);
+        if (writer) {
+            uint8_t* row = kv + (size_t)pos * A.row_bytes;
+            kv_put<KVB>(row, kvh * hd + tid, q);
+            kv_put<KVB>(row, kv_dim + kvh * hd + tid, qv);
+        }
+        kv_put<KVB>(kpk, tid, q);
+        newv[tid] = qv;
     }
     if (!do_attend) return;
 
     // --- q prep (att_qnorm_scale + att_qrot)
-    for (int idx = tid; idx < GH; idx += kThreads) {
-        const int g = idx / hd, i = idx - g * hd;
-        const int h = kvh * G + g;
-        const int16_t* qh = qkv + h * hd;
+    if (el) {
         float rq = 1.0f;
         if (A.qk_norm) {
-            const float ss = (float)(long long)ssk[1 + g] * (1.0f / 65536.0f);
+            const float ss = (float)ssq * (1.0f / 65536.0f);
             float r = rsqrt_d(ss / (float)hd + 1e-6f);
             r = fminf(r, 127.0f);
             rq = floorf(r * 65536.0f + 0.5f) / 65536.0f;
         }
-        int j, ti;
-        bool first;
-        rope_pair(A.rope_half, hd, i, j, ti, first);
-        float qv = (float)qh[i] / 256.0f, b = (float)qh[j] / 256.0f;
+        float qv = (float)qhi / 256.0f, b = (float)qhj / 256.0f;
         if (A.qk_norm) {
-            qv = (qv * rq) * ((float)qn[i] / 256.0f);
-            b = (b * rq) * ((float)qn[j] / 256.0f);
+            qv = (qv * rq) * ((float)qni / 256.0f);
+            b = (b * rq) * ((float)qnj / 256.0f);
         }
-        const float co = (float)rt[2 * ti] / 4096.0f, sn = (float)rt[2 * ti + 1] / 4096.0f;
         const float o = first ? (qv * co) - (b * sn) : (b * sn) + (qv * co);
-        qrot[idx] = q16_round(o * 256.0f);
+        q_split<KVB>(q16_round(o * 256.0f), tid, qhw, qlw);
     }
+    v_stage_store(A, vstage, vreg);
     __syncthreads();
 
-    // --- scores (att_score): exact dot, times 1/sqrt(hd), 1/1024 grid; one
-    // (position, head) per thread, the heads of a position in adjacent lanes
+    // --- scores (att_score): exact dot, times 1/sqrt(hd), 1/1024 grid; lpp
+    // adjacent lanes per position, joined by exact integer shuffles; the
+    // running maximum per wave
     const float invsqrt = 1.0f / sqrtf((float)hd);
     const float unit = KVB == 16 ? 1.0f / 524288.0f : 1.0f / 4096.0f;
-    const uint8_t* khead = kv + (size_t)kvh * hd * (KVB / 8);
-    for (int idx = tid; idx < G * npos; idx += kThreads) {
-        const int t = idx / G, g = idx - t * G;
-        const int* qg = qrot + g * hd;
-        long long d = 0;
-        if (t == pos && do_write) {
-            for (int i = 0; i < hd; ++i) d += (long long)qg[i] * newk[i];
+    int m = -32768;
+    for (int it = 0;; ++it) {
+        const int t = tid / lpp + it * P;
+        if (t >= npos) break;
+        int sh = 0, sl = 0, sk = 0;
+        if (own_row && t == pos) {
+            const uint4* src = reinterpret_cast<const uint4*>(kpk);
+#pragma unroll
+            for (int k = 0; k < KP; ++k) {
+                const int v = sj + k * lpp;
+                if (v < nv) dot_vec<KVB>(qhw, qlw, v, src[v], sh, sl, sk);
+            }
+        } else if (it == 0) {
+#pragma unroll
+            for (int k = 0; k < KP; ++k) {
+                const int v = sj + k * lpp;
+                if (v < nv) dot_vec<KVB>(qhw, qlw, v, kreg[k], sh, sl, sk);
+            }
         } else {
-            d = dot_row<KVB>(qg, khead + (size_t)t * A.row_bytes, hd);
+            const uint4* src = reinterpret_cast<const uint4*>(khead + (size_t)t * A.row_bytes);
+            uint4 kr[KP];
+#pragma unroll
+            for (int k = 0; k < KP; ++k) kr[k] = src[min(sj + k * lpp, nv - 1)];
+#pragma unroll
+            for (int k = 0; k < KP; ++k) {
+                const int v = sj + k * lpp;
+                if (v < nv) dot_vec<KVB>(qhw, qlw, v, kr[k], sh, sl, sk);
+            }
         }
-        const float s = (float)d * unit;
-        float f = floorf((s * invsqrt) * 1024.0f + 0.5f);
-        f = fminf(fmaxf(f, -32768.0f), 32767.0f);
-        sc[(size_t)g * seq + t] = (int16_t)f;
+        long long d = 256ll * sh + sl;
+        if (KVB == 8) d += 128ll * sk;
+        for (int o = 1; o < lpp; o <<= 1) d += __shfl_xor(d, o, 64);
+        if (sj == 0) {
+            const float s = (float)d * unit;
+            float f = floorf((s * invsqrt) * 1024.0f + 0.5f);
+            f = fminf(fmaxf(f, -32768.0f), 32767.0f);
+            sc[t] = (int16_t)f;
+            m = max(m, (int)f);
+        }
     }
+    for (int o = 32; o >= 1; o >>= 1) m = max(m, __shfl_xor(m, o, 64));
+    if (lane == 0) wmax[wave] = m;
     __syncthreads();
 
-    // --- stats (att_stats): max per head (exact), one wave per head
-    const int wave = tid >> 6, lane = tid & 63;
-    for (int g = wave; g < G; g += kThreads / 64) {
-        int m = -32768;
-        for (int t = lane; t < npos; t += 64) m = max(m, (int)sc[(size_t)g * seq + t]);
-        for (int o = 32; o >= 1; o >>= 1) m = max(m, __shfl_xor(m, o, 64));
-        if (lane == 0) mxs[g] = (float)m / 1024.0f;
-    }
+    // --- stats (att_stats): the max (exact), exponentials, chunk sums in
+    // position order, then the chunk sums in chunk order (every thread)
+    int mi = -32768;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) mi = max(mi, wmax[w]);
+    const float mx = (float)mi / 1024.0f;
+    for (int t = tid; t < npos; t += kThreads) ep[t] = exp_d((float)sc[t] / 1024.0f - mx);
     __syncthreads();
-    for (int idx = tid; idx < G * npos; idx += kThreads) {
-        const int g = idx / npos, t = idx - g * npos;
-        ep[(size_t)g * seq + t] = exp_d((float)sc[(size_t)g * seq + t] / 1024.0f - mxs[g]);
-    }
-    __syncthreads();
-    // chunk sums of exp, in position order within a chunk
-    for (int idx = tid; idx < G * nch; idx += kThreads) {
-        const int g = idx / nch, c = idx - g * nch;
-        const int t0 = c * kChunk, t1 = min(t0 + kChunk, npos);
-        const float* e = ep + (size_t)g * seq;
+    for (int c = tid; c < nch; c += kThreads) {
+        const int n = min(kChunk, npos - c * kChunk);
+        const float4* e4 = reinterpret_cast<const float4*>(ep + c * kChunk);
+        float e[kChunk];
+#pragma unroll
+        for (int k = 0; k < kChunk / 4; ++k) {
+            const float4 f = e4[k];
+            e[4 * k] = f.x;
+            e[4 * k + 1] = f.y;
+            e[4 * k + 2] = f.z;
+            e[4 * k + 3] = f.w;
+        }
         double cs = 0.0;
-        for (int t = t0; t < t1; ++t) cs += (double)e[t];
-        csum[g * A.nchmax + c] = cs;
+#pragma unroll
+        for (int u = 0; u < kChunk; ++u)
+            if (u < n) cs += (double)e[u];
+        csum[c] = cs;
     }
     __syncthreads();
-    if (tid < G) {
-        const int g = tid;
+    float iv;
+    {
         double sum = 0.0;
-        for (int c = 0; c < nch; ++c) sum += csum[g * A.nchmax + c];
+        for (int c0 = 0; c0 < nch; c0 += 8) {
+            double cv[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) cv[k] = csum[min(c0 + k, A.nchmax - 1)];
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                if (c0 + k < nch) sum += cv[k];
+        }
         const float fs = (float)sum;
         float qs = floorf(fs * 32.0f + 0.5f);
         qs = fminf(fmaxf(qs, -32768.0f), 32767.0f);
         const float sd = qs / 32.0f;
-        invs[g] = sd > 0.0f ? 1.0f / sd : 0.0f;
+        iv = sd > 0.0f ? 1.0f / sd : 0.0f;
     }
-    __syncthreads();
 
-    // --- weighted V (att_v): rounds of vR chunks; a thread sums one chunk of
-    // one (head, element), then the round's chunk sums join the running total
-    // in chunk order
+    // --- weighted V (att_v): rounds of vR chunks; a thread sums E elements
+    // (one 32-bit word) of one chunk, each in position order, then the
+    // round's chunk sums join the running total in chunk order
+    // a += p*v with v = q*vunit: p (24-bit mantissa) times q (at most 16
+    // bits) is exact in double, so fma(p*vunit, q, a) rounds exactly as the
+    // add of the product does
     const float vunit = KVB == 16 ? 1.0f / 2048.0f : 1.0f / 16.0f;
-    const uint8_t* vhead = kv + (size_t)(kv_dim + kvh * hd) * (KVB / 8);
-    const bool own_last = do_write != 0;  // position pos comes from LDS
+    const double vunit_d = vunit;
     for (int c0 = 0; c0 < nch; c0 += A.vR) {
         const int nr = min(A.vR, nch - c0);
-        for (int idx = tid; idx < nr * GH; idx += kThreads) {
-            const int r = idx / GH, gi = idx - r * GH;
-            const int g = gi / hd, i = gi - g * hd;
-            const int t0 = (c0 + r) * kChunk, t1 = min(t0 + kChunk, npos);
-            const int tend = (own_last && t1 == npos) ? t1 - 1 : t1;
-            const float* pg = ep + (size_t)g * seq;
-            const float iv = invs[g];
-            const uint8_t* vp = vhead + (size_t)i * (KVB / 8);
-            double a = 0.0;
-            int t = t0;
-            for (; t + 8 <= tend; t += 8) {
-                int q[8];
+        if (c0 > 0) {
+            // a later round: its rows through the same LDS slots
+            v_stage_load(A, vhead, c0, npos, vreg);
+            v_stage_store(A, vstage, vreg);
+            __syncthreads();
+        }
+        if (vr < nr) {
+            const int t0 = (c0 + vr) * kChunk, t1 = min(t0 + kChunk, npos);
+            const int tend = (own_row && t1 == npos) ? t1 - 1 : t1;
+            const int n = tend - t0;
+            double a[E];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) q[u] = kv_get<KVB>(vp + (size_t)(t + u) * A.row_bytes, 0);
+            for (int e = 0; e < E; ++e) a[e] = 0.0;
+            const float4* e4 = reinterpret_cast<const float4*>(ep + t0);
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const float p = pg[t + u] * iv;
-                    const float v = (float)q[u] * vunit;
-                    a += (double)p * (double)v;
+            for (int k = 0; k < kChunk / 4; ++k) {
+                const float4 f = e4[k];
+                const float pe[4] = {f.x, f.y, f.z, f.w};
+                unsigned wv[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) wv[u] = vstage[(4 * k + u) * kThreads + tid];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    if (4 * k + u < n) {
+                        const double pp = (double)(pe[u] * iv) * vunit_d;
+#pragma unroll
+                        for (int e = 0; e < E; ++e) a[e] = fma(pp, (double)v_field<KVB>(wv[u], e), a[e]);
+                    }
                 }
             }
-            for (; t < tend; ++t) {
-                const float p = pg[t] * iv;
-                const float v = (float)kv_get<KVB>(vp + (size_t)t * A.row_bytes, 0) * vunit;
-                a += (double)p * (double)v;
-            }
             if (tend != t1) {
-                const float p = pg[pos] * iv;
-                const float v = (float)newv[i] * vunit;
-                a += (double)p * (double)v;
+                const float p = ep[pos] * iv;
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    const float v = (float)newv[vw * E + e] * vunit;
+                    a[e] += (double)p * (double)v;
+                }
             }
-            vpart[idx] = a;
+#pragma unroll
+            for (int e = 0; e < E; ++e) vpart[vr * hd + vw * E + e] = a[e];
         }
         __syncthreads();
         const bool last = c0 + nr >= nch;
-        for (int gi = tid; gi < GH; gi += kThreads) {
-            double s = c0 == 0 ? 0.0 : acc[gi];
-            for (int r = 0; r < nr; ++r) s += vpart[r * GH + gi];
-            if (last) {
-                const int g = gi / hd, i = gi - g * hd;
-                out[(kvh * G + g) * hd + i] = (int16_t)q16_round((float)s * 256.0f);
-            } else {
-                acc[gi] = s;
+        for (int i = tid; i < hd; i += kThreads) {
+            double s = c0 == 0 ? 0.0 : acc[i];
+            for (int r0 = 0; r0 < nr; r0 += 8) {
+                double pv[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) pv[k] = vpart[min(r0 + k, A.vR - 1) * hd + i];
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    if (r0 + k < nr) s += pv[k];
             }
+            if (last) out[h * hd + i] = (int16_t)q16_round((float)s * 256.0f);
+            else acc[i] = s;
         }
-        __syncthreads();
+        if (!last) __syncthreads();
     }
 }
 
-// LDS carve-up of one workgroup; returns the bytes used.
+// LDS carve-up of one workgroup and the lane plan; returns the bytes used.
 size_t attn_layout(AttnDev& A) {
-    const int G = A.group, hd = A.hd, GH = G * hd;
+    const int hd = A.hd;
+    const int nv = hd * A.kv_bits / 128;
+    const int kp = A.kv_bits == 16 ? kKPre<16> : kKPre<8>;
+    const int E = A.kv_bits == 16 ? 2 : 4;
+    A.lpp = 1;
+    while (A.lpp * kp < nv) A.lpp *= 2;
     A.nchmax = (A.seq + kChunk - 1) / kChunk;
-    A.vR = GH >= kThreads ? 1 : kThreads / GH;
+    A.vW = hd / E;
+    A.vR = kThreads / A.vW;
     size_t off = 0;
     auto take = [&](size_t bytes) {
         const size_t o = off;
         off = (off + bytes + 15) & ~(size_t)15;
         return (int)o;
     };
-    A.o_ssk = take(8 * (size_t)(1 + G));
-    A.o_mx = take(4 * (size_t)G);
-    A.o_invs = take(4 * (size_t)G);
-    A.o_newk = take(4 * (size_t)hd);
+    A.o_wmax = take(4 * (size_t)(kThreads / 64));
     A.o_newv = take(4 * (size_t)hd);
-    A.o_qrot = take(4 * (size_t)GH);
-    A.o_sc = take(2 * (size_t)G * A.seq);
-    A.o_ep = take(4 * (size_t)G * A.seq);
-    A.o_csum = take(8 * (size_t)G * A.nchmax);
-    A.o_vpart = take(8 * (size_t)A.vR * GH);
-    A.o_acc = take(8 * (size_t)GH);
+    A.o_kpk = take((size_t)hd * A.kv_bits / 8);
+    A.o_qhw = take(4 * (size_t)(hd / E));
+    A.o_qlw = take(4 * (size_t)(hd / E));
+    A.o_sc = take(2 * (size_t)A.seq);
+    A.o_ep = take(4 * (size_t)A.nchmax * kChunk);
+    A.o_csum = take(8 * (size_t)A.nchmax);
+    A.o_vpart = take(8 * (size_t)A.vR * hd);
+    A.o_acc = take(8 * (size_t)hd);
+    A.o_vst = take(4 * (size_t)kChunk * kThreads);
     return off;
 }
 
@@ -400,7 +555,7 @@ int launch(vgx_attn* at, int layer, int pos, int ntok, const int16_t* qkv, int16
     const AttnDev& A = at->a;
     const int16_t* qn = at->qn ? at->qn + (size_t)layer * A.hd : nullptr;
     const int16_t* kn = at->kn ? at->kn + (size_t)layer * A.hd : nullptr;
-    const dim3 grid(A.kv_heads, ntok);
+    const dim3 grid(att ? A.heads : A.kv_heads, ntok);
     if (A.kv_bits == 16)
         hipLaunchKernelGGL(attn_kernel<16>, grid, dim3(kThreads), at->lds, at->ctx->stream, A,
                            at->kv[layer], at->rtab, qn, kn, qkv, out, pos, w, att);
@@ -423,7 +578,6 @@ int vgx_attn_create(vgx_ctx* ctx, const vgx_attn_desc* d, vgx_attn** out) {
     if (d->heads % d->kv_heads) return vgx_fail(VGX_EINVAL, "vgx_attn_create: heads not a multiple of kv_heads");
     if (d->head_dim % 16 || d->head_dim > 256)
         return vgx_fail(VGX_EINVAL, "vgx_attn_create: head_dim must be a multiple of 16, at most 256");
-    if (d->heads / d->kv_heads > 16) return vgx_fail(VGX_EINVAL, "vgx_attn_create: more than 16 query heads per KV head");
     if (d->heads * d->head_dim != d->dim) return vgx_fail(VGX_EINVAL, "vgx_attn_create: heads*head_dim != dim");
     if (d->kv_bits != 16 && d->kv_bits != 8) return vgx_fail(VGX_EINVAL, "vgx_attn_create: kv_bits must be 16 or 8");
     if (!d->rope_cos || !d->rope_sin) return vgx_fail(VGX_EINVAL, "vgx_attn_create: rope tables are NULL");

@@ -331,7 +331,14 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
     // lane only -- the epilogue's per-row operands (row scales, residual), so
     // their latency hides under the main loop.  With RI rows per lane those
     // registers would cost occupancy, which the streaming launches need more.
+    // With one row per lane (the latency-bound decode shapes) a lane's first
+    // NPF chunks all go out in begin_tile, and each chunk consumed is
+    // replaced by the one NPF chunks ahead: one memory round trip per tile
+    // instead of one per chunk.  Those loads read clamped in-range addresses
+    // unconditionally (a chunk or row past the end is computed and dropped):
+    // a predicated load would be waited for before the next one is issued.
     constexpr bool PF = RI == 1;
+    constexpr int NPF = PF ? 4 : 1;
     MatDev M;
     int units = 0, unit0 = 0;
     const uint8_t* body = nullptr;
@@ -339,6 +346,18 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
     int pres[RI][RPU];
     uint4 w[RI], w3[RI];
     uint32_t smv[RI], smv3[RI];
+    uint4 pb[NPF], pb3[NPF];     // PF: the lane's chunks cl + s*LPR (+ k*NPF*LPR)
+    uint32_t psm[NPF], psm3[NPF];  // PF, q4: their scale/min words
+    auto pf_load = [&](int s, int c) {
+        const int u = min(unit0 + rs, units - 1);
+        const int cc = min(c, nch - 1);
+        pb[s] = wload(body + (size_t)u * ustride + (size_t)cc * 16);
+        if (EPI == EPI_GATE) pb3[s] = wload(body3 + (size_t)u * ustride + (size_t)cc * 16);
+        if (KIND == VGX_Q4) {
+            psm[s] = M.sm[(size_t)u * nch + cc];
+            if (EPI == EPI_GATE) psm3[s] = M3.sm[(size_t)u * nch + cc];
+        }
+    };
     auto begin_tile = [&](int tile) {
         const int mi = L.bpm > 0 ? tile / L.bpm : find_mat(L, tile);
         M = L.nmat <= kInlineMats ? L.md[mi] : L.mats[mi];
@@ -349,13 +368,18 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
         for (int it = 0; it < (PF ? RI : 0); ++it) {
 #pragma unroll
             for (int hr = 0; hr < RPU; ++hr) {
-                const int row = (unit0 + it * RPI + rs) * RPU + hr;
-                const bool rok = row < M.rows;
-                pw[it][hr] = (KIND != VGX_Q4 && rok) ? M.wsr[row] : 0.0f;
-                pw3[it][hr] = (KIND != VGX_Q4 && EPI == EPI_GATE && rok) ? M3.wsr[row] : 0.0f;
+                // clamped rows: a row past the end is never stored
+                const int row = min((unit0 + it * RPI + rs) * RPU + hr, M.rows - 1);
+                pw[it][hr] = KIND != VGX_Q4 ? M.wsr[row] : 0.0f;
+                pw3[it][hr] = (KIND != VGX_Q4 && EPI == EPI_GATE) ? M3.wsr[row] : 0.0f;
                 const bool has_res = (EPI == EPI_STORE || EPI == EPI_STORE_ARGMAX || EPI == EPI_SPLIT) && L.res;
-                pres[it][hr] = (has_res && rok) ? (int)L.res[M.out_off + row] : 0;
+                pres[it][hr] = has_res ? (int)L.res[M.out_off + row] : 0;
             }
+        }
+        if (PF) {
+#pragma unroll
+            for (int s = 0; s < NPF; ++s) pf_load(s, cl + s * LPR);
+            return;
         }
 #pragma unroll
         for (int it = 0; it < RI; ++it) {
@@ -488,7 +512,44 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
             for (int k = 0; k < NV; ++k) acc[it][k] = 0.0;
         const float ps = M.ps;
         const float ps3 = (EPI == EPI_GATE) ? M3.ps : 0.0f;
-        for (int j = 0; j < niter; ++j) {
+        // one chunk c of row slot it: weights wv, scale/min word sm (and the
+        // gate's second matrix)
+        auto q4_step = [&](int it, int c, const uint4 wv, uint32_t sm, const uint4 wv3, uint32_t sm3) {
+            const uint4 xhe = lds[4 * c], xle = lds[4 * c + 1], xho = lds[4 * c + 2], xlo = lds[4 * c + 3];
+            const float Xg = (float)xg[c];
+            const int kk = (EPI == EPI_SPLIT && c >= L.split_chunk) ? 1 : 0;
+            const int D = q4_chunk(wv, xhe, xle, xho, xlo);
+            const float sa = (float)(int16_t)(sm & 0xFFFFu) * ps;
+            const float ma = (float)(int16_t)(sm >> 16) * ps;
+            const float t1 = sa * (float)D;
+            const float t2 = ma * Xg;
+            const float t = t1 + t2;
+            if (EPI == EPI_SPLIT) {
+                if (kk) acc[it][NV - 1] += (double)t; else acc[it][0] += (double)t;
+            } else {
+                acc[it][0] += (double)t;
+            }
+            if (EPI == EPI_GATE) {
+                const int D3 = q4_chunk(wv3, xhe, xle, xho, xlo);
+                const float sb = (float)(int16_t)(sm3 & 0xFFFFu) * ps3;
+                const float mb = (float)(int16_t)(sm3 >> 16) * ps3;
+                const float u1 = sb * (float)D3;
+                const float u2 = mb * Xg;
+                const float u = u1 + u2;
+                acc[it][NV - 1] += (double)u;
+            }
+        };
+        if (PF) {
+            for (int j0 = 0; j0 < niter; j0 += NPF) {
+#pragma unroll
+                for (int s = 0; s < NPF; ++s) {
+                    const int c = cl + (j0 + s) * LPR;
+                    if (c < nch) q4_step(0, c, pb[s], psm[s], pb3[s], psm3[s]);
+                    if (j0 + s + NPF < niter) pf_load(s, c + NPF * LPR);
+                }
+            }
+        }
+        for (int j = 0; j < (PF ? 0 : niter); ++j) {
             const int c = cl + j * LPR;
             const bool cok = c < nch;
             uint4 wn[RI], wn3[RI];
@@ -511,32 +572,8 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
                 }
             }
             if (cok) {
-                const uint4 xhe = lds[4 * c], xle = lds[4 * c + 1], xho = lds[4 * c + 2], xlo = lds[4 * c + 3];
-                const float Xg = (float)xg[c];
-                const int kk = (EPI == EPI_SPLIT && c >= L.split_chunk) ? 1 : 0;
 #pragma unroll
-                for (int it = 0; it < RI; ++it) {
-                    const int D = q4_chunk(w[it], xhe, xle, xho, xlo);
-                    const float sa = (float)(int16_t)(smv[it] & 0xFFFFu) * ps;
-                    const float ma = (float)(int16_t)(smv[it] >> 16) * ps;
-                    const float t1 = sa * (float)D;
-                    const float t2 = ma * Xg;
-                    const float t = t1 + t2;
-                    if (EPI == EPI_SPLIT) {
-                        if (kk) acc[it][NV - 1] += (double)t; else acc[it][0] += (double)t;
-                    } else {
-                        acc[it][0] += (double)t;
-                    }
-                    if (EPI == EPI_GATE) {
-                        const int D3 = q4_chunk(w3[it], xhe, xle, xho, xlo);
-                        const float sb = (float)(int16_t)(smv3[it] & 0xFFFFu) * ps3;
-                        const float mb = (float)(int16_t)(smv3[it] >> 16) * ps3;
-                        const float u1 = sb * (float)D3;
-                        const float u2 = mb * Xg;
-                        const float u = u1 + u2;
-                        acc[it][NV - 1] += (double)u;
-                    }
-                }
+                for (int it = 0; it < RI; ++it) q4_step(it, c, w[it], smv[it], w3[it], smv3[it]);
             }
             if (more) {
 #pragma unroll
@@ -592,7 +629,70 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
 #pragma unroll
         for (int k = 0; k < NI; ++k) acc[it][k] = 0;
 
-    for (int j = 0; j < niter; ++j) {
+    // one chunk c of row slot it: weights wa (and wb, the gate's second matrix)
+    auto step = [&](int it, int c, const uint4 wa, const uint4 wb) {
+        // column half for the split epilogue
+        const int hb = (EPI == EPI_SPLIT && c >= L.split_chunk) ? 1 : 0;
+        if (KIND == VGX_Q8) {
+            const uint4 xh = lds[2 * c], xl = lds[2 * c + 1];
+            int s1 = 0;
+            uint32_t s2 = 0;
+            q8_chunk(wa, xh, xl, s1, s2);
+            const int o = 2 * hb;
+            acc[it][o] += s1;
+            acc[it][o + 1] += (int)s2;
+            if (EPI == EPI_GATE) {
+                int t1 = 0;
+                uint32_t t2 = 0;
+                q8_chunk(wb, xh, xl, t1, t2);
+                acc[it][2] += t1;
+                acc[it][3] += (int)t2;
+            }
+        } else {  // T3: 4 texels = 32 columns of a row pair
+            const uint4 xh0 = lds[4 * c], xh1 = lds[4 * c + 1];
+            const uint4 xl0 = lds[4 * c + 2], xl1 = lds[4 * c + 3];
+            const uint32_t xh[8] = {xh0.x, xh0.y, xh0.z, xh0.w, xh1.x, xh1.y, xh1.z, xh1.w};
+            const uint32_t xl[8] = {xl0.x, xl0.y, xl0.z, xl0.w, xl1.x, xl1.y, xl1.z, xl1.w};
+#pragma unroll
+            for (int m = 0; m < (EPI == EPI_GATE ? 2 : 1); ++m) {
+                const uint4 wv = m == 0 ? wa : wb;
+                const uint32_t td[4] = {wv.x, wv.y, wv.z, wv.w};
+                int a1 = 0, b1 = 0;
+                uint32_t a2 = 0, b2 = 0;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const uint32_t T = td[t];
+                    const uint32_t l0 = lut[T & 0xFFu], l1 = lut[(T >> 8) & 0xFFu];
+                    const uint32_t l2 = lut[(T >> 16) & 0xFFu], l3 = lut[T >> 24];
+                    a1 = sdot4(l0, xh[2 * t], a1);
+                    a1 = sdot4(l1, xh[2 * t + 1], a1);
+                    a2 = udot4(l0, xl[2 * t], a2);
+                    a2 = udot4(l1, xl[2 * t + 1], a2);
+                    b1 = sdot4(l2, xh[2 * t], b1);
+                    b1 = sdot4(l3, xh[2 * t + 1], b1);
+                    b2 = udot4(l2, xl[2 * t], b2);
+                    b2 = udot4(l3, xl[2 * t + 1], b2);
+                }
+                // layout per unit: [half or matrix][row of pair][s1, s2]
+                const int o = 4 * (m + hb);
+                acc[it][o + 0] += a1;
+                acc[it][o + 1] += (int)a2;
+                acc[it][o + 2] += b1;
+                acc[it][o + 3] += (int)b2;
+            }
+        }
+    };
+    if (PF) {
+        for (int j0 = 0; j0 < niter; j0 += NPF) {
+#pragma unroll
+            for (int s = 0; s < NPF; ++s) {
+                const int c = cl + (j0 + s) * LPR;
+                if (c < nch) step(0, c, pb[s], pb3[s]);
+                if (j0 + s + NPF < niter) pf_load(s, c + NPF * LPR);
+            }
+        }
+    }
+    for (int j = 0; j < (PF ? 0 : niter); ++j) {
         const int c = cl + j * LPR;
         const bool cok = c < nch;
         uint4 wn[RI], wn3[RI];
@@ -611,62 +711,8 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
             }
         }
         if (cok) {
-            // column half for the split epilogue
-            const int hb = (EPI == EPI_SPLIT && c >= L.split_chunk) ? 1 : 0;
-            if (KIND == VGX_Q8) {
-                const uint4 xh = lds[2 * c], xl = lds[2 * c + 1];
 #pragma unroll
-                for (int it = 0; it < RI; ++it) {
-                    int s1 = 0;
-                    uint32_t s2 = 0;
-                    q8_chunk(w[it], xh, xl, s1, s2);
-                    const int o = 2 * hb;
-                    acc[it][o] += s1;
-                    acc[it][o + 1] += (int)s2;
-                    if (EPI == EPI_GATE) {
-                        int t1 = 0;
-                        uint32_t t2 = 0;
-                        q8_chunk(w3[it], xh, xl, t1, t2);
-                        acc[it][2] += t1;
-                        acc[it][3] += (int)t2;
-                    }
-                }
-            } else {  // T3: 4 texels = 32 columns of a row pair
-                const uint4 xh0 = lds[4 * c], xh1 = lds[4 * c + 1];
-                const uint4 xl0 = lds[4 * c + 2], xl1 = lds[4 * c + 3];
-                const uint32_t xh[8] = {xh0.x, xh0.y, xh0.z, xh0.w, xh1.x, xh1.y, xh1.z, xh1.w};
-                const uint32_t xl[8] = {xl0.x, xl0.y, xl0.z, xl0.w, xl1.x, xl1.y, xl1.z, xl1.w};
-#pragma unroll
-                for (int it = 0; it < RI; ++it) {
-#pragma unroll
-                    for (int m = 0; m < (EPI == EPI_GATE ? 2 : 1); ++m) {
-                        const uint4 wv = m == 0 ? w[it] : w3[it];
-                        const uint32_t td[4] = {wv.x, wv.y, wv.z, wv.w};
-                        int a1 = 0, b1 = 0;
-                        uint32_t a2 = 0, b2 = 0;
-#pragma unroll
-                        for (int t = 0; t < 4; ++t) {
-                            const uint32_t T = td[t];
-                            const uint32_t l0 = lut[T & 0xFFu], l1 = lut[(T >> 8) & 0xFFu];
-                            const uint32_t l2 = lut[(T >> 16) & 0xFFu], l3 = lut[T >> 24];
-                            a1 = sdot4(l0, xh[2 * t], a1);
-                            a1 = sdot4(l1, xh[2 * t + 1], a1);
-                            a2 = udot4(l0, xl[2 * t], a2);
-                            a2 = udot4(l1, xl[2 * t + 1], a2);
-                            b1 = sdot4(l2, xh[2 * t], b1);
-                            b1 = sdot4(l3, xh[2 * t + 1], b1);
-                            b2 = udot4(l2, xl[2 * t], b2);
-                            b2 = udot4(l3, xl[2 * t + 1], b2);
-                        }
-                        // layout per unit: [half or matrix][row of pair][s1, s2]
-                        const int o = 4 * (m + hb);
-                        acc[it][o + 0] += a1;
-                        acc[it][o + 1] += (int)a2;
-                        acc[it][o + 2] += b1;
-                        acc[it][o + 3] += (int)b2;
-                    }
-                }
-            }
+            for (int it = 0; it < RI; ++it) step(it, c, w[it], w3[it]);
         }
         if (more) {
 #pragma unroll
@@ -789,7 +835,8 @@ template <int KIND, int EPI, int XM>
 KernFn pick_kernel(int lpr, int ri) {
 #define VGX_K(LP, R) \
     if (lpr == LP && ri == R) return gemv_kernel<KIND, LP, R, EPI, XM>;
-    VGX_K(8, 1) VGX_K(8, 4) VGX_K(16, 1) VGX_K(16, 4) VGX_K(32, 1) VGX_K(32, 4) VGX_K(64, 1) VGX_K(64, 4)
+    // the plan pairs 4 rows per lane with 8 or 16 lanes per row only
+    VGX_K(8, 1) VGX_K(8, 4) VGX_K(16, 1) VGX_K(16, 4) VGX_K(32, 1) VGX_K(64, 1)
 #undef VGX_K
     return nullptr;
 }
