@@ -869,8 +869,12 @@ size_t lds_bytes(int kind, int cols) {
 
 // Rows per lane: 4 when the matrix has enough rows to give every CU several
 // waves anyway (the bandwidth-bound launches), else 1 (the latency-bound
-// decode shapes).  Lanes per row, latency-bound: enough that each lane has
-// about four chunks, at most one wave per row.  Bandwidth-bound, from a sweep
+// decode shapes).  Lanes per row, latency-bound: q8 and q4 enough that each
+// lane has about four chunks, at most one wave per row; t3 one chunk per lane
+// where a wave covers the row (its table unpacking is the costly part, and
+// shorter lanes spread it over more CUs; measured on the 0.5B ternary decode:
+// +10%, while q8 decode lost 7% the same way).  Each lane's chunks all load in
+// one round trip.  Bandwidth-bound, from a sweep
 // of HBM-streamed launches on MI355X: q8 keeps 16 lanes on a row up to 64
 // chunks (K <= 1024) and 8 beyond (more chunks per lane in flight; int32
 // accumulators are cheap); q4 (fp64 group sums, more registers per chunk) and
@@ -882,7 +886,12 @@ int vgx_gemv_plan(int kind, int rows, int cols, int num_cu, int* lpr, int* ri, i
     const int units = kind == VGX_T3 ? (rows + 1) / 2 : rows;
     const int waves1 = (units + 64 / l - 1) / (64 / l);
     const int r = waves1 >= 16 * num_cu ? 4 : 1;
-    if (r == 4) l = kind == VGX_Q8 ? (nch <= 64 ? 16 : 8) : (nch <= 48 ? 8 : 16);
+    if (r == 4) {
+        l = kind == VGX_Q8 ? (nch <= 64 ? 16 : 8) : (nch <= 48 ? 8 : 16);
+    } else if (kind == VGX_T3) {
+        l = 8;
+        while (l < 64 && l < nch) l <<= 1;
+    }
     const int rpi = 64 / l;
     *lpr = l;
     *ri = r;
