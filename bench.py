@@ -191,6 +191,32 @@ def ternary_decode_bench(runs):
                         "t3", 16, 128, 256, runs)
 
 
+def ternary_batch_bench(runs, nseq=32):
+    """C5 at batch 32: the same ternary model, 32 sequences of 128 prompt
+    tokens (each prefilled on its own KV cache), then 256 greedy steps in
+    lockstep; decode tokens/s = 32 x 255 steps over the decode time."""
+    import numpy as np
+    from vgx import synth
+    from vgx.engine import Engine
+
+    spec = synth.bitcpm_spec(seq=512)
+    blob = synth.container(spec, "t3", seed=0, q8_row=True)
+    prompts = np.stack([synth.prompt(128, spec.vocab, seed=s) for s in range(nseq)])
+    eng = Engine(blob, kv_bits=16)
+    eng.generate_batch(prompts, 256)
+    pf, dc = [], []
+    for _ in range(runs):
+        _toks, p, d = eng.generate_batch(prompts, 256)
+        pf.append(p)
+        dc.append(d)
+    eng.close()
+    ms_step = float(np.median(dc)) / 255
+    return {"model": "0.5B Llama-shaped t3 (per-row ternary P(0)=0.4), seed 0", "sequences": nseq, "prompt": 128,
+            "gen": 256, "seq": 512, "kv": "q16", "tokens_per_s": round(nseq * 1000.0 / ms_step, 1),
+            "ms_per_step": round(ms_step, 4), "prefill_ms_all_sequences": round(float(np.median(pf)), 2),
+            "runs": runs}
+
+
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 matrix-core peak, TOPS
 
 
@@ -285,7 +311,7 @@ def main():
     ap.add_argument("--skip-decode", action="store_true")
     ap.add_argument("--copy-mb", type=int, default=0, help="also time a device copy of this many MiB")
     ap.add_argument("--cpu-decode-steps", type=int, default=16)
-    ap.add_argument("--only", choices=["gemv", "decode", "prefill", "hybrid", "ternary"], default=None,
+    ap.add_argument("--only", choices=["gemv", "decode", "prefill", "hybrid", "ternary", "ternary32"], default=None,
                     help="run one leg (for profiling); the JSON line then carries that leg only")
     ap.add_argument("--prefill-runs", type=int, default=5)
     ap.add_argument("--skip-prefill", action="store_true")
@@ -306,6 +332,9 @@ def main():
         return
     if args.only == "prefill":
         print(json.dumps({"prefill": prefill_bench(args.prefill_runs)}))
+        return
+    if args.only == "ternary32":
+        print(json.dumps({"decode_c5_batch32": ternary_batch_bench(args.decode_runs)}))
         return
     if args.only in ("hybrid", "ternary"):
         fn = hybrid_decode_bench if args.only == "hybrid" else ternary_decode_bench
@@ -440,6 +469,7 @@ def main():
                   ("decode_c5_batch1", ternary_decode_bench(args.decode_runs), 4)]
         for key, (_b, _p, _t, res), _n in others:
             out[key] = res
+        out["decode_c5_batch32"] = ternary_batch_bench(max(1, args.decode_runs // 2))
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
         if not args.skip_decode:

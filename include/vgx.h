@@ -196,6 +196,15 @@ int vgx_rmsnorm_batch(vgx_ctx* ctx, int ntok, int dim, const int16_t* x, const i
 int vgx_embed_q8_batch(vgx_ctx* ctx, const int8_t* emb, const float* emb_scale, int vocab, int dim, int ntok,
                        const int* tokens, int16_t* x);
 
+/* One matrix holding the rows of n q8 or t3 matrices of equal cols, in order
+ * (the LM head tiles as a single operand of vgx_gemm, for batched decode);
+ * every row keeps its own scale, so its results are unchanged.  A t3 matrix
+ * before the last must have an even row count. */
+int vgx_mat_concat(vgx_ctx* ctx, int n, vgx_mat* const* mats, vgx_mat** out);
+/* argmax_token (engine/src/sampling.cpp:160-162, the first maximum) of each
+ * row of a row-major nrows x n q16 array (device); tokens: device int[nrows]. */
+int vgx_argmax_rows(vgx_ctx* ctx, int nrows, int n, const int16_t* v, int* tokens);
+
 /* Session::embedding (engine/src/session.cpp:342-371), q8 rows: x = the
  * host-grid q16 of emb[token]*emb_scale[token].  emb: vocab x dim signed
  * bytes (device), emb_scale: vocab f32 (device), token: device int. */
@@ -229,6 +238,22 @@ int vgx_attn_block(vgx_attn* a, int layer, int pos, const int16_t* qkv, int16_t*
  * rows of dim + 2*kv_dim, out ntok rows of dim.  Append all rows first. */
 int vgx_kv_append_batch(vgx_attn* a, int layer, int pos0, int ntok, const int16_t* qkv);
 int vgx_attn_decode_batch(vgx_attn* a, int layer, int pos0, int ntok, const int16_t* qkv, int16_t* out);
+
+/* ---- several sequences in lockstep (batched greedy decode).  No counterpart
+ * in the reference, which decodes one sequence; each sequence's results are
+ * the exact results of the single-sequence entry points on it.
+ * vgx_attn_create_seqs: the KV caches of nseq sequences (each seq rows per
+ *   layer); vgx_attn_create is nseq = 1.
+ * vgx_attn_seq_view: a handle on sequence s's cache that every
+ *   single-sequence entry point takes (its prompt's batched prefill, the
+ *   MMKV1 row export/import); it shares the parent's buffers, so free it
+ *   before the parent.
+ * vgx_attn_block_seqs: vgx_attn_block of position pos for sequences
+ *   0..nseq-1 in one launch; qkv holds nseq consecutive rows of
+ *   dim + 2*kv_dim, out nseq rows of dim. */
+int vgx_attn_create_seqs(vgx_ctx* ctx, const vgx_attn_desc* desc, int nseq, vgx_attn** out);
+int vgx_attn_seq_view(vgx_attn* a, int s, vgx_attn** out);
+int vgx_attn_block_seqs(vgx_attn* a, int layer, int pos, int nseq, const int16_t* qkv, int16_t* out);
 
 /* ---- LFM2 gated short convolution: replaces GPU::init_conv, set_conv_kernel,
  * conv_block's gate/conv3/gate passes and clear_conv_state

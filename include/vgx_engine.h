@@ -47,6 +47,15 @@ int vgx_engine_prefill(vgx_engine* e, const int* tokens, int n, int pos0, int16_
  * min(seq, 512), which is also the default.  Applies to vgx_engine_prefill
  * and to vgx_engine_generate's prompt. */
 int vgx_engine_set_prefill_batch(vgx_engine* e, int n);
+/* Greedy generation for nseq sequences in lockstep (no counterpart in the
+ * reference, which decodes one sequence): prompts is nseq x n_prompt, out
+ * nseq x n_gen, each row exactly what vgx_engine_generate gives for that
+ * prompt.  Each prompt is prefilled on its own KV cache, then every step runs
+ * all sequences at once (GEMMs on the int8 matrix cores over nseq rows, one
+ * attention launch).  nseq at most min(seq, 512); not for conv (hybrid)
+ * models. */
+int vgx_engine_generate_batch(vgx_engine* e, int nseq, const int* prompts, int n_prompt, int n_gen, int* out,
+                              double* prefill_ms, double* decode_ms);
 /* The message of the last failed engine call on this thread. */
 const char* vgx_engine_last_error(void);
 

@@ -113,3 +113,49 @@ def test_attention_rails(gpu, bits, hd):
         torch.cuda.synchronize()
         assert np.array_equal(got.cpu().numpy(), want), pos
     A.free()
+
+
+@pytest.mark.parametrize("bits", [16, 8])
+def test_attention_sequences_in_lockstep(gpu, bits):
+    """vgx_attn_block_seqs: nseq sequences at the same position, each on its
+    own cache, equal the oracle run on each sequence alone; a view of one
+    sequence takes the single-sequence entry points (batched append and
+    decode, row export)."""
+    dim, heads, kvh, hd, seq, nseq = 256, 4, 2, 64, 48, 3
+    rng = np.random.default_rng(11 + bits)
+    rc, rs = o.rope_cos_sin(10000.0, hd, seq)
+    rtab = o.rope_table(rc, rs)
+    qn = rng.uniform(0.5, 1.5, (1, hd)).astype(np.float32)
+    kn = rng.uniform(0.5, 1.5, (1, hd)).astype(np.float32)
+    A = gpu.attention(dim=dim, heads=heads, kv_heads=kvh, head_dim=hd, seq=seq, layers=1, kv_bits=bits,
+                      rope_half=1, qk_norm=1, rope_cos=rc, rope_sin=rs, q_norm=qn, k_norm=kn, nseq=nseq)
+    c = o.attn_cfg(dim, heads, kvh, hd, seq, bits, 1, 1)
+    rb = o.kv_row_bytes(c)
+    qnq, knq = o.quantize_act(qn[0]), o.quantize_act(kn[0])
+    kv = [np.zeros(seq * rb, np.uint8) for _ in range(nseq)]
+    width = dim + 2 * kvh * hd
+    # sequence 1's first 9 positions through a view: one batched append + decode
+    v1 = A.view(1)
+    pre = np.clip(rng.standard_normal((9, width)) * 500, -32768, 32767).astype(np.int16)
+    got = v1.block_batch(0, 0, dev(pre))
+    torch.cuda.synchronize()
+    for p in range(9):
+        want = o.attn_block(c, pre[p], qnq, knq, rtab, p, kv[1])
+        assert np.array_equal(got[p].cpu().numpy(), want), p
+    # then all three in lockstep from position 9 (sequences 0 and 2 start
+    # from caches of zeros, which the oracle mirrors)
+    for pos in range(9, 30):
+        q = np.clip(rng.standard_normal((nseq, width)) * 500, -32768, 32767).astype(np.int16)
+        out = A.block_seqs(0, pos, dev(q))
+        torch.cuda.synchronize()
+        for s in range(nseq):
+            want = o.attn_block(c, q[s], qnq, knq, rtab, pos, kv[s])
+            assert np.array_equal(out[s].cpu().numpy(), want), (s, pos)
+    for s in range(nseq):
+        assert np.array_equal(A.view(s).read_rows(0, 0, 30), kv[s][:30 * rb]), s
+    from vgx import lib as vl
+    with pytest.raises(vl.VgxError):
+        A.block_seqs(0, 30, dev(np.zeros((nseq + 1, width), np.int16)))  # more sequences than caches
+    with pytest.raises(vl.VgxError):
+        A.view(nseq)
+    A.free()

@@ -252,3 +252,52 @@ def test_engine_refusals(gpu):
         Engine(bytes(bad))  # body crc
     with pytest.raises(vl.VgxError):
         Engine(blob[:-16])  # truncated
+
+
+@pytest.mark.parametrize("scheme", ["q8", "t3", "q4"])
+def test_generate_batch_equals_single(gpu, scheme):
+    """Sequences decoded in lockstep (GEMMs over the sequences, one attention
+    launch for all of them) give exactly the tokens each prompt gives alone."""
+    spec = synth.tiny_spec(seq=48, hidden=2112 if scheme != "t3" else 96)
+    blob = synth.container(spec, scheme, seed=8)
+    prompts = np.stack([synth.prompt(7, spec.vocab, seed=s) for s in range(5)])
+    eng = Engine(blob)
+    got, pf, dc = eng.generate_batch(prompts, 12)
+    assert got.shape == (5, 12)
+    for s in range(5):
+        want, _, _ = eng.generate(prompts[s], 12)
+        assert list(got[s]) == list(want), s
+    # a second call with fewer sequences reuses the caches
+    got2, _, _ = eng.generate_batch(prompts[3:], 12)
+    assert np.array_equal(got2, got[3:])
+    eng.close()
+
+
+def test_generate_batch_minimind3_shape(gpu):
+    """The C1 model shape with 8 sequences: every row equals its own single
+    generation (q8 per-row, KV q16)."""
+    spec = synth.minimind3_spec(seq=96)
+    blob = synth.container(spec, "q8", seed=0, q8_row=True)
+    prompts = np.stack([synth.prompt(16, spec.vocab, seed=s) for s in range(8)])
+    eng = Engine(blob)
+    got, _, _ = eng.generate_batch(prompts, 24)
+    for s in (0, 5, 7):
+        want, _, _ = eng.generate(prompts[s], 24)
+        assert list(got[s]) == list(want), s
+    eng.close()
+
+
+def test_generate_batch_refusals(gpu):
+    from vgx import lib as vl
+    spec = synth.tiny_hybrid_spec(seq=16)
+    eng = Engine(synth.container(spec, "q8", seed=0))
+    with pytest.raises(vl.VgxError):
+        eng.generate_batch(np.zeros((2, 4), np.int32), 3)  # conv models decode one sequence
+    eng.close()
+    spec = synth.tiny_spec(seq=16)
+    eng = Engine(synth.container(spec, "q8", seed=0))
+    with pytest.raises(vl.VgxError):
+        eng.generate_batch(np.zeros((2, 10), np.int32), 8)  # 10 + 8 - 1 > 16
+    with pytest.raises(vl.VgxError):
+        eng.generate_batch(np.zeros((17, 4), np.int32), 2)  # more sequences than min(seq, 512)
+    eng.close()

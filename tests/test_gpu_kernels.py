@@ -310,3 +310,36 @@ def test_mat_clone_and_errors(gpu):
         gpu.upload(bad)  # cols not a multiple of 16
     with pytest.raises(vl.VgxError):
         gpu.matvec(W, x[1:])  # misaligned activation pointer
+
+
+@pytest.mark.parametrize("kind", ["q8", "t3"])
+def test_mat_concat_gemm_and_argmax_rows(gpu, kind):
+    """The LM head of the batched decode: logits tiles concatenated into one
+    matrix keep every row's scale, so its GEMM over n rows equals each tile's
+    GEMV on each row; the per-row argmax keeps the first maximum."""
+    rng = np.random.default_rng(71)
+    dim, sizes = 256, [96, 96, 40]
+    tiles = [q8_matrix(rng, r, dim) if kind == "q8" else t3_matrix(rng, r, dim) for r in sizes]
+    mats = [gpu.upload(t) for t in tiles]
+    cat = gpu.concat(mats)
+    assert cat.rows == sum(sizes)
+    X = np.stack([rand_x(rng, dim) for _ in range(5)])
+    got = host(gpu.gemm(cat, dev(X)))
+    for i in range(5):
+        want = np.concatenate([o.store(oracle_rowval(t, X[i])) for t in tiles])
+        assert np.array_equal(got[i], want), i
+    V = rng.integers(-300, 300, (7, 1000)).astype(np.int16)
+    V[2, [5, 900]] = 400  # ties: the first maximum wins
+    V[4] = 0
+    assert np.array_equal(host(gpu.argmax_rows(dev(V))), [o.argmax_i16(v) for v in V])
+    from vgx import lib as vl
+    with pytest.raises(vl.VgxError):
+        gpu.concat([mats[0], gpu.upload(q4_matrix(rng, 32, dim))])  # q4 scales are per matrix
+    if kind == "t3":
+        odd_t = t3_matrix(rng, 33, dim)
+        odd = gpu.upload(odd_t)
+        with pytest.raises(vl.VgxError):
+            gpu.concat([odd, mats[0]])  # an odd t3 matrix must come last
+        cat2 = gpu.concat([mats[0], odd])
+        want = np.concatenate([o.store(oracle_rowval(tiles[0], X[0])), o.store(oracle_rowval(odd_t, X[0]))])
+        assert np.array_equal(host(gpu.gemm(cat2, dev(X[:1])))[0], want)

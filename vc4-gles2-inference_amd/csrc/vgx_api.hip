@@ -222,6 +222,53 @@ int vgx_mat_clone(vgx_ctx* ctx, const vgx_mat* src, vgx_mat** out) {
     return VGX_OK;
 }
 
+int vgx_mat_concat(vgx_ctx* ctx, int n, vgx_mat* const* mats, vgx_mat** out) {
+    if (!ctx || !mats || !out || n <= 0) return vgx_fail(VGX_EINVAL, "vgx_mat_concat: NULL argument or n <= 0");
+    *out = nullptr;
+    const MatDev& a = mats[0]->d;
+    if (a.kind == VGX_Q4) return vgx_fail(VGX_EINVAL, "vgx_mat_concat: q4 scales are per matrix; q8 and t3 only");
+    size_t body = 0, plane = 0;
+    long long rows = 0;
+    for (int i = 0; i < n; ++i) {
+        if (!mats[i]) return vgx_fail(VGX_EINVAL, "vgx_mat_concat: NULL matrix");
+        const MatDev& d = mats[i]->d;
+        if (d.kind != a.kind || d.cols != a.cols) return vgx_fail(VGX_EINVAL, "vgx_mat_concat: kinds or cols differ");
+        if (d.kind == VGX_T3 && (d.rows % 2) && i != n - 1)
+            return vgx_fail(VGX_EINVAL, "vgx_mat_concat: a t3 matrix before the last has an odd row count");
+        body += mats[i]->body_bytes;
+        plane += mats[i]->plane_bytes;
+        rows += d.rows;
+    }
+    if (rows > (1 << 30)) return vgx_fail(VGX_EINVAL, "vgx_mat_concat: too many rows");
+    VGX_HIP(hipSetDevice(ctx->device));
+    vgx_mat* m = new vgx_mat();
+    m->d = a;
+    m->d.rows = (int)rows;
+    m->d.out_off = m->d.blk_off = 0;
+    m->body_bytes = body;
+    m->plane_bytes = plane;
+    hipError_t e = hipMalloc(&m->body_alloc, body);
+    if (e == hipSuccess) e = hipMalloc(&m->plane_alloc, plane);
+    size_t bo = 0, po = 0;
+    for (int i = 0; i < n && e == hipSuccess; ++i) {
+        e = hipMemcpyAsync(static_cast<uint8_t*>(m->body_alloc) + bo, mats[i]->body_alloc, mats[i]->body_bytes,
+                           hipMemcpyDeviceToDevice, ctx->stream);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(static_cast<uint8_t*>(m->plane_alloc) + po, mats[i]->plane_alloc,
+                               mats[i]->plane_bytes, hipMemcpyDeviceToDevice, ctx->stream);
+        bo += mats[i]->body_bytes;
+        po += mats[i]->plane_bytes;
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) { vgx_mat_free(m); return vgx_hip_fail(e, "vgx_mat_concat"); }
+    m->d.body = static_cast<const uint8_t*>(m->body_alloc);
+    m->d.wsr = static_cast<const float*>(m->plane_alloc);
+    int st = mat_finish(ctx, m);
+    if (st != VGX_OK) { vgx_mat_free(m); return st; }
+    *out = m;
+    return VGX_OK;
+}
+
 int vgx_mat_free(vgx_mat* m) {
     if (!m) return VGX_OK;
     if (m->body_alloc) (void)hipFree(m->body_alloc);
@@ -446,7 +493,14 @@ int vgx_logits_argmax(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, int16_
     if (!token || !logits) return vgx_fail(VGX_EINVAL, "vgx_logits_argmax: NULL output");
     int st = launch_group(ctx, g, x, nullptr, logits);
     if (st != VGX_OK) return st;
-    return vgx_argmax_launch(logits, g->rows, token, ctx->stream);
+    return vgx_argmax_launch(logits, g->rows, 1, token, ctx->stream);
+}
+
+int vgx_argmax_rows(vgx_ctx* ctx, int nrows, int n, const int16_t* v, int* tokens) {
+    if (!ctx || !v || !tokens) return vgx_fail(VGX_EINVAL, "vgx_argmax_rows: NULL argument");
+    if (nrows <= 0 || nrows > 65535 || n <= 0) return vgx_fail(VGX_EINVAL, "vgx_argmax_rows: empty or oversized shape");
+    VGX_HIP(hipSetDevice(ctx->device));
+    return vgx_argmax_launch(v, n, nrows, tokens, ctx->stream);
 }
 
 int vgx_gemv_group_rms(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, const int16_t* rms_w, float eps,

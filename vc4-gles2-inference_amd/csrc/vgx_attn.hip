@@ -59,6 +59,9 @@ struct vgx_attn {
     int16_t* qn = nullptr;     // [layers][hd] q16
     int16_t* kn = nullptr;
     size_t lds = 0;
+    int nseq = 1;           // sequences whose caches follow one another in each layer
+    size_t seq_bytes = 0;   // one sequence's cache of one layer: seq rows
+    bool owner = true;      // false for a view of one sequence (shares every buffer)
 };
 
 namespace {
@@ -201,7 +204,8 @@ template <int KVB>
 __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t* kv, const int32_t* rtab,
                                                         const int16_t* qn, const int16_t* kn,
                                                         const int16_t* qkv, int16_t* out, int pos0,
-                                                        int do_write, int do_attend) {
+                                                        int do_write, int do_attend, size_t seq_stride,
+                                                        int pos_step) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int E = KVB == 16 ? 2 : 4;  // values per 32-bit word
     constexpr int KP = kKPre<KVB>;
@@ -215,7 +219,11 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     // blockIdx.y: the position's offset in a batch of consecutive positions,
     // whose qkv and output rows are consecutive rows
-    const int pos = pos0 + blockIdx.y;
+    // (blockIdx.y: a batch of consecutive positions of one sequence, pos_step
+    // 1; or the same position of consecutive sequences, each with its own
+    // cache seq_stride bytes on, pos_step 0)
+    const int pos = pos0 + blockIdx.y * pos_step;
+    kv += (size_t)blockIdx.y * seq_stride;
     qkv += (size_t)blockIdx.y * (A.dim + 2 * kv_dim);
     if (out) out += (size_t)blockIdx.y * A.dim;
     const int npos = pos + 1;
@@ -541,27 +549,38 @@ size_t attn_layout(AttnDev& A) {
 // Positions pos .. pos + ntok - 1 (their qkv and output rows consecutive).
 // With ntok > 1 the KV write and the attention must be separate launches: a
 // position reads the rows the others write.
-int launch(vgx_attn* at, int layer, int pos, int ntok, const int16_t* qkv, int16_t* out, int w, int att) {
+int launch(vgx_attn* at, int layer, int pos, int ntok, const int16_t* qkv, int16_t* out, int w, int att,
+           bool seqs = false) {
     if (!at) return vgx_fail(VGX_EINVAL, "attention: NULL handle");
     if (layer < 0 || layer >= at->layers || !at->kv[layer])
         return vgx_fail(VGX_ERANGE, "attention: layer " + std::to_string(layer) + " has no KV cache");
     if (ntok <= 0 || ntok > 65535) return vgx_fail(VGX_EINVAL, "attention: ntok outside 1..65535");
-    if (pos < 0 || pos > at->a.seq - ntok)
-        return vgx_fail(VGX_ERANGE, "attention: positions " + std::to_string(pos) + ".." +
-                                        std::to_string(pos + ntok - 1) + " outside the KV length");
+    if (seqs) {
+        if (ntok > at->nseq)
+            return vgx_fail(VGX_ERANGE, "attention: " + std::to_string(ntok) + " sequences, the cache holds " +
+                                            std::to_string(at->nseq));
+        if (pos < 0 || pos >= at->a.seq)
+            return vgx_fail(VGX_ERANGE, "attention: position " + std::to_string(pos) + " outside the KV length");
+    } else {
+        if (pos < 0 || pos > at->a.seq - ntok)
+            return vgx_fail(VGX_ERANGE, "attention: positions " + std::to_string(pos) + ".." +
+                                            std::to_string(pos + ntok - 1) + " outside the KV length");
+        if (ntok > 1 && w && att) return vgx_fail(VGX_EINVAL, "attention: a batch writes its KV rows first");
+    }
     if (!qkv || (att && !out)) return vgx_fail(VGX_EINVAL, "attention: NULL buffer");
-    if (ntok > 1 && w && att) return vgx_fail(VGX_EINVAL, "attention: a batch writes its KV rows first");
     VGX_HIP(hipSetDevice(at->ctx->device));
     const AttnDev& A = at->a;
     const int16_t* qn = at->qn ? at->qn + (size_t)layer * A.hd : nullptr;
     const int16_t* kn = at->kn ? at->kn + (size_t)layer * A.hd : nullptr;
     const dim3 grid(att ? A.heads : A.kv_heads, ntok);
+    const size_t stride = seqs ? at->seq_bytes : 0;
+    const int step = seqs ? 0 : 1;
     if (A.kv_bits == 16)
         hipLaunchKernelGGL(attn_kernel<16>, grid, dim3(kThreads), at->lds, at->ctx->stream, A,
-                           at->kv[layer], at->rtab, qn, kn, qkv, out, pos, w, att);
+                           at->kv[layer], at->rtab, qn, kn, qkv, out, pos, w, att, stride, step);
     else
         hipLaunchKernelGGL(attn_kernel<8>, grid, dim3(kThreads), at->lds, at->ctx->stream, A,
-                           at->kv[layer], at->rtab, qn, kn, qkv, out, pos, w, att);
+                           at->kv[layer], at->rtab, qn, kn, qkv, out, pos, w, att, stride, step);
     VGX_LAUNCH_CHECK("attention launch");
     return VGX_OK;
 }
@@ -571,8 +590,13 @@ int launch(vgx_attn* at, int layer, int pos, int ntok, const int16_t* qkv, int16
 extern "C" {
 
 int vgx_attn_create(vgx_ctx* ctx, const vgx_attn_desc* d, vgx_attn** out) {
+    return vgx_attn_create_seqs(ctx, d, 1, out);
+}
+
+int vgx_attn_create_seqs(vgx_ctx* ctx, const vgx_attn_desc* d, int nseq, vgx_attn** out) {
     if (!ctx || !d || !out) return vgx_fail(VGX_EINVAL, "vgx_attn_create: NULL argument");
     *out = nullptr;
+    if (nseq <= 0 || nseq > 65535) return vgx_fail(VGX_EINVAL, "vgx_attn_create_seqs: nseq outside 1..65535");
     if (d->dim <= 0 || d->heads <= 0 || d->kv_heads <= 0 || d->head_dim <= 0 || d->seq <= 0 || d->layers <= 0)
         return vgx_fail(VGX_EINVAL, "vgx_attn_create: empty shape");
     if (d->heads % d->kv_heads) return vgx_fail(VGX_EINVAL, "vgx_attn_create: heads not a multiple of kv_heads");
@@ -597,7 +621,9 @@ int vgx_attn_create(vgx_ctx* ctx, const vgx_attn_desc* d, vgx_attn** out) {
         return vgx_fail(VGX_EINVAL, "vgx_attn_create: seq too long for one workgroup's LDS");
     }
     auto fail = [&](hipError_t e, const char* w) { vgx_attn_free(at); return vgx_hip_fail(e, w); };
-    const size_t lb = (size_t)A.seq * A.row_bytes;
+    at->nseq = nseq;
+    at->seq_bytes = (size_t)A.seq * A.row_bytes;
+    const size_t lb = at->seq_bytes * nseq;
     at->kv.assign((size_t)d->layers, nullptr);
     for (int l = 0; l < d->layers; ++l) {
         if (d->layer_is_attn && !d->layer_is_attn[l]) continue;
@@ -636,8 +662,25 @@ int vgx_attn_create(vgx_ctx* ctx, const vgx_attn_desc* d, vgx_attn** out) {
     return VGX_OK;
 }
 
+int vgx_attn_seq_view(vgx_attn* a, int s, vgx_attn** out) {
+    if (!a || !out) return vgx_fail(VGX_EINVAL, "vgx_attn_seq_view: NULL argument");
+    *out = nullptr;
+    if (s < 0 || s >= a->nseq) return vgx_fail(VGX_ERANGE, "vgx_attn_seq_view: no such sequence");
+    vgx_attn* v = new vgx_attn(*a);
+    v->owner = false;
+    v->nseq = 1;
+    for (auto& p : v->kv)
+        if (p) p += (size_t)s * a->seq_bytes;
+    *out = v;
+    return VGX_OK;
+}
+
 int vgx_attn_free(vgx_attn* at) {
     if (!at) return VGX_OK;
+    if (!at->owner) {
+        delete at;
+        return VGX_OK;
+    }
     for (uint8_t* p : at->kv) if (p) (void)hipFree(p);
     if (at->rtab) (void)hipFree(at->rtab);
     if (at->qn) (void)hipFree(at->qn);
@@ -656,6 +699,10 @@ int vgx_attn_decode(vgx_attn* a, int layer, int pos, const int16_t* qkv, int16_t
 
 int vgx_attn_block(vgx_attn* a, int layer, int pos, const int16_t* qkv, int16_t* out) {
     return launch(a, layer, pos, 1, qkv, out, 1, 1);
+}
+
+int vgx_attn_block_seqs(vgx_attn* a, int layer, int pos, int nseq, const int16_t* qkv, int16_t* out) {
+    return launch(a, layer, pos, nseq, qkv, out, 1, 1, true);
 }
 
 int vgx_kv_append_batch(vgx_attn* a, int layer, int pos0, int ntok, const int16_t* qkv) {

@@ -779,8 +779,11 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
 }
 
 // argmax with the first-maximum rule over int16 values, one block.
+// Row blockIdx.x of a row-major [rows][n] array; out[blockIdx.x].
 __global__ void __launch_bounds__(1024) argmax_kernel(const int16_t* v, int n, int* out) {
     __shared__ int sv[16], si[16];
+    v += (size_t)blockIdx.x * n;
+    out += blockIdx.x;
     int best = -65536, bi = 0x7fffffff;
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
         int x = v[i];
@@ -922,8 +925,8 @@ int vgx_gemv_launch(const GemvLaunch& L, hipStream_t s) {
     return VGX_OK;
 }
 
-int vgx_argmax_launch(const int16_t* v, int n, int* out, hipStream_t s) {
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, v, n, out);
+int vgx_argmax_launch(const int16_t* v, int n, int rows, int* out, hipStream_t s) {
+    hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(1024), 0, s, v, n, out);
     VGX_LAUNCH_CHECK("argmax launch");
     return VGX_OK;
 }

@@ -119,5 +119,5 @@ struct GemvLaunch {
 
 int vgx_gemv_plan(int kind, int rows, int cols, int num_cu, int* lpr, int* ri, int* rows_per_block);
 int vgx_gemv_launch(const GemvLaunch& L, hipStream_t s);
-int vgx_argmax_launch(const int16_t* v, int n, int* out, hipStream_t s);
+int vgx_argmax_launch(const int16_t* v, int n, int rows, int* out, hipStream_t s);
 int vgx_dequant_launch(const MatDev& d, float* out, hipStream_t s);

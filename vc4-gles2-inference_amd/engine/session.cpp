@@ -42,6 +42,9 @@ struct vgx_engine {
     std::vector<Layer> L;
     std::vector<vgx_mat*> head_tiles;
     vgx_group* head = nullptr;
+    vgx_attn_desc attn_desc{};  // with the host tables it points into
+    std::vector<float> rope_c, rope_s;
+    std::vector<uint8_t> attn_flag;
     int8_t* emb = nullptr;
     float* emb_scale = nullptr;
     int16_t *h = nullptr, *x1 = nullptr, *qkv = nullptr, *att = nullptr, *hbuf = nullptr;
@@ -52,6 +55,14 @@ struct vgx_engine {
     // batches of pbatch (serial steps when pbatch < 2)
     int pcap = 0, pbatch = 0;
     int16_t *bh = nullptr, *bx1 = nullptr, *bxn = nullptr, *bqkv = nullptr, *batt = nullptr, *bhid = nullptr;
+    // batched decode of nseq sequences in lockstep: their KV caches, the LM
+    // head as one matrix, nseq rows of logits, the token history
+    vgx_attn* attn_b = nullptr;
+    int nseq_b = 0;
+    vgx_mat* head_cat = nullptr;
+    int16_t* blog = nullptr;
+    int* btok = nullptr;
+    size_t btok_cap = 0;
     std::vector<void*> allocs;
 
     ~vgx_engine() {
@@ -61,6 +72,8 @@ struct vgx_engine {
         }
         vgx_group_free(head);
         for (vgx_mat* t : head_tiles) vgx_mat_free(t);
+        vgx_mat_free(head_cat);
+        vgx_attn_free(attn_b);
         vgx_attn_free(attn);
         vgx_conv_free(conv);
         for (void* p : allocs) (void)hipFree(p);
@@ -240,7 +253,10 @@ struct vgx_engine {
         if ((st = vgx_group_create(ctx, (int)head_tiles.size(), head_tiles.data(), &head))) return st;
         // attention state: Session's rope tables (engine/src/session.cpp:188-202)
         const int half = hd / 2;
-        std::vector<float> rc((size_t)seq * half), rs((size_t)seq * half);
+        std::vector<float>& rc = rope_c;
+        std::vector<float>& rs = rope_s;
+        rc.assign((size_t)seq * half, 0.0f);
+        rs.assign((size_t)seq * half, 0.0f);
         for (int p = 0; p < seq; ++p)
             for (int i = 0; i < half; ++i) {
                 float freq = 1.0f / powf(m.theta, (2.0f * i) / hd);
@@ -248,7 +264,8 @@ struct vgx_engine {
                 rc[(size_t)p * half + i] = cosf(a);
                 rs[(size_t)p * half + i] = sinf(a);
             }
-        vgx_attn_desc ad{};
+        vgx_attn_desc& ad = attn_desc;
+        ad = vgx_attn_desc{};
         ad.dim = D; ad.heads = m.heads; ad.kv_heads = m.kv_heads; ad.head_dim = hd; ad.seq = seq;
         ad.layers = m.layers; ad.kv_bits = kv_bits; ad.rope_half = m.rope_half; ad.qk_norm = m.qk_norm;
         ad.rope_cos = rc.data(); ad.rope_sin = rs.data();
@@ -260,7 +277,7 @@ struct vgx_engine {
             ad.q_norm = reinterpret_cast<const float*>(qn->body);
             ad.k_norm = reinterpret_cast<const float*>(kn->body);
         }
-        std::vector<uint8_t> attn_flag((size_t)m.layers);
+        attn_flag.assign((size_t)m.layers, 0);
         for (int l = 0; l < m.layers; ++l) attn_flag[l] = is_conv(l) ? 0 : 1;
         ad.layer_is_attn = attn_flag.data();
         if ((st = vgx_attn_create(ctx, &ad, &attn))) return st;
@@ -286,7 +303,7 @@ struct vgx_engine {
     // consumes it (the attention norm in the qkv draw, the FFN norm in the
     // gate, the final norm in the LM head with its argmax): five launches a
     // layer.
-    int forward(const int* token_dev, int pos, bool want_logits, int* next_dev) {
+    int forward(const int* token_dev, int pos, bool want_logits, int* next_dev, vgx_attn* A) {
         int st;
         const int D = m.dim;
         const float eps = m.rms_eps;
@@ -302,7 +319,7 @@ struct vgx_engine {
                 if ((st = vgx_gemv(ctx, ly.conv_out, att, h, x1))) return st;
             } else {
                 if ((st = vgx_gemv_rms(ctx, ly.qkv, h, ly.rms_att, eps, nullptr, qkv))) return st;
-                if ((st = vgx_attn_block(attn, l, pos, qkv, att))) return st;
+                if ((st = vgx_attn_block(A, l, pos, qkv, att))) return st;
                 if ((st = vgx_gemv(ctx, ly.wo, att, h, x1))) return st;
             }
             if ((st = vgx_ffn_gate_rms(ctx, ly.w1, ly.w3, x1, ly.rms_ffn, eps, ly.hs, hbuf))) return st;
@@ -320,7 +337,7 @@ struct vgx_engine {
     // n positions appended before any of them attends.  Every row is the exact
     // result of forward() on that position, so the logits of the last one are
     // identical to the serial loop's.
-    int prefill(const int* toks_dev, int pos0, int n, bool want_logits, int* next_dev) {
+    int prefill(const int* toks_dev, int pos0, int n, bool want_logits, int* next_dev, vgx_attn* A) {
         int st;
         const int D = m.dim;
         const float eps = m.rms_eps;
@@ -337,8 +354,8 @@ struct vgx_engine {
                 if ((st = vgx_gemm(ctx, ly.conv_out, n, batt, bh, bx1))) return st;
             } else {
                 if ((st = vgx_gemm(ctx, ly.qkv, n, bxn, nullptr, bqkv))) return st;
-                if ((st = vgx_kv_append_batch(attn, l, pos0, n, bqkv))) return st;
-                if ((st = vgx_attn_decode_batch(attn, l, pos0, n, bqkv, batt))) return st;
+                if ((st = vgx_kv_append_batch(A, l, pos0, n, bqkv))) return st;
+                if ((st = vgx_attn_decode_batch(A, l, pos0, n, bqkv, batt))) return st;
                 if ((st = vgx_gemm(ctx, ly.wo, n, batt, bh, bx1))) return st;
             }
             if ((st = vgx_rmsnorm_batch(ctx, n, D, bx1, ly.rms_ffn, eps, bxn))) return st;
@@ -352,19 +369,66 @@ struct vgx_engine {
     }
 
     // The prompt tokens at toks_dev[0..n) for positions pos0.., in batches of
-    // up to pbatch (one position at a time when pbatch < 2).
-    int run_prompt(const int* toks_dev, int pos0, int n, int* next_dev) {
+    // up to pbatch (one position at a time when pbatch < 2), on the KV cache A.
+    int run_prompt(const int* toks_dev, int pos0, int n, int* next_dev, vgx_attn* A) {
         int st;
         if (pbatch < 2) {
             for (int p = 0; p < n; ++p)
-                if ((st = forward(toks_dev + p, pos0 + p, p == n - 1, next_dev))) return st;
+                if ((st = forward(toks_dev + p, pos0 + p, p == n - 1, next_dev, A))) return st;
             return VGX_OK;
         }
         for (int p = 0; p < n; p += pbatch) {
             const int b = n - p < pbatch ? n - p : pbatch;
-            if ((st = prefill(toks_dev + p, pos0 + p, b, p + b == n, next_dev))) return st;
+            if ((st = prefill(toks_dev + p, pos0 + p, b, p + b == n, next_dev, A))) return st;
         }
         return VGX_OK;
+    }
+
+    // Caches and buffers for nseq sequences in lockstep (kept for later calls
+    // with as many or fewer).
+    int ensure_batch(int nseq, size_t ntok) {
+        int st;
+        if (conv) return fail(VGX_EINVAL, "batched decode: conv (hybrid) models are not supported");
+        if (nseq > pcap) return fail(VGX_EINVAL, "batched decode: more than " + std::to_string(pcap) + " sequences");
+        if (!head_cat && (st = vgx_mat_concat(ctx, (int)head_tiles.size(), head_tiles.data(), &head_cat))) return st;
+        if (nseq > nseq_b) {
+            vgx_attn_free(attn_b);
+            attn_b = nullptr;
+            nseq_b = 0;
+            if ((st = vgx_attn_create_seqs(ctx, &attn_desc, nseq, &attn_b))) return st;
+            if ((st = dalloc(&blog, (size_t)nseq * m.vocab))) return st;
+            nseq_b = nseq;
+        }
+        if (ntok > btok_cap) {
+            if ((st = dalloc(&btok, ntok))) return st;
+            btok_cap = ntok;
+        }
+        return VGX_OK;
+    }
+
+    // One position of nseq sequences at once: forward() on each row, the
+    // GEMVs as GEMMs over the nseq rows, the attention of every sequence on
+    // its own cache in one launch, the final norm + LM head + argmax per row.
+    int forward_seqs(const int* toks_dev, int pos, int nseq, int* next_dev) {
+        int st;
+        const int D = m.dim;
+        const float eps = m.rms_eps;
+        if ((st = vgx_embed_q8_batch(ctx, emb, emb_scale, m.vocab, D, nseq, toks_dev, bh))) return st;
+        for (int l = 0; l < m.layers; ++l) {
+            Layer& ly = L[l];
+            if ((st = vgx_rmsnorm_batch(ctx, nseq, D, bh, ly.rms_att, eps, bxn))) return st;
+            if ((st = vgx_gemm(ctx, ly.qkv, nseq, bxn, nullptr, bqkv))) return st;
+            if ((st = vgx_attn_block_seqs(attn_b, l, pos, nseq, bqkv, batt))) return st;
+            if ((st = vgx_gemm(ctx, ly.wo, nseq, batt, bh, bx1))) return st;
+            if ((st = vgx_rmsnorm_batch(ctx, nseq, D, bx1, ly.rms_ffn, eps, bxn))) return st;
+            if ((st = vgx_ffn_gate_batch(ctx, ly.w1, ly.w3, nseq, bxn, ly.hs, bhid))) return st;
+            if (ffn_chunk) st = vgx_gemm_add_split(ctx, ly.w2, ffn_chunk, nseq, bhid, bx1, bh);
+            else st = vgx_gemm(ctx, ly.w2, nseq, bhid, bx1, bh);
+            if (st) return st;
+        }
+        if ((st = vgx_rmsnorm_batch(ctx, nseq, D, bh, rms_final, eps, bxn))) return st;
+        if ((st = vgx_gemm(ctx, head_cat, nseq, bxn, nullptr, blog))) return st;
+        return vgx_argmax_rows(ctx, nseq, m.vocab, blog, next_dev);
     }
 };
 
@@ -424,7 +488,7 @@ int vgx_engine_step(vgx_engine* e, int token, int pos, int16_t* logits_host, int
     int* slot = e->toks + e->seq;
     if (hipMemcpyAsync(slot, &token, sizeof(int), hipMemcpyHostToDevice, s) != hipSuccess)
         return fail(VGX_EHIP, "token upload");
-    int st = e->forward(slot, pos, true, slot);
+    int st = e->forward(slot, pos, true, slot, e->attn);
     if (st) return st;
     if (logits_host && hipMemcpyAsync(logits_host, e->logits, (size_t)e->m.vocab * 2, hipMemcpyDeviceToHost, s) != hipSuccess)
         return fail(VGX_EHIP, "logits readback");
@@ -451,11 +515,11 @@ int vgx_engine_generate(vgx_engine* e, const int* prompt, int n_prompt, int n_ge
     if (hipDeviceSynchronize() != hipSuccess) return fail(VGX_EHIP, "sync");
     auto t0 = std::chrono::steady_clock::now();
     int st;
-    if ((st = e->run_prompt(e->toks, 0, n_prompt, gen))) return st;
+    if ((st = e->run_prompt(e->toks, 0, n_prompt, gen, e->attn))) return st;
     if (hipStreamSynchronize(s) != hipSuccess) return fail(VGX_EHIP, "prefill sync");
     auto t1 = std::chrono::steady_clock::now();
     for (int i = 1; i < n_gen; ++i)
-        if ((st = e->forward(gen + i - 1, n_prompt + i - 1, true, gen + i))) return st;
+        if ((st = e->forward(gen + i - 1, n_prompt + i - 1, true, gen + i, e->attn))) return st;
     if (hipStreamSynchronize(s) != hipSuccess) return fail(VGX_EHIP, "decode sync");
     auto t2 = std::chrono::steady_clock::now();
     if (hipMemcpy(out, gen, (size_t)n_gen * sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
@@ -486,7 +550,7 @@ int vgx_engine_prefill(vgx_engine* e, const int* tokens, int n, int pos0, int16_
     int* slot = e->toks + e->seq;
     if (hipMemcpyAsync(dst, tokens, (size_t)n * sizeof(int), hipMemcpyHostToDevice, s) != hipSuccess)
         return fail(VGX_EHIP, "token upload");
-    int st = e->run_prompt(dst, pos0, n, slot);
+    int st = e->run_prompt(dst, pos0, n, slot, e->attn);
     if (st) return st;
     if (logits_host && hipMemcpyAsync(logits_host, e->logits, (size_t)e->m.vocab * 2, hipMemcpyDeviceToHost, s) != hipSuccess)
         return fail(VGX_EHIP, "logits readback");
@@ -494,6 +558,51 @@ int vgx_engine_prefill(vgx_engine* e, const int* tokens, int n, int pos0, int16_
     if (hipMemcpyAsync(&nx, slot, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess) return fail(VGX_EHIP, "token readback");
     if (hipStreamSynchronize(s) != hipSuccess) return fail(VGX_EHIP, "prefill sync");
     if (next) *next = nx;
+    return VGX_OK;
+}
+
+int vgx_engine_generate_batch(vgx_engine* e, int nseq, const int* prompts, int n_prompt, int n_gen, int* out,
+                              double* prefill_ms, double* decode_ms) {
+    g_err.clear();
+    if (!e || !prompts || !out) return fail(VGX_EINVAL, "vgx_engine_generate_batch: NULL argument");
+    if (nseq <= 0) return fail(VGX_EINVAL, "vgx_engine_generate_batch: nseq <= 0");
+    if (n_prompt <= 0 || n_gen <= 0 || n_prompt + n_gen - 1 > e->seq)
+        return fail(VGX_ERANGE, "vgx_engine_generate_batch: prompt + generation longer than the KV length");
+    const size_t np = (size_t)nseq * n_prompt, ng = (size_t)nseq * n_gen;
+    for (size_t i = 0; i < np; ++i)
+        if (prompts[i] < 0 || prompts[i] >= e->m.vocab) return fail(VGX_EINVAL, "prompt token outside the vocabulary");
+    int st;
+    if ((st = e->ensure_batch(nseq, np + ng))) return st;
+    hipStream_t s = static_cast<hipStream_t>(vgx_ctx_stream(e->ctx));
+    // device tokens: the prompts [nseq][n_prompt], then the generated tokens
+    // step-major [n_gen][nseq] (one step's tokens are the next step's input)
+    int* dprompt = e->btok;
+    int* gen = e->btok + np;
+    if (hipMemcpy(dprompt, prompts, np * sizeof(int), hipMemcpyHostToDevice) != hipSuccess)
+        return fail(VGX_EHIP, "prompt upload");
+    if (hipDeviceSynchronize() != hipSuccess) return fail(VGX_EHIP, "sync");
+    auto t0 = std::chrono::steady_clock::now();
+    for (int q = 0; q < nseq; ++q) {
+        vgx_attn* view = nullptr;
+        if ((st = vgx_attn_seq_view(e->attn_b, q, &view))) return st;
+        st = e->run_prompt(dprompt + (size_t)q * n_prompt, 0, n_prompt, gen + q, view);
+        vgx_attn_free(view);
+        if (st) return st;
+    }
+    if (hipStreamSynchronize(s) != hipSuccess) return fail(VGX_EHIP, "prefill sync");
+    auto t1 = std::chrono::steady_clock::now();
+    for (int i = 1; i < n_gen; ++i)
+        if ((st = e->forward_seqs(gen + (size_t)(i - 1) * nseq, n_prompt + i - 1, nseq, gen + (size_t)i * nseq)))
+            return st;
+    if (hipStreamSynchronize(s) != hipSuccess) return fail(VGX_EHIP, "decode sync");
+    auto t2 = std::chrono::steady_clock::now();
+    std::vector<int> g(ng);
+    if (hipMemcpy(g.data(), gen, ng * sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
+        return fail(VGX_EHIP, "token readback");
+    for (int q = 0; q < nseq; ++q)
+        for (int i = 0; i < n_gen; ++i) out[(size_t)q * n_gen + i] = g[(size_t)i * nseq + q];
+    if (prefill_ms) *prefill_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+    if (decode_ms) *decode_ms = std::chrono::duration<double, std::milli>(t2 - t1).count();
     return VGX_OK;
 }
 

@@ -21,6 +21,8 @@ _SIGS = {
                                  ctypes.POINTER(ctypes.c_double)]),
     "vgx_engine_prefill": (_I, [_P, _P, _I, _I, _P, ctypes.POINTER(_I)]),
     "vgx_engine_set_prefill_batch": (_I, [_P, _I]),
+    "vgx_engine_generate_batch": (_I, [_P, _I, _P, _I, _I, _P, ctypes.POINTER(ctypes.c_double),
+                                       ctypes.POINTER(ctypes.c_double)]),
     "vgx_engine_last_error": (ctypes.c_char_p, []),
 }
 _lib = None
@@ -93,6 +95,17 @@ class Engine:
         pf, dc = ctypes.c_double(), ctypes.c_double()
         _check(load().vgx_engine_generate(self.h, p.ctypes.data, p.size, n_gen, out.ctypes.data,
                                           ctypes.byref(pf), ctypes.byref(dc)))
+        return out, pf.value, dc.value
+
+    def generate_batch(self, prompts, n_gen):
+        """Greedy generation for the rows of prompts (nseq x n_prompt) in
+        lockstep: (nseq x n_gen tokens, prefill_ms, decode_ms)."""
+        p = np.ascontiguousarray(prompts, np.int32)
+        nseq, n_prompt = p.shape
+        out = np.empty((nseq, n_gen), np.int32)
+        pf, dc = ctypes.c_double(), ctypes.c_double()
+        _check(load().vgx_engine_generate_batch(self.h, nseq, p.ctypes.data, n_prompt, n_gen, out.ctypes.data,
+                                                ctypes.byref(pf), ctypes.byref(dc)))
         return out, pf.value, dc.value
 
     def close(self):

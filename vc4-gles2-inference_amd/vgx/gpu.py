@@ -146,7 +146,7 @@ class Attention:
     """GPU::init_attention's state: KV cache, RoPE table, q/k norm weights."""
 
     def __init__(self, gpu, dim, heads, kv_heads, head_dim, seq, layers, kv_bits, rope_half, qk_norm,
-                 rope_cos, rope_sin, q_norm=None, k_norm=None, layer_is_attn=None):
+                 rope_cos, rope_sin, q_norm=None, k_norm=None, layer_is_attn=None, nseq=1):
         L = _l.load()
         self._keep = [np.ascontiguousarray(rope_cos, np.float32), np.ascontiguousarray(rope_sin, np.float32),
                       None if q_norm is None else np.ascontiguousarray(q_norm, np.float32),
@@ -156,9 +156,26 @@ class Attention:
                         _np_ptr(self._keep[0]), _np_ptr(self._keep[1]), _np_ptr(self._keep[2]),
                         _np_ptr(self._keep[3]), _np_ptr(self._keep[4]))
         h = ctypes.c_void_p()
-        _l.check(L.vgx_attn_create(gpu.ctx, ctypes.byref(d), ctypes.byref(h)))
-        self.gpu, self.h, self.dim, self.seq = gpu, h, dim, seq
+        _l.check(L.vgx_attn_create_seqs(gpu.ctx, ctypes.byref(d), nseq, ctypes.byref(h)))
+        self.gpu, self.h, self.dim, self.seq, self.nseq = gpu, h, dim, seq, nseq
         self.row_bytes = int(L.vgx_kv_row_bytes(h))
+        self.views = []
+
+    def view(self, s):
+        """Sequence s's cache as a single-sequence Attention (freed with the parent)."""
+        h = ctypes.c_void_p()
+        _l.check(_l.load().vgx_attn_seq_view(self.h, s, ctypes.byref(h)))
+        v = Attention.__new__(Attention)
+        v.gpu, v.h, v.dim, v.seq, v.nseq, v.row_bytes, v.views = self.gpu, h, self.dim, self.seq, 1, self.row_bytes, []
+        self.views.append(v)
+        return v
+
+    def block_seqs(self, layer, pos, qkv, out=None):
+        """Position pos of the sequences 0..n-1 for the n rows of qkv."""
+        n = qkv.shape[0]
+        out = out if out is not None else torch.empty((n, self.dim), dtype=torch.int16, device=qkv.device)
+        _l.check(_l.load().vgx_attn_block_seqs(self.h, layer, pos, n, _ptr(qkv), _ptr(out)))
+        return out
 
     def kv_append(self, layer, pos, qkv):
         _l.check(_l.load().vgx_kv_append(self.h, layer, pos, _ptr(qkv)))
@@ -193,6 +210,8 @@ class Attention:
         _l.check(_l.load().vgx_kv_write_rows(self.h, layer, row0, data.size // self.row_bytes, _np_ptr(data)))
 
     def free(self):
+        for v in getattr(self, "views", []):
+            v.free()
         if self.h:
             _l.load().vgx_attn_free(self.h)
             self.h = None
@@ -250,6 +269,21 @@ class GPU:
 
     def group(self, mats):
         return Group(self, mats)
+
+    def concat(self, mats):
+        """One matrix with the rows of mats in order (q8 or t3, equal cols)."""
+        arr = (ctypes.c_void_p * len(mats))(*[m.h for m in mats])
+        h = ctypes.c_void_p()
+        _l.check(_l.load().vgx_mat_concat(self.ctx, len(mats), arr, ctypes.byref(h)))
+        c = Mat.__new__(Mat)
+        c.gpu, c.h, c.rows, c.cols, c.kind = self, h, sum(m.rows for m in mats), mats[0].cols, mats[0].kind
+        return c
+
+    def argmax_rows(self, v, out=None):
+        """The first maximum of each row of a 2-D int16 tensor."""
+        out = out if out is not None else torch.empty(v.shape[0], dtype=torch.int32, device=v.device)
+        _l.check(_l.load().vgx_argmax_rows(self.ctx, v.shape[0], v.shape[1], _ptr(v), _ptr(out)))
+        return out
 
     # -- GEMV family
     def matvec(self, mat, x, res=None, out=None):

@@ -50,6 +50,8 @@ _SIGS = {
     "vgx_ctx_sync": (_I, [_P]),
     "vgx_mat_upload": (_I, [_P, ctypes.POINTER(WeightDesc), ctypes.POINTER(_P)]),
     "vgx_mat_clone": (_I, [_P, _P, ctypes.POINTER(_P)]),
+    "vgx_mat_concat": (_I, [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(_P)]),
+    "vgx_argmax_rows": (_I, [_P, _I, _I, _P, _P]),
     "vgx_mat_free": (_I, [_P]),
     "vgx_mat_shape": (_I, [_P, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "vgx_mat_weight_bytes": (ctypes.c_size_t, [_P]),
@@ -88,6 +90,9 @@ _SIGS = {
     "vgx_kv_append": (_I, [_P, _I, _I, _P]),
     "vgx_attn_decode": (_I, [_P, _I, _I, _P, _P]),
     "vgx_attn_block": (_I, [_P, _I, _I, _P, _P]),
+    "vgx_attn_create_seqs": (_I, [_P, _P, _I, ctypes.POINTER(_P)]),
+    "vgx_attn_seq_view": (_I, [_P, _I, ctypes.POINTER(_P)]),
+    "vgx_attn_block_seqs": (_I, [_P, _I, _I, _I, _P, _P]),
     "vgx_kv_row_bytes": (_I, [_P]),
     "vgx_kv_read_rows": (_I, [_P, _I, _I, _I, _P]),
     "vgx_kv_write_rows": (_I, [_P, _I, _I, _I, _P]),
