@@ -78,29 +78,23 @@ __device__ __forceinline__ i32x16 mfma(const Op& a, const Op& b, const i32x16& c
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(a.v, b.v, c, 0, 0, 0);
 }
 
-// A operands: 16 q16 activations at columns k0..k0+15 of one token row, as the
+// A operands: 16 q16 activations (two 16-byte loads of one token row) as the
 // high-byte plane and the low-byte plane minus 128; xsum = their exact sum.
-__device__ __forceinline__ void x_operands(const int16_t* xrow, int k0, bool ok, Op& xh, Op& xl, int& xsum) {
-    if (!ok) {
-        for (int i = 0; i < 4; ++i) { xh.d[i] = 0u; xl.d[i] = 0u; }
-        xsum = 0;
-        return;
-    }
-    const uint4* p = reinterpret_cast<const uint4*>(xrow + k0);
-    const uint4 a = p[0], b = p[1];
+// ok = false gives zeros.
+__device__ __forceinline__ void x_planes(const uint4 a, const uint4 b, bool ok, Op& xh, Op& xl, int& xsum) {
     const uint32_t d[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
     int sh = 0;
     uint32_t sl = 0;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const uint32_t lo = perm(d[2 * k + 1], d[2 * k], 0x06040200u);  // low bytes of 4k..4k+3
-        const uint32_t hi = perm(d[2 * k + 1], d[2 * k], 0x07050301u);
+        const uint32_t lo = ok ? perm(d[2 * k + 1], d[2 * k], 0x06040200u) : 0x80808080u;  // low bytes of 4k..4k+3
+        const uint32_t hi = ok ? perm(d[2 * k + 1], d[2 * k], 0x07050301u) : 0u;
         xh.d[k] = hi;
         xl.d[k] = lo ^ 0x80808080u;
         sh = sdot4(hi, 0x01010101u, sh);
         sl = __builtin_amdgcn_udot4(lo, 0x01010101u, sl, false);
     }
-    xsum = 256 * sh + (int)sl;
+    xsum = ok ? 256 * sh + (int)sl : 0;
 }
 
 // Four 2-bit t3 codes (one byte) as four int8 levels: bit 0 = |level|,
@@ -116,22 +110,31 @@ __device__ __forceinline__ uint32_t t3_levels(uint32_t b) {
     return r;
 }
 
-// B operand: weight row n, columns k0..k0+15, as int8 levels; wsum = their sum.
+// The bytes of weight row n, columns k0..k0+15: 16 (q8) or 8 (q4, t3, in .x
+// and .y; for t3 the texel pair holding row n).
 template <int KIND>
-__device__ __forceinline__ void w_operand(const MatDev& M, int n, int k0, int K, bool ok, Op& w, int& wsum) {
-    if (!ok) {
-        for (int i = 0; i < 4; ++i) w.d[i] = 0u;
-        wsum = 0;
-        return;
+__device__ __forceinline__ uint4 w_raw(const MatDev& M, int n, int k0, int K) {
+    if (KIND == VGX_Q8) return *reinterpret_cast<const uint4*>(M.body + (size_t)n * K + k0);
+    uint2 v;
+    if (KIND == VGX_Q4) {
+        v = *reinterpret_cast<const uint2*>(M.body + (size_t)n * (K >> 1) + (k0 >> 1));
+    } else {
+        const size_t ustride = (size_t)(K >> 3) * 4;
+        v = *reinterpret_cast<const uint2*>(M.body + (size_t)(n >> 1) * ustride + (size_t)(k0 >> 3) * 4);
     }
+    return make_uint4(v.x, v.y, 0u, 0u);
+}
+
+// B operand from those bytes: the 16 weights as int8 levels; wsum = their
+// sum.  ok = false gives zeros.
+template <int KIND>
+__device__ __forceinline__ void w_planes(const uint4 v, int n, bool ok, Op& w, int& wsum) {
     if (KIND == VGX_Q8) {
-        const uint4 v = *reinterpret_cast<const uint4*>(M.body + (size_t)n * K + k0);
         w.d[0] = v.x ^ 0x80808080u;
         w.d[1] = v.y ^ 0x80808080u;
         w.d[2] = v.z ^ 0x80808080u;
         w.d[3] = v.w ^ 0x80808080u;
     } else if (KIND == VGX_Q4) {
-        const uint2 v = *reinterpret_cast<const uint2*>(M.body + (size_t)n * (K >> 1) + (k0 >> 1));
         const uint32_t lo0 = v.x & 0x0F0F0F0Fu, hi0 = (v.x >> 4) & 0x0F0F0F0Fu;
         const uint32_t lo1 = v.y & 0x0F0F0F0Fu, hi1 = (v.y >> 4) & 0x0F0F0F0Fu;
         // low nibble = even column: interleave (lo.b0, hi.b0, lo.b1, hi.b1), ...
@@ -141,14 +144,14 @@ __device__ __forceinline__ void w_operand(const MatDev& M, int n, int k0, int K,
         w.d[3] = perm(hi1, lo1, 0x07030602u);
     } else {
         // texel (c, u): b0 b1 = row 2u columns 8c..8c+7, b2 b3 = row 2u+1
-        const size_t ustride = (size_t)(K >> 3) * 4;
-        const uint2 v = *reinterpret_cast<const uint2*>(M.body + (size_t)(n >> 1) * ustride + (size_t)(k0 >> 3) * 4);
         const int sh = (n & 1) * 16;
         w.d[0] = t3_levels((v.x >> sh) & 0xFFu);
         w.d[1] = t3_levels((v.x >> (sh + 8)) & 0xFFu);
         w.d[2] = t3_levels((v.y >> sh) & 0xFFu);
         w.d[3] = t3_levels((v.y >> (sh + 8)) & 0xFFu);
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w.d[i] = ok ? w.d[i] : 0u;
     int s = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) s = sdot4(w.d[i], 0x01010101u, s);
@@ -208,30 +211,60 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(const GemmLaunch G) {
     }
     const float ps = M.ps, ps3 = G.M3.ps;
 
-    // a step's operands, loaded one step ahead of the multiply
+    // A step's operands: the raw bytes of the lane's NPF next steps are in
+    // flight together (each step's loads go out NPF steps ahead of its
+    // multiply), from clamped in-range addresses, unconditionally -- a
+    // predicated load would be waited for before the next one is issued --
+    // and out-of-range tokens, rows and columns become zeros when the bytes
+    // are turned into operands.
     struct Ops {
         Op xh, xl, w, w3;
         int xs, ws, ws3;
         uint32_t sm, sm3;
     };
-    auto load = [&](int s, Ops& o) {
-        const int k0 = s * kTile + half * 16;
-        const bool kok = k0 < K;
-        x_operands(xrow, k0, tok && kok, o.xh, o.xl, o.xs);
-        w_operand<KIND>(M, n, k0, K, nok && kok, o.w, o.ws);
-        o.ws3 = 0;
-        if (EPI == BEPI_GATE) w_operand<KIND>(G.M3, n, k0, K, nok && kok, o.w3, o.ws3);
+    struct Raw {
+        uint4 xa, xb, w, w3;
+        uint32_t sm, sm3;
+    };
+    const int nn = nok ? n : M.rows - 1;
+    auto raw_load = [&](int s, Raw& r) {
+        const int k0 = min(s * kTile + half * 16, K - 16);
+        const uint4* p = reinterpret_cast<const uint4*>(xrow + k0);
+        r.xa = p[0];
+        r.xb = p[1];
+        r.w = w_raw<KIND>(M, nn, k0, K);
+        if (EPI == BEPI_GATE) r.w3 = w_raw<KIND>(G.M3, nn, k0, K);
         if (KIND == VGX_Q4) {
-            o.sm = nok ? M.sm[(size_t)n * (K >> 5) + s] : 0u;
-            o.sm3 = (EPI == BEPI_GATE && nok) ? G.M3.sm[(size_t)n * (K >> 5) + s] : 0u;
+            r.sm = M.sm[(size_t)nn * (K >> 5) + s];
+            if (EPI == BEPI_GATE) r.sm3 = G.M3.sm[(size_t)nn * (K >> 5) + s];
         }
     };
-    Ops cur;
-    if (s_beg < s_end) load(s_beg, cur);
-    for (int s = s_beg; s < s_end; ++s) {
-        Ops nxt;
-        const bool more = s + 1 < s_end;
-        if (more) load(s + 1, nxt);
+    auto process = [&](int s, const Raw& r, Ops& o) {
+        const int k0 = s * kTile + half * 16;
+        const bool kok = k0 < K;
+        x_planes(r.xa, r.xb, tok && kok, o.xh, o.xl, o.xs);
+        w_planes<KIND>(r.w, n, nok && kok, o.w, o.ws);
+        o.ws3 = 0;
+        if (EPI == BEPI_GATE) w_planes<KIND>(r.w3, n, nok && kok, o.w3, o.ws3);
+        if (KIND == VGX_Q4) {
+            o.sm = nok ? r.sm : 0u;
+            o.sm3 = (EPI == BEPI_GATE && nok) ? r.sm3 : 0u;
+        }
+    };
+    constexpr int NPF = 4;
+    Raw rb[NPF];
+    if (s_beg < s_end) {
+#pragma unroll
+        for (int j = 0; j < NPF; ++j) raw_load(min(s_beg + j, s_end - 1), rb[j]);
+    }
+    for (int s0 = s_beg; s0 < s_end; s0 += NPF)
+#pragma unroll
+    for (int j = 0; j < NPF; ++j) {
+        const int s = s0 + j;
+        if (s >= s_end) break;
+        Ops cur;
+        process(s, rb[j], cur);
+        raw_load(min(s + NPF, s_end - 1), rb[j]);
         const int k0 = s * kTile + half * 16;
         if (KIND != VGX_Q4) {
             if (EPI == BEPI_SPLIT) {
@@ -290,7 +323,6 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(const GemmLaunch G) {
                 }
             }
         }
-        if (more) cur = nxt;
     }
 
     // waves 1..3 hand over; wave 0 adds the partials in wave order and stores
