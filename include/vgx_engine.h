@@ -37,6 +37,12 @@ int vgx_engine_step(vgx_engine* e, int token, int pos, int16_t* logits_host, int
  * the n_gen-1 steps after it.  Either timing pointer may be NULL. */
 int vgx_engine_generate(vgx_engine* e, const int* prompt, int n_prompt, int n_gen, int* out,
                         double* prefill_ms, double* decode_ms);
+/* The same with positions 0..n_cached-1 of the prompt already in the KV cache
+ * (a loaded prefix cache): only positions n_cached.. are prefilled, so
+ * 0 <= n_cached < n_prompt (the reference re-runs at least the last prompt
+ * token for its logits, engine/src/worker.cpp:277-279). */
+int vgx_engine_generate_from(vgx_engine* e, const int* prompt, int n_prompt, int n_cached, int n_gen, int* out,
+                             double* prefill_ms, double* decode_ms);
 /* Prompt positions pos0 .. pos0+n-1 in batches: Session::step_group
  * (engine/src/session.cpp:1741-1795) on the int8 matrix cores.  Every
  * position's result equals vgx_engine_step's, so logits_host (vocab int16 of
@@ -56,6 +62,18 @@ int vgx_engine_set_prefill_batch(vgx_engine* e, int n);
  * models. */
 int vgx_engine_generate_batch(vgx_engine* e, int nseq, const int* prompts, int n_prompt, int n_gen, int* out,
                               double* prefill_ms, double* decode_ms);
+/* The MMKV1 prefix cache (engine/src/prefix_cache.cpp:25-207).  save: the
+ * KV rows of positions 0..n-1 (the caller has run toks[0..n) through the
+ * engine) and, for a hybrid model, the conv history, under a header naming
+ * the container (file size and mtime), the shape and the KV packing; plus the
+ * JSON sidecar path + ".json" with system_fnv / tools_fnv as the reference
+ * records them.  load: refuses a cache written for another container, shape
+ * or packing (VGX_EINVAL) before touching the device state; on success the
+ * KV rows, the conv history and the token history are in place, *n is the
+ * cached token count and toks (cap entries, may be NULL) holds the ids. */
+int vgx_engine_save_prefix(vgx_engine* e, const char* path, const int* toks, int n, uint64_t system_fnv,
+                           uint64_t tools_fnv);
+int vgx_engine_load_prefix(vgx_engine* e, const char* path, int* toks, int cap, int* n);
 /* The message of the last failed engine call on this thread. */
 const char* vgx_engine_last_error(void);
 

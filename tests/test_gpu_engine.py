@@ -301,3 +301,106 @@ def test_generate_batch_refusals(gpu):
     with pytest.raises(vl.VgxError):
         eng.generate_batch(np.zeros((17, 4), np.int32), 2)  # more sequences than min(seq, 512)
     eng.close()
+
+
+def _mmkv_header(raw):
+    """The MMKV1 header fields (engine/src/prefix_cache.cpp:33-56)."""
+    import struct
+    assert raw[:5] == b"MMKV1"
+    ver, size, mtime = struct.unpack_from("<IQQ", raw, 8)
+    dims = struct.unpack_from("<8I", raw, 28)
+    theta, flags, n, width = struct.unpack_from("<fIII", raw, 60)
+    off = 76
+    vsw = None
+    if ver >= 3:
+        vsw, = struct.unpack_from("<I", raw, off)
+        off += 4
+    kscale, = struct.unpack_from("<f", raw, off)
+    off += 4
+    toks = np.frombuffer(raw, np.uint32, n, off)
+    return dict(version=ver, size=size, mtime=mtime, dims=dims, theta=theta, flags=flags, n=n, width=width,
+                vsw=vsw, kscale=kscale, toks=toks, body=off + 4 * n)
+
+
+@pytest.mark.parametrize("kv_bits", [16, 8])
+def test_prefix_cache_round_trip(gpu, tmp_path, kv_bits):
+    """MMKV1: a cache saved after a prompt, loaded into a fresh engine, resumes
+    to exactly the tokens the uncached run gives; the file holds the reference
+    header and the KV rows in the texel byte layout."""
+    import json
+    spec = synth.tiny_spec(seq=48)
+    blob = synth.container(spec, "q8", seed=5)
+    prompt = synth.prompt(20, spec.vocab, seed=4)
+    full, _, _ = Engine(blob, kv_bits=kv_bits).generate(prompt, 10)
+    a = Engine(blob, kv_bits=kv_bits)
+    a.prefill(prompt[:14], logits=False)
+    path = tmp_path / "p.mmkv"
+    a.save_prefix(path, prompt[:14], system_fnv=0x1234, tools_fnv=5)
+    raw = path.read_bytes()
+    h = _mmkv_header(raw)
+    kv_dim = spec.kv_heads * spec.head_dim
+    assert h["version"] == 2 and h["size"] == len(blob) and h["mtime"] == 0
+    assert h["dims"] == (spec.dim, spec.hidden, spec.layers, spec.heads, spec.kv_heads, spec.vocab, 48,
+                         spec.head_dim)
+    assert h["flags"] == 1 | 2 | (4 if kv_bits == 16 else 8) and h["n"] == 14
+    assert h["width"] == (kv_dim if kv_bits == 16 else kv_dim // 2)
+    assert h["kscale"] == (2048.0 if kv_bits == 16 else 16.0)
+    assert list(h["toks"]) == list(prompt[:14])
+    rb = h["width"] * 4
+    assert len(raw) == h["body"] + spec.layers * 14 * rb
+    side = json.loads((tmp_path / "p.mmkv.json").read_text())
+    assert side["format"] == "mmkv" and side["n_tokens"] == 14 and side["system_fnv64"] == "%016x" % 0x1234
+    fnv = 1469598103934665603
+    for t in prompt[:14]:
+        for b in range(4):
+            fnv = ((fnv ^ ((int(t) >> (8 * b)) & 0xFF)) * 1099511628211) & ((1 << 64) - 1)
+    assert side["tokens_fnv64"] == "%016x" % fnv
+    a.close()
+    b = Engine(blob, kv_bits=kv_bits)
+    assert list(b.load_prefix(path)) == list(prompt[:14])
+    got, _, _ = b.generate_from(prompt, 14, 10)
+    assert list(got) == list(full)
+    b.close()
+    # refusals: another KV packing, another container, a damaged header
+    from vgx import lib as vl
+    c = Engine(blob, kv_bits=8 if kv_bits == 16 else 16)
+    with pytest.raises(vl.VgxError):
+        c.load_prefix(path)
+    c.close()
+    other = synth.container(synth.tiny_spec(seq=48), "q8", seed=6, q8_row=True)
+    if len(other) != len(blob):
+        d = Engine(other, kv_bits=kv_bits)
+        with pytest.raises(vl.VgxError):
+            d.load_prefix(path)
+        d.close()
+    bad = bytearray(raw)
+    bad[28] ^= 1  # dim
+    (tmp_path / "bad.mmkv").write_bytes(bytes(bad))
+    e = Engine(blob, kv_bits=kv_bits)
+    with pytest.raises(vl.VgxError):
+        e.load_prefix(tmp_path / "bad.mmkv")
+    e.close()
+
+
+def test_prefix_cache_hybrid_conv_history(gpu, tmp_path):
+    """A hybrid's cache (version 4) carries the conv history, so a reload
+    resumes the conv layers exactly."""
+    spec = synth.tiny_hybrid_spec(seq=48, hidden=2112)
+    w = synth.dense_weights(spec, seed=6, std=0.05, conv_std=0.5)
+    blob = synth.container(spec, "q8", weights=w)
+    prompt = synth.prompt(17, spec.vocab, seed=2)
+    full, _, _ = Engine(blob).generate(prompt, 9)
+    a = Engine(blob)
+    a.prefill(prompt[:11], logits=False)
+    path = tmp_path / "h.mmkv"
+    a.save_prefix(path, prompt[:11])
+    a.close()
+    h = _mmkv_header(path.read_bytes())
+    assert h["version"] == 4 and h["vsw"] == 0 and h["flags"] & 32
+    nconv = sum(1 for t in spec.layer_types if t == "conv")
+    assert len(path.read_bytes()) == h["body"] + spec.layers * 11 * h["width"] * 4 + nconv * 2 * 2 * spec.dim
+    b = Engine(blob)
+    b.load_prefix(path)
+    got, _, _ = b.generate_from(prompt, 11, 9)
+    assert list(got) == list(full)
+    b.close()

@@ -3,11 +3,13 @@
 // engine/src/session.cpp:1459-1584) issued as libvgx launches on one stream,
 // and greedy generation with the token kept on the device.
 #include <hip/hip_runtime.h>
+#include <sys/stat.h>
 
 #include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <fstream>
 #include <memory>
 #include <string>
 #include <vector>
@@ -64,6 +66,8 @@ struct vgx_engine {
     int* btok = nullptr;
     size_t btok_cap = 0;
     std::vector<void*> allocs;
+    // the container's identity, as the prefix cache header records it
+    uint64_t src_size = 0, src_mtime = 0;
 
     ~vgx_engine() {
         for (auto& l : L) {
@@ -453,6 +457,11 @@ int vgx_engine_open(const char* path, int device, int seq, int kv_bits, vgx_engi
     vgx_engine* e = new vgx_engine();
     std::string err;
     if (!e->c.open(path, err)) { delete e; return fail(VGX_EINVAL, err); }
+    struct stat st {};
+    if (stat(path, &st) == 0) {
+        e->src_size = (uint64_t)st.st_size;
+        e->src_mtime = (uint64_t)st.st_mtime;
+    }
     return engine_finish_open(e, device, seq, kv_bits, out);
 }
 
@@ -462,6 +471,7 @@ int vgx_engine_open_bytes(const void* data, size_t size, int device, int seq, in
     vgx_engine* e = new vgx_engine();
     std::string err;
     if (!e->c.open_bytes(static_cast<const uint8_t*>(data), size, err)) { delete e; return fail(VGX_EINVAL, err); }
+    e->src_size = size;  // no file: mtime 0
     return engine_finish_open(e, device, seq, kv_bits, out);
 }
 
@@ -501,10 +511,17 @@ int vgx_engine_step(vgx_engine* e, int token, int pos, int16_t* logits_host, int
 
 int vgx_engine_generate(vgx_engine* e, const int* prompt, int n_prompt, int n_gen, int* out,
                         double* prefill_ms, double* decode_ms) {
+    return vgx_engine_generate_from(e, prompt, n_prompt, 0, n_gen, out, prefill_ms, decode_ms);
+}
+
+int vgx_engine_generate_from(vgx_engine* e, const int* prompt, int n_prompt, int n_cached, int n_gen, int* out,
+                             double* prefill_ms, double* decode_ms) {
     g_err.clear();
     if (!e || !prompt || !out) return fail(VGX_EINVAL, "vgx_engine_generate: NULL argument");
     if (n_prompt <= 0 || n_gen <= 0 || n_prompt + n_gen - 1 > e->seq)
         return fail(VGX_ERANGE, "vgx_engine_generate: prompt + generation longer than the KV length");
+    if (n_cached < 0 || n_cached >= n_prompt)
+        return fail(VGX_ERANGE, "vgx_engine_generate: the cached prefix must leave at least one prompt token");
     for (int i = 0; i < n_prompt; ++i)
         if (prompt[i] < 0 || prompt[i] >= e->m.vocab) return fail(VGX_EINVAL, "prompt token outside the vocabulary");
     hipStream_t s = static_cast<hipStream_t>(vgx_ctx_stream(e->ctx));
@@ -515,7 +532,7 @@ int vgx_engine_generate(vgx_engine* e, const int* prompt, int n_prompt, int n_ge
     if (hipDeviceSynchronize() != hipSuccess) return fail(VGX_EHIP, "sync");
     auto t0 = std::chrono::steady_clock::now();
     int st;
-    if ((st = e->run_prompt(e->toks, 0, n_prompt, gen, e->attn))) return st;
+    if ((st = e->run_prompt(e->toks + n_cached, n_cached, n_prompt - n_cached, gen, e->attn))) return st;
     if (hipStreamSynchronize(s) != hipSuccess) return fail(VGX_EHIP, "prefill sync");
     auto t1 = std::chrono::steady_clock::now();
     for (int i = 1; i < n_gen; ++i)
@@ -603,6 +620,211 @@ int vgx_engine_generate_batch(vgx_engine* e, int nseq, const int* prompts, int n
         for (int i = 0; i < n_gen; ++i) out[(size_t)q * n_gen + i] = g[(size_t)i * nseq + q];
     if (prefill_ms) *prefill_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
     if (decode_ms) *decode_ms = std::chrono::duration<double, std::milli>(t2 - t1).count();
+    return VGX_OK;
+}
+
+// ---------------------------------------------------------------------------
+// The MMKV1 prefix cache (engine/src/prefix_cache.cpp:25-207): a header that
+// names the container (size, mtime), the shape and the KV packing, the token
+// ids, then per layer the n KV rows in the texel byte layout (q16 big-endian,
+// q8 bytes), and for a hybrid (version 4) the two conv history rows of every
+// conv layer (x[pos-2], then x[pos-1]; q16 big-endian, two per texel).  A
+// conv layer has no KV cache; its row block is written as zeros and skipped
+// on load.  The JSON sidecar (path + ".json") repeats the header's fields.
+
+namespace {
+
+struct MmkvHeader {
+    uint32_t version, dim, hidden, layers, heads, kv_heads, vocab, seq, head_dim, flags, n, width, vsw;
+    uint64_t size, mtime;
+    float theta, kscale;
+};
+
+MmkvHeader mmkv_expect(const vgx_engine* e, uint32_t n) {
+    MmkvHeader h{};
+    const bool hybrid = e->conv != nullptr;
+    h.version = hybrid ? 4u : 2u;
+    h.size = e->src_size;
+    h.mtime = e->src_mtime;
+    h.dim = (uint32_t)e->m.dim;
+    h.hidden = (uint32_t)e->m.hidden;
+    h.layers = (uint32_t)e->m.layers;
+    h.heads = (uint32_t)e->m.heads;
+    h.kv_heads = (uint32_t)e->m.kv_heads;
+    h.vocab = (uint32_t)e->m.vocab;
+    h.seq = (uint32_t)e->seq;
+    h.head_dim = (uint32_t)e->m.head_dim();
+    h.theta = e->m.theta;
+    // qk_norm 1, rope_half 2, KV q16 4 / q8 8, 8-bit activations 16, hybrid 32
+    h.flags = (e->m.qk_norm ? 1u : 0u) | (e->m.rope_half ? 2u : 0u) | (e->kv_bits == 16 ? 4u : 8u) |
+              (hybrid ? 32u : 0u);
+    h.n = n;
+    const int kv_dim = e->m.kv_dim();
+    h.width = (uint32_t)(e->kv_bits == 16 ? kv_dim : kv_dim / 2);  // texels per KV row
+    h.vsw = 0;
+    h.kscale = e->kv_bits == 16 ? 2048.0f : 16.0f;
+    return h;
+}
+
+std::string hex64(uint64_t v) {
+    char b[32];
+    std::snprintf(b, sizeof(b), "%016llx", (unsigned long long)v);
+    return b;
+}
+
+}  // namespace
+
+int vgx_engine_save_prefix(vgx_engine* e, const char* path, const int* toks, int n, uint64_t system_fnv,
+                           uint64_t tools_fnv) {
+    g_err.clear();
+    if (!e || !path || !toks) return fail(VGX_EINVAL, "vgx_engine_save_prefix: NULL argument");
+    if (n <= 0 || n > e->seq) return fail(VGX_ERANGE, "vgx_engine_save_prefix: token count outside 1..seq");
+    const MmkvHeader h = mmkv_expect(e, (uint32_t)n);
+    std::ofstream f(path, std::ios::binary);
+    if (!f) return fail(VGX_EINVAL, std::string("vgx_engine_save_prefix: cannot write ") + path);
+    const char magic[8] = {'M', 'M', 'K', 'V', '1', 0, 0, 0};
+    f.write(magic, 8);
+    auto u32 = [&](uint32_t v) { f.write(reinterpret_cast<const char*>(&v), 4); };
+    auto u64 = [&](uint64_t v) { f.write(reinterpret_cast<const char*>(&v), 8); };
+    auto f32 = [&](float v) { f.write(reinterpret_cast<const char*>(&v), 4); };
+    u32(h.version);
+    u64(h.size);
+    u64(h.mtime);
+    u32(h.dim); u32(h.hidden); u32(h.layers); u32(h.heads);
+    u32(h.kv_heads); u32(h.vocab); u32(h.seq); u32(h.head_dim);
+    f32(h.theta);
+    u32(h.flags);
+    u32(h.n);
+    u32(h.width);
+    if (h.version >= 3) u32(h.vsw);
+    f32(h.kscale);
+    uint64_t fnv = 1469598103934665603ull;  // FNV-1a over the ids' little-endian bytes
+    for (int i = 0; i < n; ++i) {
+        u32((uint32_t)toks[i]);
+        for (int b = 0; b < 4; ++b) {
+            fnv ^= (uint8_t)((uint32_t)toks[i] >> (8 * b));
+            fnv *= 1099511628211ull;
+        }
+    }
+    const int rb = vgx_kv_row_bytes(e->attn);
+    std::vector<uint8_t> rows((size_t)rb * n);
+    for (int l = 0; l < e->m.layers; ++l) {
+        if (e->is_conv(l)) {
+            std::fill(rows.begin(), rows.end(), 0);
+        } else {
+            int st = vgx_kv_read_rows(e->attn, l, 0, n, rows.data());
+            if (st) return st;
+        }
+        f.write(reinterpret_cast<const char*>(rows.data()), (std::streamsize)rows.size());
+    }
+    if (e->conv) {
+        const int D = e->m.dim;
+        std::vector<int16_t> st2((size_t)2 * D);
+        std::vector<uint8_t> be((size_t)2 * D);
+        for (int l = 0; l < e->m.layers; ++l) {
+            if (!e->is_conv(l)) continue;
+            int st = vgx_conv_state_read(e->conv, l, st2.data());
+            if (st) return st;
+            for (int which = 0; which < 2; ++which) {
+                for (int i = 0; i < D; ++i) {
+                    const uint16_t v = (uint16_t)st2[(size_t)which * D + i];
+                    be[2 * i] = (uint8_t)(v >> 8);
+                    be[2 * i + 1] = (uint8_t)(v & 0xFF);
+                }
+                f.write(reinterpret_cast<const char*>(be.data()), (std::streamsize)be.size());
+            }
+        }
+    }
+    if (!f) return fail(VGX_EHIP, std::string("vgx_engine_save_prefix: write failed: ") + path);
+    f.close();
+    std::ofstream sm(std::string(path) + ".json");
+    if (sm) {
+        sm << "{\"format\":\"mmkv\",\"version\":" << h.version << ",\"source_size\":" << h.size
+           << ",\"source_mtime\":" << h.mtime << ",\"dim\":" << h.dim << ",\"hidden\":" << h.hidden
+           << ",\"layers\":" << h.layers << ",\"heads\":" << h.heads << ",\"kv_heads\":" << h.kv_heads
+           << ",\"vocab\":" << h.vocab << ",\"seq\":" << h.seq << ",\"head_dim\":" << h.head_dim
+           << ",\"rope_theta\":" << (double)h.theta << ",\"kv_bits\":" << e->kv_bits << ",\"act_fmt\":\"x16_2\""
+           << ",\"hybrid\":" << (e->conv ? "true" : "false") << ",\"kv_scale\":" << (double)h.kscale
+           << ",\"kv_width\":" << h.width << ",\"vstep\":0,\"n_tokens\":" << n << ",\"tokens_fnv64\":\""
+           << hex64(fnv) << "\",\"system_fnv64\":\"" << hex64(system_fnv) << "\",\"tools_fnv64\":\""
+           << hex64(tools_fnv) << "\",\"template\":\"\"}\n";
+    }
+    return VGX_OK;
+}
+
+int vgx_engine_load_prefix(vgx_engine* e, const char* path, int* toks, int cap, int* n_out) {
+    g_err.clear();
+    if (!e || !path || !n_out) return fail(VGX_EINVAL, "vgx_engine_load_prefix: NULL argument");
+    *n_out = 0;
+    std::ifstream f(path, std::ios::binary);
+    if (!f) return fail(VGX_EINVAL, std::string("vgx_engine_load_prefix: cannot read ") + path);
+    char magic[8] = {};
+    f.read(magic, 8);
+    if (!f || std::memcmp(magic, "MMKV1", 5) != 0) return fail(VGX_EINVAL, "vgx_engine_load_prefix: not an MMKV1 file");
+    MmkvHeader h{};
+    auto u32 = [&](uint32_t& v) { f.read(reinterpret_cast<char*>(&v), 4); };
+    auto u64 = [&](uint64_t& v) { f.read(reinterpret_cast<char*>(&v), 8); };
+    u32(h.version);
+    u64(h.size);
+    u64(h.mtime);
+    u32(h.dim); u32(h.hidden); u32(h.layers); u32(h.heads);
+    u32(h.kv_heads); u32(h.vocab); u32(h.seq); u32(h.head_dim);
+    f.read(reinterpret_cast<char*>(&h.theta), 4);
+    u32(h.flags);
+    u32(h.n);
+    u32(h.width);
+    if (h.version >= 3) u32(h.vsw);
+    f.read(reinterpret_cast<char*>(&h.kscale), 4);
+    const MmkvHeader w = mmkv_expect(e, h.n);
+    // load_prefix_cache's refusals (engine/src/prefix_cache.cpp:151-168): a
+    // cache for another container, shape or packing is not loaded
+    if (!f || h.version != w.version || h.size != w.size || h.mtime != w.mtime || h.dim != w.dim ||
+        h.hidden != w.hidden || h.layers != w.layers || h.heads != w.heads || h.kv_heads != w.kv_heads ||
+        h.vocab != w.vocab || h.seq != w.seq || h.head_dim != w.head_dim || h.theta != w.theta ||
+        h.flags != w.flags || h.width != w.width || h.vsw != 0 || h.n == 0 || h.n > (uint32_t)e->seq ||
+        std::memcmp(&h.kscale, &w.kscale, 4) != 0)
+        return fail(VGX_EINVAL, "vgx_engine_load_prefix: the cache was written for another model, shape or KV packing");
+    if (toks && (int)h.n > cap) return fail(VGX_ERANGE, "vgx_engine_load_prefix: token buffer too small");
+    std::vector<int> ids(h.n);
+    for (uint32_t i = 0; i < h.n; ++i) {
+        uint32_t v = 0;
+        u32(v);
+        ids[i] = (int)v;
+    }
+    const int rb = vgx_kv_row_bytes(e->attn);
+    std::vector<uint8_t> rows((size_t)rb * h.n);
+    std::vector<std::vector<uint8_t>> kv((size_t)e->m.layers);
+    for (int l = 0; l < e->m.layers; ++l) {
+        f.read(reinterpret_cast<char*>(rows.data()), (std::streamsize)rows.size());
+        if (!f) return fail(VGX_EINVAL, "vgx_engine_load_prefix: truncated KV rows");
+        if (!e->is_conv(l)) kv[l] = rows;
+    }
+    std::vector<std::vector<int16_t>> cs;
+    if (e->conv) {
+        const int D = e->m.dim;
+        std::vector<uint8_t> be((size_t)2 * D);
+        cs.assign((size_t)e->m.layers, {});
+        for (int l = 0; l < e->m.layers; ++l) {
+            if (!e->is_conv(l)) continue;
+            cs[l].resize((size_t)2 * D);
+            for (int which = 0; which < 2; ++which) {
+                f.read(reinterpret_cast<char*>(be.data()), (std::streamsize)be.size());
+                if (!f) return fail(VGX_EINVAL, "vgx_engine_load_prefix: truncated conv history");
+                for (int i = 0; i < D; ++i)
+                    cs[l][(size_t)which * D + i] = (int16_t)(uint16_t)((be[2 * i] << 8) | be[2 * i + 1]);
+            }
+        }
+    }
+    // everything read and checked: now the device state changes
+    int st;
+    for (int l = 0; l < e->m.layers; ++l)
+        if (!e->is_conv(l) && (st = vgx_kv_write_rows(e->attn, l, 0, (int)h.n, kv[l].data()))) return st;
+    for (int l = 0; e->conv && l < e->m.layers; ++l)
+        if (e->is_conv(l) && (st = vgx_conv_state_write(e->conv, l, cs[l].data()))) return st;
+    if (hipMemcpy(e->toks, ids.data(), (size_t)h.n * sizeof(int), hipMemcpyHostToDevice) != hipSuccess)
+        return fail(VGX_EHIP, "token history upload");
+    if (toks) std::memcpy(toks, ids.data(), (size_t)h.n * sizeof(int));
+    *n_out = (int)h.n;
     return VGX_OK;
 }
 

@@ -23,6 +23,10 @@ _SIGS = {
     "vgx_engine_set_prefill_batch": (_I, [_P, _I]),
     "vgx_engine_generate_batch": (_I, [_P, _I, _P, _I, _I, _P, ctypes.POINTER(ctypes.c_double),
                                        ctypes.POINTER(ctypes.c_double)]),
+    "vgx_engine_generate_from": (_I, [_P, _P, _I, _I, _I, _P, ctypes.POINTER(ctypes.c_double),
+                                      ctypes.POINTER(ctypes.c_double)]),
+    "vgx_engine_save_prefix": (_I, [_P, ctypes.c_char_p, _P, _I, ctypes.c_uint64, ctypes.c_uint64]),
+    "vgx_engine_load_prefix": (_I, [_P, ctypes.c_char_p, _P, _I, ctypes.POINTER(_I)]),
     "vgx_engine_last_error": (ctypes.c_char_p, []),
 }
 _lib = None
@@ -96,6 +100,29 @@ class Engine:
         _check(load().vgx_engine_generate(self.h, p.ctypes.data, p.size, n_gen, out.ctypes.data,
                                           ctypes.byref(pf), ctypes.byref(dc)))
         return out, pf.value, dc.value
+
+    def generate_from(self, prompt, n_cached, n_gen):
+        """generate() with prompt[:n_cached] already in the KV cache."""
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.empty(n_gen, np.int32)
+        pf, dc = ctypes.c_double(), ctypes.c_double()
+        _check(load().vgx_engine_generate_from(self.h, p.ctypes.data, p.size, n_cached, n_gen, out.ctypes.data,
+                                               ctypes.byref(pf), ctypes.byref(dc)))
+        return out, pf.value, dc.value
+
+    def save_prefix(self, path, toks, system_fnv=0, tools_fnv=0):
+        """The MMKV1 cache of positions 0..len(toks)-1 (and its .json sidecar)."""
+        t = np.ascontiguousarray(toks, np.int32)
+        _check(load().vgx_engine_save_prefix(self.h, str(path).encode(), t.ctypes.data, t.size, system_fnv,
+                                             tools_fnv))
+
+    def load_prefix(self, path):
+        """Load an MMKV1 cache; returns its token ids."""
+        n = ctypes.c_int()
+        buf = np.empty(self.seq, np.int32)
+        _check(load().vgx_engine_load_prefix(self.h, str(path).encode(), buf.ctypes.data, buf.size,
+                                             ctypes.byref(n)))
+        return buf[:n.value].copy()
 
     def generate_batch(self, prompts, n_gen):
         """Greedy generation for the rows of prompts (nseq x n_prompt) in
