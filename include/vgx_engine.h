@@ -30,6 +30,9 @@ int vgx_engine_open_bytes(const void* data, size_t size, int device, int seq, in
                           vgx_engine** out);
 int vgx_engine_close(vgx_engine* e);
 int vgx_engine_info(const vgx_engine* e, int* dim, int* layers, int* vocab, int* seq);
+/* The number of LFM2 conv layers (key 14 of the container); 0 for a model of
+ * attention layers only, < 0 for a NULL engine. */
+int vgx_engine_conv_layers(const vgx_engine* e);
 /* One position: logits_host (vocab int16, q16 grid) and next (argmax) may be NULL. */
 int vgx_engine_step(vgx_engine* e, int token, int pos, int16_t* logits_host, int* next);
 /* Greedy generation: n_prompt tokens at positions 0.., then n_gen tokens into

@@ -489,6 +489,13 @@ int vgx_engine_info(const vgx_engine* e, int* dim, int* layers, int* vocab, int*
     return VGX_OK;
 }
 
+int vgx_engine_conv_layers(const vgx_engine* e) {
+    if (!e) return -1;
+    int n = 0;
+    for (int l = 0; l < e->m.layers; ++l) n += e->is_conv(l) ? 1 : 0;
+    return n;
+}
+
 int vgx_engine_step(vgx_engine* e, int token, int pos, int16_t* logits_host, int* next) {
     g_err.clear();
     if (!e) return fail(VGX_EINVAL, "vgx_engine_step: NULL engine");

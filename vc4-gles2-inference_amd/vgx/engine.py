@@ -26,6 +26,7 @@ _SIGS = {
     "vgx_engine_generate_from": (_I, [_P, _P, _I, _I, _I, _P, ctypes.POINTER(ctypes.c_double),
                                       ctypes.POINTER(ctypes.c_double)]),
     "vgx_engine_save_prefix": (_I, [_P, ctypes.c_char_p, _P, _I, ctypes.c_uint64, ctypes.c_uint64]),
+    "vgx_engine_conv_layers": (_I, [_P]),
     "vgx_engine_load_prefix": (_I, [_P, ctypes.c_char_p, _P, _I, ctypes.POINTER(_I)]),
     "vgx_engine_last_error": (ctypes.c_char_p, []),
 }
