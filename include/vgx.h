@@ -239,6 +239,18 @@ int vgx_attn_block(vgx_attn* a, int layer, int pos, const int16_t* qkv, int16_t*
 int vgx_kv_append_batch(vgx_attn* a, int layer, int pos0, int ntok, const int16_t* qkv);
 int vgx_attn_decode_batch(vgx_attn* a, int layer, int pos0, int ntok, const int16_t* qkv, int16_t* out);
 
+/* ---- a decode step captured once and replayed for every token (a HIP
+ * graph: its kernel arguments are fixed, so the position lives in device
+ * memory).  No counterpart in the reference, whose host loop issues each
+ * step (engine/src/session.cpp:1827-1842).
+ * vgx_attn_block_at: vgx_attn_block at the position *pos_dev (clamped into
+ *   the cache; the host cannot check it).
+ * vgx_decode_advance: hist[*pos + 1] = *token (when inside hist_len), then
+ *   ++*pos; one thread, so a replayed step leaves the next one's position
+ *   and the token history in place. */
+int vgx_attn_block_at(vgx_attn* a, int layer, const int* pos_dev, const int16_t* qkv, int16_t* out);
+int vgx_decode_advance(vgx_ctx* ctx, int* pos, const int* token, int* hist, int hist_len);
+
 /* ---- several sequences in lockstep (batched greedy decode).  No counterpart
  * in the reference, which decodes one sequence; each sequence's results are
  * the exact results of the single-sequence entry points on it.

@@ -404,3 +404,46 @@ def test_prefix_cache_hybrid_conv_history(gpu, tmp_path):
     got, _, _ = b.generate_from(prompt, 11, 9)
     assert list(got) == list(full)
     b.close()
+
+
+@pytest.mark.parametrize("scheme", ["q8", "t3"])
+def test_decode_graph_equals_launches(gpu, scheme):
+    """The decode step replayed as one captured graph (the position and token
+    in device memory) gives the tokens of the step-by-step launches, replay
+    after replay, with other engine work and syncs in between."""
+    spec = synth.tiny_spec(seq=64, hidden=2112 if scheme != "t3" else 96)
+    blob = synth.container(spec, scheme, seed=21)
+    a, b = Engine(blob), Engine(blob)
+    b.set_graphs(False)
+    for k in range(4):
+        prompt = synth.prompt(5 + 3 * k, spec.vocab, seed=30 + k)
+        ga, _, _ = a.generate(prompt, 20)
+        gb, _, _ = b.generate(prompt, 20)
+        assert list(ga) == list(gb), k
+        # eager work on the graph engine between replays: a step and a prefill
+        la, _ = a.step(int(prompt[0]), 0)
+        lb, _ = b.step(int(prompt[0]), 0)
+        assert np.array_equal(la, lb)
+    a.close()
+    b.close()
+
+
+def test_decode_graph_hybrid_and_cache(gpu, tmp_path):
+    """The graph on a hybrid (conv state advancing inside the replay) and
+    resuming from a loaded prefix cache."""
+    spec = synth.tiny_hybrid_spec(seq=48, hidden=2112)
+    blob = synth.container(spec, "q8", weights=synth.dense_weights(spec, seed=7, std=0.05, conv_std=0.5))
+    prompt = synth.prompt(9, spec.vocab, seed=5)
+    a, b = Engine(blob), Engine(blob)
+    b.set_graphs(False)
+    ga, _, _ = a.generate(prompt, 16)
+    gb, _, _ = b.generate(prompt, 16)
+    assert list(ga) == list(gb)
+    a.prefill(prompt[:6], logits=False)
+    a.save_prefix(tmp_path / "g.mmkv", prompt[:6])
+    c = Engine(blob)
+    c.load_prefix(tmp_path / "g.mmkv")
+    gc, _, _ = c.generate_from(prompt, 6, 16)
+    assert list(gc) == list(gb)
+    for e in (a, b, c):
+        e.close()

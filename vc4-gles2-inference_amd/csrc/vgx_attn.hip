@@ -1,6 +1,6 @@
 // Decode attention over the packed KV cache, with the KV pack (append).
 //
-// One workgroup of 1024 threads per query head: it prepares the head's query
+// One workgroup of 512 threads per query head: it prepares the head's query
 // (q-norm factor on its 1/65536 grid, RoPE, q16), scores every position
 // 0..pos (exact integer dot products, 1/1024 grid), forms the (max, sum)
 // statistics on their q16 grids and the weighted V sum.  In a launch that also
@@ -140,11 +140,11 @@ __device__ __forceinline__ void q_split(int q, int i, int* qhw, int* qlw) {
 // 255*2^15*2^8 < 2^31).  KVB 8: sh += sum qh*k, sl += sum (ql-128)*k,
 // sk += sum k over int8 quads (each below 2^23).  q . k = 256*sh + sl
 // (+ 128*sk for KVB 8).
+// a, b: the query's qh and ql words of that vector (zero for a vector past the
+// row); ones: 0x01010101 (zero past the row).
 template <int KVB>
-__device__ __forceinline__ void dot_vec(const int* qhw, const int* qlw, int v, const uint4 w, int& sh, int& sl,
+__device__ __forceinline__ void dot_vec(const int4 a, const int4 b, int ones, const uint4 w, int& sh, int& sl,
                                         int& sk) {
-    const int4 a = reinterpret_cast<const int4*>(qhw)[v];
-    const int4 b = reinterpret_cast<const int4*>(qlw)[v];
     const unsigned ws[4] = {w.x, w.y, w.z, w.w};
     const int as[4] = {a.x, a.y, a.z, a.w}, bs[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
@@ -157,7 +157,7 @@ __device__ __forceinline__ void dot_vec(const int* qhw, const int* qlw, int v, c
         } else {
             sh = __builtin_amdgcn_sdot4(as[u], (int)ws[u], sh, false);
             sl = __builtin_amdgcn_sdot4(bs[u], (int)ws[u], sl, false);
-            sk = __builtin_amdgcn_sdot4(0x01010101, (int)ws[u], sk, false);
+            sk = __builtin_amdgcn_sdot4(ones, (int)ws[u], sk, false);
         }
     }
 }
@@ -205,7 +205,7 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
                                                         const int16_t* qn, const int16_t* kn,
                                                         const int16_t* qkv, int16_t* out, int pos0,
                                                         int do_write, int do_attend, size_t seq_stride,
-                                                        int pos_step) {
+                                                        int pos_step, const int* pos_ptr) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int E = KVB == 16 ? 2 : 4;  // values per 32-bit word
     constexpr int KP = kKPre<KVB>;
@@ -222,7 +222,10 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     // (blockIdx.y: a batch of consecutive positions of one sequence, pos_step
     // 1; or the same position of consecutive sequences, each with its own
     // cache seq_stride bytes on, pos_step 0)
-    const int pos = pos0 + blockIdx.y * pos_step;
+    // pos_ptr: the position read from device memory (a launch captured once
+    // and replayed for every token), clamped into the cache
+    const int p0 = pos_ptr ? min(max(*pos_ptr, 0), A.seq - 1) : pos0;
+    const int pos = p0 + blockIdx.y * pos_step;
     kv += (size_t)blockIdx.y * seq_stride;
     qkv += (size_t)blockIdx.y * (A.dim + 2 * kv_dim);
     if (out) out += (size_t)blockIdx.y * A.dim;
@@ -356,34 +359,42 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     // running maximum per wave
     const float invsqrt = 1.0f / sqrtf((float)hd);
     const float unit = KVB == 16 ? 1.0f / 524288.0f : 1.0f / 4096.0f;
+    // The lane's query words are the same for every position: held in
+    // registers, zeroed for a vector past the row, so the dot products below
+    // run on every vector slot without branches.
+    int4 qa[KP], qb[KP];
+    int ones[KP];
+#pragma unroll
+    for (int k = 0; k < KP; ++k) {
+        const int v = sj + k * lpp;
+        const int vc = min(v, nv - 1);
+        const bool in = v < nv;
+        const int4 a = reinterpret_cast<const int4*>(qhw)[vc], b = reinterpret_cast<const int4*>(qlw)[vc];
+        qa[k] = in ? a : make_int4(0, 0, 0, 0);
+        qb[k] = in ? b : make_int4(0, 0, 0, 0);
+        ones[k] = in ? 0x01010101 : 0;
+    }
+    const uint4* own4 = reinterpret_cast<const uint4*>(kpk);
     int m = -32768;
     for (int it = 0;; ++it) {
         const int t = tid / lpp + it * P;
         if (t >= npos) break;
         int sh = 0, sl = 0, sk = 0;
-        if (own_row && t == pos) {
-            const uint4* src = reinterpret_cast<const uint4*>(kpk);
+        uint4 w[KP];
+        if (it == 0) {
 #pragma unroll
-            for (int k = 0; k < KP; ++k) {
-                const int v = sj + k * lpp;
-                if (v < nv) dot_vec<KVB>(qhw, qlw, v, src[v], sh, sl, sk);
-            }
-        } else if (it == 0) {
-#pragma unroll
-            for (int k = 0; k < KP; ++k) {
-                const int v = sj + k * lpp;
-                if (v < nv) dot_vec<KVB>(qhw, qlw, v, kreg[k], sh, sl, sk);
-            }
+            for (int k = 0; k < KP; ++k) w[k] = kreg[k];
         } else {
             const uint4* src = reinterpret_cast<const uint4*>(khead + (size_t)t * A.row_bytes);
-            uint4 kr[KP];
 #pragma unroll
-            for (int k = 0; k < KP; ++k) kr[k] = src[min(sj + k * lpp, nv - 1)];
+            for (int k = 0; k < KP; ++k) w[k] = src[min(sj + k * lpp, nv - 1)];
+        }
+        // the own position's K is the LDS copy (its cache row is being written)
+        const bool own = own_row && t == pos;
 #pragma unroll
-            for (int k = 0; k < KP; ++k) {
-                const int v = sj + k * lpp;
-                if (v < nv) dot_vec<KVB>(qhw, qlw, v, kr[k], sh, sl, sk);
-            }
+        for (int k = 0; k < KP; ++k) {
+            const uint4 o = own4[min(sj + k * lpp, nv - 1)];
+            dot_vec<KVB>(qa[k], qb[k], ones[k], own ? o : w[k], sh, sl, sk);
         }
         long long d = 256ll * sh + sl;
         if (KVB == 8) d += 128ll * sk;
@@ -420,10 +431,11 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
             e[4 * k + 2] = f.z;
             e[4 * k + 3] = f.w;
         }
+        // adding +0.0 leaves a sum of non-negative terms unchanged: the
+        // positions past npos are selected out without a branch
         double cs = 0.0;
 #pragma unroll
-        for (int u = 0; u < kChunk; ++u)
-            if (u < n) cs += (double)e[u];
+        for (int u = 0; u < kChunk; ++u) cs += u < n ? (double)e[u] : 0.0;
         csum[c] = cs;
     }
     __syncthreads();
@@ -435,8 +447,7 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
 #pragma unroll
             for (int k = 0; k < 8; ++k) cv[k] = csum[min(c0 + k, A.nchmax - 1)];
 #pragma unroll
-            for (int k = 0; k < 8; ++k)
-                if (c0 + k < nch) sum += cv[k];
+            for (int k = 0; k < 8; ++k) sum += c0 + k < nch ? cv[k] : 0.0;
         }
         const float fs = (float)sum;
         float qs = floorf(fs * 32.0f + 0.5f);
@@ -476,13 +487,13 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
                 unsigned wv[4];
 #pragma unroll
                 for (int u = 0; u < 4; ++u) wv[u] = vstage[(4 * k + u) * kThreads + tid];
+                // a position past the chunk's end gets weight +0.0: a + 0*q is a
+                // (a is never -0), so every slot runs without a branch
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
-                    if (4 * k + u < n) {
-                        const double pp = (double)(pe[u] * iv) * vunit_d;
+                    const double pp = 4 * k + u < n ? (double)(pe[u] * iv) * vunit_d : 0.0;
 #pragma unroll
-                        for (int e = 0; e < E; ++e) a[e] = fma(pp, (double)v_field<KVB>(wv[u], e), a[e]);
-                    }
+                    for (int e = 0; e < E; ++e) a[e] = fma(pp, (double)v_field<KVB>(wv[u], e), a[e]);
                 }
             }
             if (tend != t1) {
@@ -505,8 +516,7 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
 #pragma unroll
                 for (int k = 0; k < 8; ++k) pv[k] = vpart[min(r0 + k, A.vR - 1) * hd + i];
 #pragma unroll
-                for (int k = 0; k < 8; ++k)
-                    if (r0 + k < nr) s += pv[k];
+                for (int k = 0; k < 8; ++k) s += r0 + k < nr ? pv[k] : 0.0;
             }
             if (last) out[h * hd + i] = (int16_t)q16_round((float)s * 256.0f);
             else acc[i] = s;
@@ -550,7 +560,7 @@ size_t attn_layout(AttnDev& A) {
 // With ntok > 1 the KV write and the attention must be separate launches: a
 // position reads the rows the others write.
 int launch(vgx_attn* at, int layer, int pos, int ntok, const int16_t* qkv, int16_t* out, int w, int att,
-           bool seqs = false) {
+           bool seqs = false, const int* pos_ptr = nullptr) {
     if (!at) return vgx_fail(VGX_EINVAL, "attention: NULL handle");
     if (layer < 0 || layer >= at->layers || !at->kv[layer])
         return vgx_fail(VGX_ERANGE, "attention: layer " + std::to_string(layer) + " has no KV cache");
@@ -577,10 +587,10 @@ int launch(vgx_attn* at, int layer, int pos, int ntok, const int16_t* qkv, int16
     const int step = seqs ? 0 : 1;
     if (A.kv_bits == 16)
         hipLaunchKernelGGL(attn_kernel<16>, grid, dim3(kThreads), at->lds, at->ctx->stream, A,
-                           at->kv[layer], at->rtab, qn, kn, qkv, out, pos, w, att, stride, step);
+                           at->kv[layer], at->rtab, qn, kn, qkv, out, pos, w, att, stride, step, pos_ptr);
     else
         hipLaunchKernelGGL(attn_kernel<8>, grid, dim3(kThreads), at->lds, at->ctx->stream, A,
-                           at->kv[layer], at->rtab, qn, kn, qkv, out, pos, w, att, stride, step);
+                           at->kv[layer], at->rtab, qn, kn, qkv, out, pos, w, att, stride, step, pos_ptr);
     VGX_LAUNCH_CHECK("attention launch");
     return VGX_OK;
 }
@@ -699,6 +709,11 @@ int vgx_attn_decode(vgx_attn* a, int layer, int pos, const int16_t* qkv, int16_t
 
 int vgx_attn_block(vgx_attn* a, int layer, int pos, const int16_t* qkv, int16_t* out) {
     return launch(a, layer, pos, 1, qkv, out, 1, 1);
+}
+
+int vgx_attn_block_at(vgx_attn* a, int layer, const int* pos_dev, const int16_t* qkv, int16_t* out) {
+    if (!pos_dev) return vgx_fail(VGX_EINVAL, "vgx_attn_block_at: NULL position");
+    return launch(a, layer, 0, 1, qkv, out, 1, 1, false, pos_dev);
 }
 
 int vgx_attn_block_seqs(vgx_attn* a, int layer, int pos, int nseq, const int16_t* qkv, int16_t* out) {

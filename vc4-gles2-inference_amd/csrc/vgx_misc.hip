@@ -72,9 +72,26 @@ __global__ void embed_q8_kernel(const int8_t* emb, const float* scale, int vocab
     }
 }
 
+// One decode step's bookkeeping on the device: the token just chosen for
+// position *pos + 1 goes to the history, and *pos advances.  One thread.
+__global__ void advance_kernel(int* pos, const int* token, int* hist, int hist_len) {
+    const int p = *pos;
+    if (p + 1 >= 0 && p + 1 < hist_len) hist[p + 1] = *token;
+    *pos = p + 1;
+}
+
 }  // namespace
 
 extern "C" {
+
+int vgx_decode_advance(vgx_ctx* ctx, int* pos, const int* token, int* hist, int hist_len) {
+    if (!ctx || !pos || !token || !hist) return vgx_fail(VGX_EINVAL, "vgx_decode_advance: NULL argument");
+    if (hist_len <= 0) return vgx_fail(VGX_EINVAL, "vgx_decode_advance: empty history");
+    VGX_HIP(hipSetDevice(ctx->device));
+    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, ctx->stream, pos, token, hist, hist_len);
+    VGX_LAUNCH_CHECK("advance launch");
+    return VGX_OK;
+}
 
 int vgx_rmsnorm(vgx_ctx* ctx, int dim, const int16_t* x, const int16_t* w, float eps, int16_t* y) {
     if (!ctx || !x || !w || !y) return vgx_fail(VGX_EINVAL, "vgx_rmsnorm: NULL argument");

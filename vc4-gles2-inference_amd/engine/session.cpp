@@ -68,8 +68,18 @@ struct vgx_engine {
     std::vector<void*> allocs;
     // the container's identity, as the prefix cache header records it
     uint64_t src_size = 0, src_mtime = 0;
+    // the greedy decode step as one HIP graph, replayed per token: the token
+    // and the position live in device memory (tok_cur, pos_dev) and the step
+    // ends by appending the token to the history and advancing the position
+    bool use_graph = true;
+    hipGraph_t step_graph = nullptr;
+    hipGraphExec_t step_exec = nullptr;
+    int *pos_dev = nullptr, *tok_cur = nullptr;
+    int pos_host = 0;
 
     ~vgx_engine() {
+        if (step_exec) (void)hipGraphExecDestroy(step_exec);
+        if (step_graph) (void)hipGraphDestroy(step_graph);
         for (auto& l : L) {
             vgx_mat_free(l.qkv); vgx_mat_free(l.wo); vgx_mat_free(l.w1); vgx_mat_free(l.w3); vgx_mat_free(l.w2);
             vgx_mat_free(l.conv_in); vgx_mat_free(l.conv_out);
@@ -307,11 +317,14 @@ struct vgx_engine {
     // consumes it (the attention norm in the qkv draw, the FFN norm in the
     // gate, the final norm in the LM head with its argmax): five launches a
     // layer.
-    int forward(const int* token_dev, int pos, bool want_logits, int* next_dev, vgx_attn* A) {
+    // pos_dev: the position is read from device memory instead (the step a
+    // graph replays; never position 0).
+    int forward(const int* token_dev, int pos, bool want_logits, int* next_dev, vgx_attn* A,
+                const int* pos_dev = nullptr) {
         int st;
         const int D = m.dim;
         const float eps = m.rms_eps;
-        if (pos == 0 && conv && (st = vgx_conv_reset(conv))) return st;  // a new sequence
+        if (!pos_dev && pos == 0 && conv && (st = vgx_conv_reset(conv))) return st;  // a new sequence
         if ((st = vgx_embed_q8(ctx, emb, emb_scale, m.vocab, D, token_dev, h))) return st;
         for (int l = 0; l < m.layers; ++l) {
             Layer& ly = L[l];
@@ -323,7 +336,8 @@ struct vgx_engine {
                 if ((st = vgx_gemv(ctx, ly.conv_out, att, h, x1))) return st;
             } else {
                 if ((st = vgx_gemv_rms(ctx, ly.qkv, h, ly.rms_att, eps, nullptr, qkv))) return st;
-                if ((st = vgx_attn_block(A, l, pos, qkv, att))) return st;
+                st = pos_dev ? vgx_attn_block_at(A, l, pos_dev, qkv, att) : vgx_attn_block(A, l, pos, qkv, att);
+                if (st) return st;
                 if ((st = vgx_gemv(ctx, ly.wo, att, h, x1))) return st;
             }
             if ((st = vgx_ffn_gate_rms(ctx, ly.w1, ly.w3, x1, ly.rms_ffn, eps, ly.hs, hbuf))) return st;
@@ -385,6 +399,36 @@ struct vgx_engine {
             const int b = n - p < pbatch ? n - p : pbatch;
             if ((st = prefill(toks_dev + p, pos0 + p, b, p + b == n, next_dev, A))) return st;
         }
+        return VGX_OK;
+    }
+
+    // The decode step captured once: forward() on the token at tok_cur and the
+    // position at pos_dev, its argmax back into tok_cur, then
+    // toks[pos + 1] = tok_cur and ++pos.  Every argument is fixed, so one
+    // instantiation serves every token of every later generation.
+    int ensure_step_graph() {
+        if (step_exec) return VGX_OK;
+        int st;
+        if (!pos_dev && ((st = dalloc(&pos_dev, 1)) || (st = dalloc(&tok_cur, 1)))) return st;
+        hipStream_t s = static_cast<hipStream_t>(vgx_ctx_stream(ctx));
+        if (hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed) != hipSuccess)
+            return fail(VGX_EHIP, "decode graph: begin capture");
+        st = forward(tok_cur, 0, true, tok_cur, attn, pos_dev);
+        if (!st) st = vgx_decode_advance(ctx, pos_dev, tok_cur, toks, seq);
+        hipGraph_t g = nullptr;
+        const hipError_t ec = hipStreamEndCapture(s, &g);
+        if (st || ec != hipSuccess) {
+            if (g) (void)hipGraphDestroy(g);
+            return st ? st : fail(VGX_EHIP, std::string("decode graph: capture: ") + hipGetErrorString(ec));
+        }
+        hipGraphExec_t x = nullptr;
+        const hipError_t ei = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+        if (ei != hipSuccess) {
+            (void)hipGraphDestroy(g);
+            return fail(VGX_EHIP, std::string("decode graph: instantiate: ") + hipGetErrorString(ei));
+        }
+        step_graph = g;
+        step_exec = x;
         return VGX_OK;
     }
 
@@ -542,14 +586,32 @@ int vgx_engine_generate_from(vgx_engine* e, const int* prompt, int n_prompt, int
     if ((st = e->run_prompt(e->toks + n_cached, n_cached, n_prompt - n_cached, gen, e->attn))) return st;
     if (hipStreamSynchronize(s) != hipSuccess) return fail(VGX_EHIP, "prefill sync");
     auto t1 = std::chrono::steady_clock::now();
-    for (int i = 1; i < n_gen; ++i)
-        if ((st = e->forward(gen + i - 1, n_prompt + i - 1, true, gen + i, e->attn))) return st;
+    if (e->use_graph && n_gen > 1) {
+        // the step graph from position n_prompt: tok_cur = gen[0], pos = n_prompt
+        if ((st = e->ensure_step_graph())) return st;
+        e->pos_host = n_prompt;  // the copy's source outlives the call's queueing
+        if (hipMemcpyAsync(e->tok_cur, gen, sizeof(int), hipMemcpyDeviceToDevice, s) != hipSuccess ||
+            hipMemcpyAsync(e->pos_dev, &e->pos_host, sizeof(int), hipMemcpyHostToDevice, s) != hipSuccess)
+            return fail(VGX_EHIP, "decode graph: state upload");
+        for (int i = 1; i < n_gen; ++i)
+            if (hipGraphLaunch(e->step_exec, s) != hipSuccess) return fail(VGX_EHIP, "decode graph: launch");
+    } else {
+        for (int i = 1; i < n_gen; ++i)
+            if ((st = e->forward(gen + i - 1, n_prompt + i - 1, true, gen + i, e->attn))) return st;
+    }
     if (hipStreamSynchronize(s) != hipSuccess) return fail(VGX_EHIP, "decode sync");
     auto t2 = std::chrono::steady_clock::now();
     if (hipMemcpy(out, gen, (size_t)n_gen * sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
         return fail(VGX_EHIP, "token readback");
     if (prefill_ms) *prefill_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
     if (decode_ms) *decode_ms = std::chrono::duration<double, std::milli>(t2 - t1).count();
+    return VGX_OK;
+}
+
+int vgx_engine_set_graphs(vgx_engine* e, int on) {
+    g_err.clear();
+    if (!e) return fail(VGX_EINVAL, "vgx_engine_set_graphs: NULL engine");
+    e->use_graph = on != 0;
     return VGX_OK;
 }
 

@@ -27,6 +27,7 @@ _SIGS = {
                                       ctypes.POINTER(ctypes.c_double)]),
     "vgx_engine_save_prefix": (_I, [_P, ctypes.c_char_p, _P, _I, ctypes.c_uint64, ctypes.c_uint64]),
     "vgx_engine_conv_layers": (_I, [_P]),
+    "vgx_engine_set_graphs": (_I, [_P, _I]),
     "vgx_engine_load_prefix": (_I, [_P, ctypes.c_char_p, _P, _I, ctypes.POINTER(_I)]),
     "vgx_engine_last_error": (ctypes.c_char_p, []),
 }
@@ -89,6 +90,10 @@ class Engine:
         _check(load().vgx_engine_prefill(self.h, t.ctypes.data, t.size, int(pos0),
                                          ctypes.c_void_p(out.ctypes.data if logits else 0), ctypes.byref(nx)))
         return out, nx.value
+
+    def set_graphs(self, on):
+        """Decode steps as one replayed HIP graph (True) or single launches."""
+        _check(load().vgx_engine_set_graphs(self.h, int(bool(on))))
 
     def set_prefill_batch(self, n):
         """Largest prompt batch (0 or 1: one position at a time)."""
