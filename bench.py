@@ -128,18 +128,30 @@ def cpu_baseline(seconds):
         body = (q.view(np.uint8) ^ 0x80).ravel()
         mats.append((rows, cols, body, o.row_scales(rows, unit, plane)))
     xs = {c: rng.standard_normal(c).astype(np.float32) for _, c in SHAPES}
-    nbytes, passes = 0, 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        for rows, cols, body, wsr in mats:
-            xq = o.quantize_act(xs[cols])
-            o.store_f32(o.rowval_q8(body, 1, rows, cols, wsr, xq))
-            nbytes += algo_bytes(rows, cols)
-        passes += 1
-    dt = time.perf_counter() - t0
-    return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": o.threads(), "kind": "port",
+
+    def run(secs):
+        nbytes, passes = 0, 0
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < secs:
+            for rows, cols, body, wsr in mats:
+                xq = o.quantize_act(xs[cols])
+                o.store_f32(o.rowval_q8(body, 1, rows, cols, wsr, xq))
+                nbytes += algo_bytes(rows, cols)
+            passes += 1
+        dt = time.perf_counter() - t0
+        return nbytes / dt / 1e9, passes, dt
+
+    cores = o.threads()
+    gbps, passes, dt = run(seconds)
+    # the same on one core (the survey asks for both)
+    o.set_threads(1)
+    gbps1, passes1, dt1 = run(max(1.0, seconds / 3))
+    o.set_threads(cores)
+    return {"value": round(gbps, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "one_core_value": round(gbps1, 3),
             "sample": "%d passes over the 5 MiniMind3 q8 GEMV shapes (one matrix each, warm host caches), "
-                      "%.1f s, oracle exact-integer q8 GEMV with OpenMP" % (passes, dt)}
+                      "%.1f s, oracle exact-integer q8 GEMV with OpenMP on %d threads; one_core_value: %d passes, "
+                      "%.1f s on 1 thread" % (passes, dt, cores, passes1, dt1)}
 
 
 def model_decode(name, spec, scheme, kv_bits, n_prompt, n_gen, runs):
@@ -215,6 +227,50 @@ def ternary_batch_bench(runs, nseq=32):
             "gen": 256, "seq": 512, "kv": "q16", "tokens_per_s": round(nseq * 1000.0 / ms_step, 1),
             "ms_per_step": round(ms_step, 4), "prefill_ms_all_sequences": round(float(np.median(pf)), 2),
             "runs": runs}
+
+
+def attention_bench(reps=200):
+    """The C3 attention microbench: MiniMind3's attention (8 query / 4 KV heads
+    of 96, q/k norm), KV q8, SEQ 768; K and V ~ N(0,1) written through the
+    pack kernel; one decode attention launch (all heads of one layer, no KV
+    write) at context 1, 64, 256, 512, 768: microseconds and the KV bytes read
+    per microsecond."""
+    import numpy as np
+    import torch
+    from vgx import gpu as vg
+
+    g = vg.GPU(0)
+    hd, seq, dim, kvh = 96, 768, 768, 4
+    half = hd // 2
+    inv = 1.0 / (1e6 ** (np.arange(half) * 2.0 / hd))
+    ang = np.outer(np.arange(seq), inv)
+    A = g.attention(dim=dim, heads=8, kv_heads=kvh, head_dim=hd, seq=seq, layers=1, kv_bits=8, rope_half=1,
+                    qk_norm=1, rope_cos=np.cos(ang).astype(np.float32), rope_sin=np.sin(ang).astype(np.float32),
+                    q_norm=np.ones((1, hd), np.float32), k_norm=np.ones((1, hd), np.float32))
+    rng = np.random.default_rng(0)
+    width = dim + 2 * kvh * hd
+    qkv = np.clip(np.rint(rng.standard_normal((seq, width)) * 256.0), -32768, 32767).astype(np.int16)
+    rows = torch.from_numpy(qkv).cuda()
+    A.block_batch(0, 0, rows)  # every row packed, every position attended once
+    out = torch.empty(dim, dtype=torch.int16, device="cuda")
+    res = []
+    for ctx in (1, 64, 256, 512, 768):
+        q = rows[ctx - 1]
+        for _ in range(20):
+            A.decode(0, ctx - 1, q, out)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            A.decode(0, ctx - 1, q, out)
+        b.record()
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / reps
+        kv_bytes = ctx * A.row_bytes
+        res.append({"context": ctx, "us": round(us, 2), "kv_bytes": kv_bytes, "GBps": round(kv_bytes / us / 1e3, 2)})
+    A.free()
+    g.close()
+    return {"shape": "MiniMind3 attention: 8 query / 4 KV heads of 96, q/k norm, KV q8, SEQ 768",
+            "launch": "vgx_attn_decode (all heads of one layer)", "reps": reps, "contexts": res}
 
 
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 matrix-core peak, TOPS
@@ -311,7 +367,8 @@ def main():
     ap.add_argument("--skip-decode", action="store_true")
     ap.add_argument("--copy-mb", type=int, default=0, help="also time a device copy of this many MiB")
     ap.add_argument("--cpu-decode-steps", type=int, default=16)
-    ap.add_argument("--only", choices=["gemv", "decode", "prefill", "hybrid", "ternary", "ternary32"], default=None,
+    ap.add_argument("--only", choices=["gemv", "decode", "prefill", "hybrid", "ternary", "ternary32", "attention"],
+                    default=None,
                     help="run one leg (for profiling); the JSON line then carries that leg only")
     ap.add_argument("--prefill-runs", type=int, default=5)
     ap.add_argument("--skip-prefill", action="store_true")
@@ -332,6 +389,9 @@ def main():
         return
     if args.only == "prefill":
         print(json.dumps({"prefill": prefill_bench(args.prefill_runs)}))
+        return
+    if args.only == "attention":
+        print(json.dumps({"attention_c3": attention_bench()}))
         return
     if args.only == "ternary32":
         print(json.dumps({"decode_c5_batch32": ternary_batch_bench(args.decode_runs)}))
@@ -463,6 +523,7 @@ def main():
         out["decode_tokens_per_s"] = dec["tokens_per_s"]
     if not args.skip_prefill:
         out["prefill"] = prefill_bench(args.prefill_runs)
+        out["attention_c3"] = attention_bench()
     others = []
     if not args.skip_models:
         others = [("decode_c4", hybrid_decode_bench(args.decode_runs), 8),
