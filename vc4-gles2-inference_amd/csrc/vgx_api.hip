@@ -432,8 +432,9 @@ int vgx_group_create(vgx_ctx* ctx, int n, const vgx_mat* const* mats, vgx_group*
     g->bpm = uniform ? blk / n : 0;
     hipError_t e = hipMalloc(&g->d_dev, sizeof(MatDev) * (size_t)n);
     if (e == hipSuccess) e = hipMemcpy(g->d_dev, ds.data(), sizeof(MatDev) * (size_t)n, hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = hipMalloc(&g->counter, 256);
-    if (e == hipSuccess) e = hipMemset(g->counter, 0, 256);
+    // a key slot per workgroup of the largest grid a launch takes (gemv_grid)
+    g->nkeys = 4 * (ctx->num_cu > 0 ? ctx->num_cu : 256);
+    if (e == hipSuccess) e = hipMalloc(&g->keys, sizeof(unsigned long long) * (size_t)g->nkeys);
     if (e != hipSuccess) { vgx_group_free(g); return vgx_hip_fail(e, "vgx_group_create"); }
     *out = g;
     return VGX_OK;
@@ -442,7 +443,7 @@ int vgx_group_create(vgx_ctx* ctx, int n, const vgx_mat* const* mats, vgx_group*
 int vgx_group_free(vgx_group* g) {
     if (!g) return VGX_OK;
     if (g->d_dev) (void)hipFree(g->d_dev);
-    if (g->counter) (void)hipFree(g->counter);
+    if (g->keys) (void)hipFree(g->keys);
     delete g;
     return VGX_OK;
 }
@@ -475,8 +476,8 @@ static int launch_group(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, cons
     L.rw = rw;
     L.eps = eps;
     L.argmax_out = argmax_out;
-    L.counter = g->counter;
-    L.argmax_key = reinterpret_cast<unsigned long long*>(g->counter + 2);
+    L.argmax_key = g->keys;
+    L.nkeys = g->nkeys;
     L.total_rows = g->rows;
     return vgx_gemv_launch(L, ctx->stream);
 }

@@ -279,15 +279,25 @@ __device__ __forceinline__ void argmax_tail(const GemvLaunch& L, unsigned long l
     __syncthreads();
     if (threadIdx.x == 0) {
         for (int k = 1; k < kWaves; ++k) key = s_k[k] > key ? s_k[k] : key;
-        const unsigned long long prev = atomicMax(L.argmax_key, key);
-        // never ~0 (the value field is at most 0xFFFF): the increment depends
-        // on the returned value
-        const unsigned inc = prev == ~0ull ? 0u : 1u;
-        if (atomicAdd(L.counter, inc) == gridDim.x - 1) {
-            const unsigned long long fin = atomicExch(L.argmax_key, 0ull);
-            *L.argmax_out = (int)(0xFFFFFFFFu - (unsigned)(fin & 0xFFFFFFFFull));
-            atomicExch(L.counter, 0u);
-        }
+        L.argmax_key[blockIdx.x] = key;
+    }
+}
+
+// The largest of n keys (the first maximum of the rows they cover), one
+// workgroup: its row index into *out.
+__global__ void __launch_bounds__(256) argmax_keys_kernel(const unsigned long long* keys, int n, int* out) {
+    __shared__ unsigned long long s_k[4];
+    unsigned long long key = 0ull;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) key = keys[i] > key ? keys[i] : key;
+    for (int o = 32; o >= 1; o >>= 1) {
+        const unsigned long long other = __shfl_xor(key, o, 64);
+        key = other > key ? other : key;
+    }
+    if ((threadIdx.x & 63) == 0) s_k[threadIdx.x >> 6] = key;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < 4; ++k) key = s_k[k] > key ? s_k[k] : key;
+        *out = (int)(0xFFFFFFFFu - (unsigned)(key & 0xFFFFFFFFull));
     }
 }
 
@@ -909,7 +919,7 @@ int vgx_gemv_launch(const GemvLaunch& L, hipStream_t s) {
                          : L.split_chunk > 0 ? EPI_SPLIT
                          : L.argmax_out ? EPI_STORE_ARGMAX : EPI_STORE;
     const int xm = L.xf ? X_F32 : L.rw ? X_RMS : X_I16;
-    if (epi == EPI_STORE_ARGMAX && !L.counter) return vgx_fail(VGX_EINVAL, "gemv: argmax without a counter");
+    if (epi == EPI_STORE_ARGMAX && !L.argmax_key) return vgx_fail(VGX_EINVAL, "gemv: argmax without key slots");
     switch (L.kind) {
         case VGX_Q8: fn = pick_epi<VGX_Q8>(epi, xm, L.lpr, L.ri); break;
         case VGX_Q4: fn = pick_epi<VGX_Q4>(epi, xm, L.lpr, L.ri); break;
@@ -920,8 +930,13 @@ int vgx_gemv_launch(const GemvLaunch& L, hipStream_t s) {
     if (shm > 160 * 1024) return vgx_fail(VGX_EINVAL, "gemv: activation row too long for LDS");
     if (L.blocks <= 0) return vgx_fail(VGX_EINVAL, "gemv: empty launch");
     const int grid = L.grid > 0 && L.grid < L.blocks ? L.grid : L.blocks;
+    if (epi == EPI_STORE_ARGMAX && grid > L.nkeys) return vgx_fail(VGX_EINVAL, "gemv: more workgroups than key slots");
     hipLaunchKernelGGL(fn, dim3(grid), dim3(kThreads), shm, s, L);
     VGX_LAUNCH_CHECK("gemv launch");
+    if (epi == EPI_STORE_ARGMAX) {
+        hipLaunchKernelGGL(argmax_keys_kernel, dim3(1), dim3(256), 0, s, L.argmax_key, grid, L.argmax_out);
+        VGX_LAUNCH_CHECK("argmax keys launch");
+    }
     return VGX_OK;
 }
 

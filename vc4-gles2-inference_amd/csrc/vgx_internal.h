@@ -73,16 +73,16 @@ struct vgx_group {
     int lpr = 64, ri = 1;
     MatDev* d_dev = nullptr;  // n descriptors with out_off / blk_off filled
     std::vector<MatDev> host;  // the same descriptors, host copy
-    // fused argmax state, 0 at rest: [0] the finished-workgroup count (u32),
-    // [2..3] the running max key (u64)
-    unsigned* counter = nullptr;
+    // fused argmax: one best-key slot (u64) per workgroup of a launch
+    unsigned long long* keys = nullptr;
+    int nkeys = 0;
 };
 
 // ---------------------------------------------------------------------------
 // Launch helpers implemented in vgx_gemv.hip.
-// EPI_STORE_ARGMAX: EPI_STORE, then the last workgroup to finish (a device
-// counter, reset by that workgroup) takes the first-maximum argmax of the
-// whole output.
+// EPI_STORE_ARGMAX: EPI_STORE, and each workgroup stores the best key of its
+// rows in its slot; a one-workgroup launch then reduces the slots to the
+// first-maximum argmax of the whole output.
 enum GemvEpi { EPI_STORE = 0, EPI_STORE_F32 = 1, EPI_GATE = 2, EPI_SPLIT = 3, EPI_STORE_ARGMAX = 4 };
 // How the activation row reaches the kernel: q16, f32 (host quantisation on
 // the device), or q16 through RMSNorm (every workgroup recomputes the
@@ -112,8 +112,8 @@ struct GemvLaunch {
     const int16_t* rw;    // RMSNorm weight, q16 (X_RMS)
     float eps;            // RMSNorm epsilon (X_RMS)
     int* argmax_out;      // EPI_STORE_ARGMAX: the index
-    unsigned* counter;    // EPI_STORE_ARGMAX: finished-workgroup counter, 0 between launches
-    unsigned long long* argmax_key;  // EPI_STORE_ARGMAX: running max key, 0 between launches
+    unsigned long long* argmax_key;  // EPI_STORE_ARGMAX: one key slot per workgroup (nkeys of them)
+    int nkeys;
     int total_rows;       // EPI_STORE_ARGMAX: length of the output
 };
 
