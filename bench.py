@@ -366,6 +366,7 @@ def main():
     ap.add_argument("--decode-runs", type=int, default=5)
     ap.add_argument("--skip-decode", action="store_true")
     ap.add_argument("--copy-mb", type=int, default=0, help="also time a device copy of this many MiB")
+    ap.add_argument("--skip-stream-ref", action="store_true", help="skip the library read/copy bandwidth reference")
     ap.add_argument("--cpu-decode-steps", type=int, default=16)
     ap.add_argument("--only", choices=["gemv", "decode", "prefill", "hybrid", "ternary", "ternary32", "attention"],
                     default=None,
@@ -504,6 +505,28 @@ def main():
         out["roofline"]["traffic_source"] = traffic.get("source")
     g.close()
     torch.cuda.synchronize()
+    if not args.skip_stream_ref:
+        # what plain library kernels reach on this part, beside the GEMV: a
+        # read-only reduction and an elementwise copy, 1 GiB each way
+        big = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(big)
+        ref = {}
+        for name, fn, nbytes in (("torch.sum, float32, 1 GiB read", lambda: big.sum(), big.numel() * 4),
+                                 ("torch.mul, float32, 1 GiB read + 1 GiB written",
+                                  lambda: torch.mul(big, 1.0, out=dst), big.numel() * 8)):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(10):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            gbps = nbytes * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9
+            ref[name] = {"GBps": round(gbps, 1), "frac_of_peak": round(gbps / 8000.0, 4)}
+        out["stream_reference"] = ref
+        del big, dst
     if args.copy_mb:
         # a plain device copy of known size: the scale for the FETCH_SIZE /
         # WRITE_SIZE counters of a profiling run of this command
