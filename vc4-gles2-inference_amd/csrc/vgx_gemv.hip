@@ -55,12 +55,30 @@ __device__ __forceinline__ T shfl_xor(T v, int o) {
     return __shfl_xor(v, o, 64);
 }
 
+// Global-memory views of the pointers in the launch descriptor.  The
+// descriptor arrives by value, so the compiler cannot tell that its pointers
+// address global memory and would emit flat accesses; a flat load also counts
+// on the LDS wait counter, so every wait for an x-plane read from LDS would
+// wait for the weight chunks still in flight as well.  Accesses through these
+// views are global loads and stores (measured: q4 HBM-streamed launches +1.4
+// points of peak, MiniMind3 decode +1%).
+template <typename T>
+using gmem_t = __attribute__((address_space(1))) T;
+template <typename T>
+__device__ __forceinline__ T gld(const T* p) {
+    return *(const gmem_t<T>*)p;
+}
+template <typename T>
+__device__ __forceinline__ void gst(T* p, T v) {
+    *(gmem_t<T>*)p = v;
+}
+
 // A 16-byte weight chunk, loaded with the nontemporal hint: every weight byte
 // is read once per GEMV, so it should not displace reused lines (measured:
 // +15% on HBM-streamed q8/q4 launches, no change on cache-resident decode).
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 wload(const uint8_t* p) {
-    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    const u32x4_t v = __builtin_nontemporal_load((const gmem_t<u32x4_t>*)p);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
@@ -70,7 +88,7 @@ __device__ __forceinline__ int find_mat(const GemvLaunch& L, int blk) {
     int lo = 0, hi = L.nmat - 1;
     while (lo < hi) {
         int mid = (lo + hi + 1) >> 1;
-        const int off = L.nmat <= kInlineMats ? L.md[mid].blk_off : L.mats[mid].blk_off;
+        const int off = L.nmat <= kInlineMats ? L.md[mid].blk_off : gld(&L.mats[mid].blk_off);
         if (off <= blk) lo = mid; else hi = mid - 1;
     }
     return lo;
@@ -128,16 +146,17 @@ __device__ __forceinline__ uint32_t rms_elem(uint32_t xv16, uint32_t wv16, float
 // inverse RMS, rw the q16 weight).  Columns >= K read as zero.
 template <int XM>
 __device__ __forceinline__ void load_x16(const GemvLaunch& L, int col, int K, float inv, uint32_t d[8]) {
-    const int16_t* x = L.x;
+    const gmem_t<int16_t>* x = (const gmem_t<int16_t>*)L.x;
+    const gmem_t<int16_t>* rw = (const gmem_t<int16_t>*)L.rw;
     if (XM != X_F32) {
         if (col + 16 <= K) {
-            const uint4* p = reinterpret_cast<const uint4*>(x + col);
-            uint4 a = p[0], b = p[1];
+            const gmem_t<u32x4_t>* p = reinterpret_cast<const gmem_t<u32x4_t>*>(x + col);
+            const u32x4_t a = p[0], b = p[1];
             d[0] = a.x; d[1] = a.y; d[2] = a.z; d[3] = a.w;
             d[4] = b.x; d[5] = b.y; d[6] = b.z; d[7] = b.w;
             if (XM == X_RMS) {
-                const uint4* q = reinterpret_cast<const uint4*>(L.rw + col);
-                const uint4 c = q[0], e = q[1];
+                const gmem_t<u32x4_t>* q = reinterpret_cast<const gmem_t<u32x4_t>*>(rw + col);
+                const u32x4_t c = q[0], e = q[1];
                 const uint32_t wd[8] = {c.x, c.y, c.z, c.w, e.x, e.y, e.z, e.w};
 #pragma unroll
                 for (int k = 0; k < 8; ++k)
@@ -151,14 +170,14 @@ __device__ __forceinline__ void load_x16(const GemvLaunch& L, int col, int K, fl
                 uint32_t lo = c0 < K ? (uint16_t)x[c0] : 0u;
                 uint32_t hi = c0 + 1 < K ? (uint16_t)x[c0 + 1] : 0u;
                 if (XM == X_RMS) {
-                    lo = c0 < K ? rms_elem(lo, (uint16_t)L.rw[c0], inv) : 0u;
-                    hi = c0 + 1 < K ? rms_elem(hi, (uint16_t)L.rw[c0 + 1], inv) : 0u;
+                    lo = c0 < K ? rms_elem(lo, (uint16_t)rw[c0], inv) : 0u;
+                    hi = c0 + 1 < K ? rms_elem(hi, (uint16_t)rw[c0 + 1], inv) : 0u;
                 }
                 d[k] = lo | (hi << 16);
             }
         }
     } else {
-        const float* xf = L.xf;
+        const gmem_t<float>* xf = (const gmem_t<float>*)L.xf;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             int c0 = col + 2 * k;
@@ -258,13 +277,11 @@ __device__ __forceinline__ int q4_chunk(const uint4 w, const uint4 xhe, const ui
 // launch.  A stored logit q at output row r is the key
 //   (q + 32768) << 32 | (0xFFFFFFFF - r)
 // so the largest key is the largest logit and, among equal logits, the first
-// row.  Each workgroup reduces its keys and folds the result into the device
-// key with atomicMax, then counts itself done; the count's increment is
-// computed from atomicMax's returned value, so the max is performed before
-// the count.  The workgroup that brings the count to gridDim.x takes the key
-// with atomicExch (which leaves 0 for the next launch), decodes the row and
-// resets the count.  Only atomics cross workgroups: nothing waits, nothing
-// is fenced.
+// row.  Each workgroup reduces the keys of its rows and stores the largest in
+// its own slot (argmax_key[blockIdx.x]); a one-workgroup launch on the same
+// stream then reduces the slots and decodes the row.  No two workgroups touch
+// one address and none waits for another: the launch boundary orders the
+// slot stores before their reduction.
 __device__ __forceinline__ unsigned long long argmax_key(int q, int row) {
     return ((unsigned long long)(unsigned)(q + 32768) << 32) | (unsigned long long)(0xFFFFFFFFu - (unsigned)row);
 }
@@ -279,7 +296,7 @@ __device__ __forceinline__ void argmax_tail(const GemvLaunch& L, unsigned long l
     __syncthreads();
     if (threadIdx.x == 0) {
         for (int k = 1; k < kWaves; ++k) key = s_k[k] > key ? s_k[k] : key;
-        L.argmax_key[blockIdx.x] = key;
+        gst(L.argmax_key + blockIdx.x, key);
     }
 }
 
@@ -364,8 +381,8 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
         pb[s] = wload(body + (size_t)u * ustride + (size_t)cc * 16);
         if (EPI == EPI_GATE) pb3[s] = wload(body3 + (size_t)u * ustride + (size_t)cc * 16);
         if (KIND == VGX_Q4) {
-            psm[s] = M.sm[(size_t)u * nch + cc];
-            if (EPI == EPI_GATE) psm3[s] = M3.sm[(size_t)u * nch + cc];
+            psm[s] = gld(M.sm + (size_t)u * nch + cc);
+            if (EPI == EPI_GATE) psm3[s] = gld(M3.sm + (size_t)u * nch + cc);
         }
     };
     auto begin_tile = [&](int tile) {
@@ -380,10 +397,10 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
             for (int hr = 0; hr < RPU; ++hr) {
                 // clamped rows: a row past the end is never stored
                 const int row = min((unit0 + it * RPI + rs) * RPU + hr, M.rows - 1);
-                pw[it][hr] = KIND != VGX_Q4 ? M.wsr[row] : 0.0f;
-                pw3[it][hr] = (KIND != VGX_Q4 && EPI == EPI_GATE) ? M3.wsr[row] : 0.0f;
+                pw[it][hr] = KIND != VGX_Q4 ? gld(M.wsr + row) : 0.0f;
+                pw3[it][hr] = (KIND != VGX_Q4 && EPI == EPI_GATE) ? gld(M3.wsr + row) : 0.0f;
                 const bool has_res = (EPI == EPI_STORE || EPI == EPI_STORE_ARGMAX || EPI == EPI_SPLIT) && L.res;
-                pres[it][hr] = has_res ? (int)L.res[M.out_off + row] : 0;
+                pres[it][hr] = has_res ? (int)gld(L.res + M.out_off + row) : 0;
             }
         }
         if (PF) {
@@ -402,8 +419,8 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
                 w3[it] = ok ? wload(body3 + (size_t)u * ustride + (size_t)c * 16)
                             : make_uint4(0, 0, 0, 0);
             if (KIND == VGX_Q4) {
-                smv[it] = ok ? M.sm[(size_t)u * nch + c] : 0u;
-                if (EPI == EPI_GATE) smv3[it] = ok ? M3.sm[(size_t)u * nch + c] : 0u;
+                smv[it] = ok ? gld(M.sm + (size_t)u * nch + c) : 0u;
+                if (EPI == EPI_GATE) smv3[it] = ok ? gld(M3.sm + (size_t)u * nch + c) : 0u;
             }
         }
     };
@@ -433,7 +450,10 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
         long long P = 0;
         for (int k = sub; k < per; k += 8) {
             const int i = p * per + k;
-            if (i < K) P += (long long)L.x[i] * L.x[i];
+            if (i < K) {
+                const long long xi = gld(L.x + i);
+                P += xi * xi;
+            }
         }
         for (int o = 4; o >= 1; o >>= 1) P += shfl_xor(P, o);
         if (sub == 0) s_rms[p] = (P + 8) >> 4;
@@ -573,11 +593,11 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
                     const bool ok = u < units && cn < nch;
                     wn[it] = ok ? wload(body + (size_t)u * ustride + (size_t)cn * 16)
                                 : make_uint4(0, 0, 0, 0);
-                    sn[it] = ok ? M.sm[(size_t)u * nch + cn] : 0u;
+                    sn[it] = ok ? gld(M.sm + (size_t)u * nch + cn) : 0u;
                     if (EPI == EPI_GATE) {
                         wn3[it] = ok ? wload(body3 + (size_t)u * ustride + (size_t)cn * 16)
                                      : make_uint4(0, 0, 0, 0);
-                        sn3[it] = ok ? M3.sm[(size_t)u * nch + cn] : 0u;
+                        sn3[it] = ok ? gld(M3.sm + (size_t)u * nch + cn) : 0u;
                     }
                 }
             }
@@ -600,22 +620,22 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
             if (u < units) {
                 const float v = (float)acc[0][0];
                 const float rv = PF ? (float)pick(pres, row_it, 0)
-                                    : (L.res ? (float)L.res[M.out_off + u] : 0.0f);
+                                    : (L.res ? (float)gld(L.res + M.out_off + u) : 0.0f);
                 if (EPI == EPI_STORE || EPI == EPI_STORE_ARGMAX) {
                     const float t = L.res ? v + rv : v;
                     const int q = q16_round(t);
-                    static_cast<int16_t*>(L.y)[M.out_off + u] = (int16_t)q;
+                    gst(static_cast<int16_t*>(L.y) + M.out_off + u, (int16_t)q);
                     if (EPI == EPI_STORE_ARGMAX) {
                         const unsigned long long k = argmax_key(q, M.out_off + u);
                         akey = k > akey ? k : akey;
                     }
                 } else if (EPI == EPI_STORE_F32) {
-                    static_cast<float*>(L.y)[M.out_off + u] = v * (1.0f / 256.0f);
+                    gst(static_cast<float*>(L.y) + M.out_off + u, v * (1.0f / 256.0f));
                 } else if (EPI == EPI_SPLIT) {
                     const float vb = (float)acc[0][NV - 1];
                     const float t = v + rv;
                     const float y1 = (float)q16_round(t);
-                    static_cast<int16_t*>(L.y)[u] = (int16_t)q16_round(vb + y1);
+                    gst(static_cast<int16_t*>(L.y) + u, (int16_t)q16_round(vb + y1));
                 } else {  // gate
                     const float vb = (float)acc[0][NV - 1];
                     const float g = (float)q16_round(v), uu = (float)q16_round(vb);
@@ -625,7 +645,7 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
                     const float r = a / dn;
                     float o = r * (uu / 256.0f);
                     o = o * ldexpf(1.0f, -L.hs);
-                    static_cast<int16_t*>(L.y)[u] = (int16_t)q16_round(o * 256.0f);
+                    gst(static_cast<int16_t*>(L.y) + u, (int16_t)q16_round(o * 256.0f));
                 }
             }
         }
@@ -749,25 +769,25 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
             const long long s = 256LL * acc[0][o] + (long long)(uint32_t)acc[0][o + 1] - corr;
             return (float)s * scale;
         };
-        const float sw = PF ? pick(pw, row_it, hr) : M.wsr[row];
-        const float rv = PF ? (float)pick(pres, row_it, hr) : (L.res ? (float)L.res[M.out_off + row] : 0.0f);
+        const float sw = PF ? pick(pw, row_it, hr) : gld(M.wsr + row);
+        const float rv = PF ? (float)pick(pres, row_it, hr) : (L.res ? (float)gld(L.res + M.out_off + row) : 0.0f);
         if (EPI == EPI_STORE || EPI == EPI_STORE_ARGMAX) {
             const float v = val(0, sw);
             const float t = L.res ? v + rv : v;
             const int q = q16_round(t);
-            static_cast<int16_t*>(L.y)[M.out_off + row] = (int16_t)q;
+            gst(static_cast<int16_t*>(L.y) + M.out_off + row, (int16_t)q);
             if (EPI == EPI_STORE_ARGMAX) {
                 const unsigned long long k = argmax_key(q, M.out_off + row);
                 akey = k > akey ? k : akey;
             }
         } else if (EPI == EPI_STORE_F32) {
-            static_cast<float*>(L.y)[M.out_off + row] = val(0, sw) * (1.0f / 256.0f);
+            gst(static_cast<float*>(L.y) + M.out_off + row, val(0, sw) * (1.0f / 256.0f));
         } else if (EPI == EPI_SPLIT) {
             const float va = val(0, sw), vb = val(1, sw);
             const float y1 = (float)q16_round(va + rv);
-            static_cast<int16_t*>(L.y)[row] = (int16_t)q16_round(vb + y1);
+            gst(static_cast<int16_t*>(L.y) + row, (int16_t)q16_round(vb + y1));
         } else {  // gate
-            const float v1 = val(0, sw), v3 = val(1, PF ? pick(pw3, row_it, hr) : M3.wsr[row]);
+            const float v1 = val(0, sw), v3 = val(1, PF ? pick(pw3, row_it, hr) : gld(M3.wsr + row));
             const float g = (float)q16_round(v1), uu = (float)q16_round(v3);
             const float a = g / 256.0f;
             const float e = (float)exp(-(double)a);
@@ -775,7 +795,7 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
             const float r = a / dn;
             float o = r * (uu / 256.0f);
             o = o * ldexpf(1.0f, -L.hs);
-            static_cast<int16_t*>(L.y)[row] = (int16_t)q16_round(o * 256.0f);
+            gst(static_cast<int16_t*>(L.y) + row, (int16_t)q16_round(o * 256.0f));
         }
         }
     }
