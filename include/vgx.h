@@ -135,6 +135,20 @@ int vgx_gemv_group_f32(vgx_ctx* ctx, const vgx_group* g, const float* x, float* 
 int vgx_logits_argmax(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, int16_t* logits,
                       int* token);
 
+/* The candidate pass of GPU::logits_candidates_from (engine/src/gpu_matvec.cpp:
+ * 152-230; kernels top2 / top2_packed, engine/src/shaders_attn.cpp:477-494, 574-594)
+ * over a q16 logits row of n values (device).  For chunk c = logits
+ * [16c, min(16c + 16, n)) out (device, 6 * ceil(n / 16) ints) receives
+ *   v1, i1   the first maximum (q16 value, index into the row)
+ *   v2, i2   the first maximum of the rest (i2 = -1: a one-logit chunk)
+ *   lm       the chunk maximum (q16)
+ *   sum      floor(2048 * S + 1/2), S the kernel's running sum of
+ *            exp((v - max) / T) over the chunk, rescaled as the max grows,
+ *            with T = max(0.0001, temp).
+ * The reference's chunks are per 1536-row logits tile; with every tile but
+ * the last a multiple of 16 rows they are these chunks of the whole row. */
+int vgx_logits_chunks(vgx_ctx* ctx, const int16_t* logits, int n, float temp, int* out);
+
 /* Fused FFN gate: h = q16( SiLU(qz(W1.x)) * qz(W3.x) * 2^-hs ) over all rows
  * -- matvec_q8_pair_swiglu / i4_gate_flat8b (engine/src/shaders.cpp:756-815,
  * 1539-1590) as dispatched by GPU::ffn_split_chunked (engine/src/gpu_ffn.cpp:67-132);
@@ -156,10 +170,11 @@ int vgx_rmsnorm(vgx_ctx* ctx, int dim, const int16_t* x, const int16_t* w, float
  *   vgx_ffn_gate_rms      rmsnorm + vgx_ffn_gate (session.cpp:1516, 1538-1569)
  *   vgx_gemv_group_rms    rmsnorm + vgx_gemv_group
  *   vgx_logits_argmax_rms the final norm + vgx_logits_argmax
- *                         (session.cpp:1580, sampling.cpp:160-162); the
- *                         argmax runs in the same launch (the last workgroup
- *                         to finish takes it), so launches over one group must
- *                         not overlap. */
+ *                         (session.cpp:1580, sampling.cpp:160-162); each
+ *                         workgroup leaves its best key in the group's key
+ *                         slots and a one-workgroup launch on the same stream
+ *                         reduces them, so launches over one group must not
+ *                         overlap. */
 int vgx_gemv_rms(vgx_ctx* ctx, const vgx_mat* W, const int16_t* x, const int16_t* rms_w, float eps,
                  const int16_t* res, int16_t* y);
 int vgx_ffn_gate_rms(vgx_ctx* ctx, const vgx_mat* W1, const vgx_mat* W3, const int16_t* x,

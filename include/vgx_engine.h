@@ -81,6 +81,45 @@ int vgx_engine_generate_batch(vgx_engine* e, int nseq, const int* prompts, int n
 int vgx_engine_save_prefix(vgx_engine* e, const char* path, const int* toks, int n, uint64_t system_fnv,
                            uint64_t tools_fnv);
 int vgx_engine_load_prefix(vgx_engine* e, const char* path, int* toks, int cap, int* n);
+/* One position with the top-k candidates of its logits instead of the logits
+ * (Session::step_candidates, engine/src/session.cpp:1844-1859, over
+ * GPU::logits_candidates_from, engine/src/gpu_matvec.cpp:97-230): the
+ * two largest logits of every 16-logit chunk (vgx_logits_chunks), sorted by
+ * value, the first topk kept in value / cand_token (cap >= topk entries, *n
+ * kept); stats = {logsumexp of logit / T, the largest logit, the softmax
+ * denominator}, T = max(0.0001, temp), from the chunks' (max, sum) pairs.
+ * *complete = 1 when the kept candidates hold at least top_p of the
+ * probability mass; otherwise full (vocab floats) receives the logits, the
+ * reference's fallback to the full read-back. */
+int vgx_engine_step_candidates(vgx_engine* e, int token, int pos, int topk, float temp, float top_p, float* value,
+                               int* cand_token, int cap, int* n, float* stats, int* complete, float* full);
+
+/* ---- token selection on the host (engine/src/sampling.cpp), for the
+ * worker's sampled requests.  Each keeps the reference's float operations and
+ * standard-library selection in order, so a seed draws the reference's token
+ * from the same logits.  Logits are floats (the q16 value / 256). */
+typedef struct vgx_sampler vgx_sampler;
+/* A generator: std::mt19937 seeded with `seed` (the request's, engine/src/worker.cpp:337). */
+int vgx_sampler_create(uint32_t seed, vgx_sampler** out);
+int vgx_sampler_free(vgx_sampler* s);
+/* sample_token / sample_token_report (sampling.cpp:119-142): softmax at temp,
+ * top_k (0 = off) renormalised, top_p prefix, one uniform draw; temp <= 0 is
+ * the first maximum.  logprob (may be NULL): of the token within the kept set. */
+int vgx_sample_logits(vgx_sampler* s, const float* logits, int n, float temp, float top_p, int top_k, int* token,
+                      float* logprob);
+/* argmax_token_report (sampling.cpp:144-155): the first maximum and its
+ * log-probability under the untempered softmax. */
+int vgx_argmax_report(const float* logits, int n, int* token, float* logprob);
+/* sample_candidate_result (sampling.cpp:164-199) over a candidate result
+ * (value / cand_token / n, strict and stats[0] as vgx_engine_step_candidates
+ * gives them); no candidates draws token 2. */
+int vgx_sample_candidates(vgx_sampler* s, const float* value, const int* cand_token, int n, int strict,
+                          float logsumexp, float temp, float top_p, int top_k, int* token);
+/* apply_sampling_penalties (sampling.cpp:16-56) in place, with the settings
+ * (1, 0, 0, 0, 0 = off) passed in; recent: the tokens generated so far. */
+int vgx_apply_penalties(float* logits, int n, const int* recent, int nrecent, float repetition, float frequency,
+                        float presence, int no_repeat_ngram, float min_p);
+
 /* The message of the last failed engine call on this thread. */
 const char* vgx_engine_last_error(void);
 

@@ -1,4 +1,5 @@
-// RMSNorm and the q8 embedding row.
+// RMSNorm, the q8 embedding row, the decode step's device bookkeeping and the
+// logits candidate pass.
 #include <cmath>
 #include <string>
 
@@ -72,6 +73,43 @@ __global__ void embed_q8_kernel(const int8_t* emb, const float* scale, int vocab
     }
 }
 
+// The candidate pass of GPU::logits_candidates_from (engine/src/gpu_matvec.cpp:
+// 152-230; kernels top2 / top2_packed, engine/src/shaders_attn.cpp:477-494 and
+// 574-594): chunk c covers logits [16c, min(16c + 16, n)), scanned in index
+// order.  With strict comparisons v1/i1 is the chunk's first maximum and
+// v2/i2 the first maximum of the rest (i2 = -1 for a one-logit chunk);
+// (lm, ls) is the scan's running maximum and sum of exp((v - lm) * invt), the
+// sum rescaled whenever the maximum grows and stored as
+// floor(ls * 2048 + 1/2).  Values are q16 integers (the logit times 256).
+// One thread per chunk; out holds 6 ints a chunk: v1, i1, v2, i2, lm, the
+// stored sum.
+__global__ void __launch_bounds__(256) chunks_kernel(const int16_t* logits, int n, float invt, int* out) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= (n + 15) / 16) return;
+    const int s = c * 16, e = min(s + 16, n);
+    int v1 = logits[s], i1 = s, v2 = 0, i2 = -1;
+    float lm = (float)v1 / 256.0f, ls = 1.0f;
+    for (int i = s + 1; i < e; ++i) {
+        const int q = logits[i];
+        if (q > v1) {
+            v2 = v1; i2 = i1; v1 = q; i1 = i;
+        } else if (i2 < 0 || q > v2) {
+            v2 = q; i2 = i;
+        }
+        const float v = (float)q / 256.0f;
+        if (v > lm) {
+            ls = ls * (float)exp((double)((lm - v) * invt)) + 1.0f;
+            lm = v;
+        } else {
+            ls += (float)exp((double)((v - lm) * invt));
+        }
+    }
+    int* o = out + (size_t)c * 6;
+    o[0] = v1; o[1] = i1; o[2] = v2; o[3] = i2;
+    o[4] = (int)lrintf(lm * 256.0f);
+    o[5] = (int)floorf(ls * 2048.0f + 0.5f);
+}
+
 // One decode step's bookkeeping on the device: the token just chosen for
 // position *pos + 1 goes to the history, and *pos advances.  One thread.
 __global__ void advance_kernel(int* pos, const int* token, int* hist, int hist_len) {
@@ -90,6 +128,19 @@ int vgx_decode_advance(vgx_ctx* ctx, int* pos, const int* token, int* hist, int 
     VGX_HIP(hipSetDevice(ctx->device));
     hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, ctx->stream, pos, token, hist, hist_len);
     VGX_LAUNCH_CHECK("advance launch");
+    return VGX_OK;
+}
+
+int vgx_logits_chunks(vgx_ctx* ctx, const int16_t* logits, int n, float temp, int* out) {
+    if (!ctx || !logits || !out) return vgx_fail(VGX_EINVAL, "vgx_logits_chunks: NULL argument");
+    if (n <= 0) return vgx_fail(VGX_EINVAL, "vgx_logits_chunks: empty logits row");
+    if (!(temp == temp)) return vgx_fail(VGX_EINVAL, "vgx_logits_chunks: temperature is NaN");
+    // the pass's uniform: invt = 1 / max(0.0001, temp) (engine/src/gpu_matvec.cpp:164)
+    const float invt = 1.0f / (temp > 0.0001f ? temp : 0.0001f);
+    const int nch = (n + 15) / 16;
+    VGX_HIP(hipSetDevice(ctx->device));
+    hipLaunchKernelGGL(chunks_kernel, dim3((nch + 255) / 256), dim3(256), 0, ctx->stream, logits, n, invt, out);
+    VGX_LAUNCH_CHECK("logits chunks launch");
     return VGX_OK;
 }
 

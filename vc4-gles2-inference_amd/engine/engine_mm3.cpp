@@ -9,18 +9,22 @@
 // Flag names follow the reference CLI (engine/src/cli.cpp:26-77: --model,
 // --gen, --greedy, --prefix-cache, --worker; KV=q16|q8 is the reference's
 // environment switch, engine/src/gpu_attn.cpp:59-61).  Text needs the
-// tokenizer, which is outside this build: prompts are token ids, and decoding
-// is greedy.
+// tokenizer, which is outside this build: prompts are token ids, and the
+// command-line generation is greedy.
 //
 // --worker speaks the reference's line protocol (engine/src/worker.cpp:81-435,
 // server/README.md "Worker protocol"): control lines {"op":"load"|"stats"|
 // "cancel"} and tab-separated request lines base64(prompt) \t max_tokens \t
-// temperature \t top_p \t seed [\t ... \t request id in column 13], answered
-// with one JSON event per line (ready, loaded, stats, start, token, done,
-// cancelled, error).  In this build the decoded prompt is a list of token ids
-// ("12 7 99" or "12,7,99"), a token event's text is the id followed by a
-// space, and temperature must be <= 0 (greedy); anything else is answered
-// with an error event.  The rolling prefix reuse is the reference's: the
+// temperature \t top_p \t seed [\t repetition \t frequency \t presence \t
+// no_repeat_ngram \t min_p \t (chat JSON) \t top_k \t request id \t
+// logprobs], answered with one JSON event per line (ready, loaded, stats,
+// start, token, done, cancelled, error).  In this build the decoded prompt is
+// a list of token ids ("12 7 99" or "12,7,99"), a token event's text is the id
+// followed by a space, and a chat-JSON column is answered with an error.
+// Temperature <= 0 decodes greedily on the device; above it each step's
+// logits (or, with --top-k-candidates and a top_k, its top-k candidates) are
+// sampled on the host with the request's seed, as the reference samples.
+// The rolling prefix reuse is the reference's: the
 // common prefix with the previous request (or the loaded prefix cache) is not
 // prefilled again -- except on a hybrid model, whose conv history only
 // matches the whole previous sequence, so a partial reuse prefills from 0.
@@ -42,6 +46,7 @@ static void usage() {
     std::fprintf(stderr,
                  "usage: engine_mm3 --model PATH (--prompt-ids a,b,c | --prompt-random N | --worker) [--gen N]\n"
                  "                  [--seq N] [--kv q16|q8] [--device D] [--seed S] [--greedy]\n"
+                 "                  [--top-k N] [--top-k-candidates]  (worker sampling defaults)\n"
                  "                  [--prefix-cache P.mmkv] [--save-prefix P.mmkv]\n");
 }
 
@@ -204,14 +209,44 @@ struct Worker {
         return true;
     }
 
+    // Process defaults a request may override: --top-k and
+    // --top-k-candidates (engine/src/cli.cpp:45-48); the penalties are off.
+    int top_k = 0;
+    bool top_k_candidates = false;
+
+    // One request (engine/src/worker.cpp:200-409).  Greedy requests
+    // (temperature <= 0, no penalties, no logprobs) keep the token on the
+    // device: the prompt is prefilled in batches and each step's argmax feeds
+    // the next.  Sampled requests read each step's logits -- or, with
+    // --top-k-candidates and a top_k, only its top-k candidates -- and draw on
+    // the host with the request's seed.
     void request(const std::vector<std::string>& f) {
         bool ok = false;
         const std::vector<int> tokens = parse_ids(base64_decode(f[0]), &ok);
         int max_new = std::atoi(f[1].c_str());
         if (max_new < 0) max_new = 0;
         const float temp = (float)std::atof(f[2].c_str());
+        float top_p = (float)std::atof(f[3].c_str());
+        if (top_p <= 0.0f || top_p > 1.0f) top_p = 0.9f;
+        const uint32_t seed = (uint32_t)std::strtoul(f[4].c_str(), nullptr, 10);
+        // columns 6..10: penalties, clamped as the reference clamps them
+        auto col = [&](size_t i) -> const char* { return f.size() > i && !f[i].empty() ? f[i].c_str() : nullptr; };
+        auto clampf = [](float v, float lo, float hi) { return v < lo ? lo : v > hi ? hi : v; };
+        const float rep = col(5) ? clampf((float)std::atof(col(5)), 0.5f, 2.0f) : 1.0f;
+        const float freq = col(6) ? clampf((float)std::atof(col(6)), -2.0f, 2.0f) : 0.0f;
+        const float pres = col(7) ? clampf((float)std::atof(col(7)), -2.0f, 2.0f) : 0.0f;
+        int ngram = col(8) ? std::atoi(col(8)) : 0;
+        ngram = ngram < 0 ? 0 : ngram > 8 ? 8 : ngram;
+        const float min_p = col(9) ? clampf((float)std::atof(col(9)), 0.0f, 1.0f) : 0.0f;
+        if (col(10)) { emit_error("this build takes token ids as the prompt (no chat template)"); return; }
+        int req_top_k = col(11) ? std::atoi(col(11)) : top_k;
+        if (req_top_k < 0) req_top_k = 0;
+        const bool want_logprobs = col(13) && std::atoi(col(13)) != 0;
+        const bool penalties = rep != 1.0f || freq != 0.0f || pres != 0.0f || ngram > 1 || min_p > 0.0f;
+        const bool greedy = temp <= 0.0f;
+        const bool fast_greedy = greedy && !want_logprobs && !penalties;
+        bool cand_mode = top_k_candidates && req_top_k > 0 && !greedy && !penalties && !want_logprobs;
         if (!ok) { emit_error("this build takes token ids as the prompt (no tokenizer)"); return; }
-        if (temp > 0.0f) { emit_error("this build decodes greedily: send temperature <= 0"); return; }
         if (tokens.empty()) { emit_error("empty prompt"); return; }
         for (int t : tokens)
             if (t >= vocab) { emit_error("prompt token outside the vocabulary"); return; }
@@ -226,14 +261,45 @@ struct Worker {
         const int from = common < n ? common : n - 1;
         emit_req("{\"event\":\"start\",\"prompt_tokens\":" + std::to_string(n) + ",\"cached_tokens\":" +
                  std::to_string(common) + ",\"prefill_tokens\":" + std::to_string(n - from) + "}");
+        std::vector<float> logits((size_t)vocab);
+        std::vector<int16_t> q16((size_t)vocab);
+        std::vector<float> cval((size_t)(req_top_k > 0 ? req_top_k : 1));
+        std::vector<int> ctok(cval.size());
+        int ncand = 0, complete = 0;
+        float cstats[3] = {0.0f, 0.0f, 0.0f};
+        // one position: the argmax (greedy), the candidates, or the logits
+        auto step = [&](int tok, int p, int* next) -> bool {
+            int st;
+            if (fast_greedy) {
+                st = vgx_engine_step(e, tok, p, nullptr, next);
+            } else if (cand_mode) {
+                st = vgx_engine_step_candidates(e, tok, p, req_top_k, temp, top_p, cval.data(), ctok.data(),
+                                                (int)cval.size(), &ncand, cstats, &complete, logits.data());
+                if (!st && !complete) cand_mode = false;  // the full logits came back instead
+            } else {
+                st = vgx_engine_step(e, tok, p, q16.data(), nullptr);
+                for (int i = 0; !st && i < vocab; ++i) logits[(size_t)i] = (float)q16[(size_t)i] / 256.0f;
+            }
+            return st == 0;
+        };
         int next = 0;
-        if (vgx_engine_prefill(e, tokens.data() + from, n - from, from, nullptr, &next)) {
+        bool fine = true;
+        if (fast_greedy) {
+            fine = vgx_engine_prefill(e, tokens.data() + from, n - from, from, nullptr, &next) == 0;
+        } else {
+            // the prompt but its last position in batches, the last for its logits
+            if (n - 1 > from) fine = vgx_engine_prefill(e, tokens.data() + from, n - 1 - from, from, nullptr, nullptr) == 0;
+            if (fine) fine = step(tokens[(size_t)n - 1], n - 1, nullptr);
+        }
+        if (!fine) {
             emit_error(vgx_engine_last_error());
             cache_tokens.clear();
             return;
         }
-        std::vector<int> all = tokens;
-        std::string full, finish = "length";
+        vgx_sampler* rng = nullptr;
+        vgx_sampler_create(seed, &rng);
+        std::vector<int> all = tokens, recent;
+        std::string full, finish = "length", lp_rows;
         int pos = n, generated = 0;
         if (max_new > kvlen - pos) max_new = kvlen - pos;
         bool cancelled = false;
@@ -242,6 +308,23 @@ struct Worker {
                 cancelled = true;
                 finish = "cancelled";
                 break;
+            }
+            float lp = 0.0f;
+            if (!fast_greedy) {
+                if (!cand_mode)
+                    vgx_apply_penalties(logits.data(), vocab, recent.data(), (int)recent.size(), rep, freq, pres, ngram,
+                                        min_p);
+                if (want_logprobs) {
+                    if (greedy) vgx_argmax_report(logits.data(), vocab, &next, &lp);
+                    else vgx_sample_logits(rng, logits.data(), vocab, temp, top_p, req_top_k, &next, &lp);
+                } else if (greedy) {
+                    vgx_argmax_report(logits.data(), vocab, &next, nullptr);
+                } else if (cand_mode) {
+                    vgx_sample_candidates(rng, cval.data(), ctok.data(), ncand, 1, cstats[0], temp, top_p, req_top_k,
+                                          &next);
+                } else {
+                    vgx_sample_logits(rng, logits.data(), vocab, temp, top_p, req_top_k, &next, nullptr);
+                }
             }
             // no special ids stated: 1 and 2 end a sequence (engine/src/worker.cpp:361-363)
             if (next == 1 || next == 2) {
@@ -252,16 +335,25 @@ struct Worker {
             const std::string piece = std::to_string(next) + " ";
             full += piece;
             emit_req("{\"event\":\"token\",\"text\":" + json_str(piece) + "}");
+            if (want_logprobs) {
+                char b[64];
+                std::snprintf(b, sizeof b, "%.9g", lp);
+                lp_rows += std::string(lp_rows.empty() ? "" : ",") + "{\"id\":" + std::to_string(next) +
+                           ",\"text\":" + json_str(piece) + ",\"lp\":" + b + "}";
+            }
             ++generated;
             all.push_back(next);
+            recent.push_back(next);
             if (i + 1 < max_new && pos < kvlen) {
-                if (vgx_engine_step(e, next, pos++, nullptr, &next)) {
+                if (!step(next, pos++, &next)) {
                     emit_error(vgx_engine_last_error());
                     cache_tokens.clear();
+                    vgx_sampler_free(rng);
                     return;
                 }
             }
         }
+        vgx_sampler_free(rng);
         // the KV holds every token run through the model: the prompt and each
         // generated token but the last (it was emitted, not yet run)
         if (!all.empty() && (int)all.size() > pos) all.resize((size_t)pos);
@@ -270,7 +362,7 @@ struct Worker {
         emit_req("{\"event\":\"done\",\"text\":" + json_str(full) + ",\"finish_reason\":" + json_str(finish) +
                  ",\"prompt_tokens\":" + std::to_string(n) + ",\"completion_tokens\":" + std::to_string(generated) +
                  ",\"cached_tokens\":" + std::to_string(common) + ",\"prefill_tokens\":" + std::to_string(n - from) +
-                 "}");
+                 (want_logprobs ? ",\"logprobs\":[" + lp_rows + "]" : std::string()) + "}");
     }
 
     bool model_is_hybrid = false;
@@ -329,8 +421,9 @@ struct Worker {
 int main(int argc, char** argv) {
     std::string model, ids, save_prefix, prefix_cache;
     int gen = 8, seq = 0, device = 0, rnd = 0, kv = 0;
-    bool worker = false;
+    bool worker = false, top_k_candidates = false;
     unsigned seed = 0;
+    int top_k = 0;
     if (const char* k = std::getenv("KV")) kv = !std::strcmp(k, "q8") ? 8 : 16;
     if (const char* m = std::getenv("MODEL")) model = m;
     for (int i = 1; i < argc; ++i) {
@@ -351,6 +444,8 @@ int main(int argc, char** argv) {
         else if (a == "--prefix-cache") prefix_cache = next();
         else if (a == "--worker") worker = true;
         else if (a == "--greedy") {}
+        else if (a == "--top-k") top_k = std::atoi(next());
+        else if (a == "--top-k-candidates") top_k_candidates = true;
         else { usage(); return 2; }
     }
     if (model.empty() || kv < 0 || (!worker && ids.empty() && rnd <= 0)) { usage(); return 2; }
@@ -360,6 +455,9 @@ int main(int argc, char** argv) {
         w.seq = seq;
         w.kv = kv ? kv : 16;
         w.prefix_path = prefix_cache;
+        w.top_k = top_k < 0 ? 0 : top_k;
+        // a candidate pass keeps top_k candidates: none without a top_k (engine/src/engine.cpp:82-86)
+        w.top_k_candidates = top_k_candidates && w.top_k > 0;
         if (!w.open_model(model)) { std::fprintf(stderr, "engine_mm3: %s\n", vgx_engine_last_error()); return 1; }
         const int rc = w.run();
         vgx_engine_close(w.e);

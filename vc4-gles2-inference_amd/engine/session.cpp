@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 #include <sys/stat.h>
 
+#include <algorithm>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -14,6 +15,7 @@
 #include <string>
 #include <vector>
 
+#include "engine_err.h"
 #include "mmcf_reader.h"
 #include "vgx.h"
 #include "vgx_engine.h"
@@ -28,6 +30,10 @@ int fail(int st, const std::string& msg) {
 }
 
 }  // namespace
+
+int engine_fail(int status, const std::string& msg) { return fail(status, msg); }
+void engine_clear_error() { g_err.clear(); }
+const std::string& engine_error() { return g_err; }
 
 struct vgx_engine {
     vgxe::Container c;
@@ -76,6 +82,13 @@ struct vgx_engine {
     hipGraphExec_t step_exec = nullptr;
     int *pos_dev = nullptr, *tok_cur = nullptr;
     int pos_host = 0;
+    // the candidate pass: its per-chunk records (device and host); valid when
+    // every LM-head tile but the last has a multiple of 16 rows, so the
+    // reference's per-tile chunks are 16-chunks of the concatenated logits
+    bool cand_tiles_ok = true;
+    int* chunk_dev = nullptr;
+    std::vector<int> chunk_host;
+    std::vector<int16_t> logits_tmp;
 
     ~vgx_engine() {
         if (step_exec) (void)hipGraphExecDestroy(step_exec);
@@ -245,6 +258,7 @@ struct vgx_engine {
         for (int i = 0; c.find(vgxe::T_LOGITS, i); ++i) {
             vgx_mat* t = nullptr;
             if ((st = upload_mat(vgxe::T_LOGITS, i, 0, -1, 0.0f, &t))) return st;
+            if (c.find(vgxe::T_LOGITS, i + 1) && c.find(vgxe::T_LOGITS, i)->rows % 16 != 0) cand_tiles_ok = false;
             head_tiles.push_back(t);
         }
         if (head_tiles.empty()) {
@@ -557,6 +571,84 @@ int vgx_engine_step(vgx_engine* e, int token, int pos, int16_t* logits_host, int
     if (hipMemcpyAsync(&nx, slot, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess) return fail(VGX_EHIP, "token readback");
     if (hipStreamSynchronize(s) != hipSuccess) return fail(VGX_EHIP, "step sync");
     if (next) *next = nx;
+    return VGX_OK;
+}
+
+int vgx_engine_step_candidates(vgx_engine* e, int token, int pos, int topk, float temp, float top_p, float* value,
+                               int* cand_token, int cap, int* n, float* stats, int* complete, float* full) {
+    g_err.clear();
+    if (!e || !value || !cand_token || !n || !stats || !complete || !full)
+        return fail(VGX_EINVAL, "vgx_engine_step_candidates: NULL argument");
+    if (topk <= 0 || cap < topk) return fail(VGX_EINVAL, "vgx_engine_step_candidates: need 0 < top_k <= cap");
+    if (!e->cand_tiles_ok)
+        return fail(VGX_EINVAL, "vgx_engine_step_candidates: an LM-head tile before the last is not a multiple of 16 rows");
+    if (pos < 0 || pos >= e->seq) return fail(VGX_ERANGE, "vgx_engine_step_candidates: position outside the KV length");
+    if (token < 0 || token >= e->m.vocab)
+        return fail(VGX_EINVAL, "vgx_engine_step_candidates: token outside the vocabulary");
+    const int V = e->m.vocab, nch = (V + 15) / 16;
+    int st;
+    if (!e->chunk_dev && (st = e->dalloc(&e->chunk_dev, (size_t)nch * 6))) return st;
+    e->chunk_host.resize((size_t)nch * 6);
+    hipStream_t s = static_cast<hipStream_t>(vgx_ctx_stream(e->ctx));
+    int* slot = e->toks + e->seq;
+    if (hipMemcpyAsync(slot, &token, sizeof(int), hipMemcpyHostToDevice, s) != hipSuccess)
+        return fail(VGX_EHIP, "token upload");
+    if ((st = e->forward(slot, pos, true, slot, e->attn))) return st;
+    if ((st = vgx_logits_chunks(e->ctx, e->logits, V, temp, e->chunk_dev))) return st;
+    if (hipMemcpyAsync(e->chunk_host.data(), e->chunk_dev, (size_t)nch * 6 * sizeof(int), hipMemcpyDeviceToHost, s) !=
+            hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return fail(VGX_EHIP, "candidate readback");
+    // GPU::logits_candidates_from's host side (engine/src/gpu_matvec.cpp:
+    // 175-229): both ranks of every chunk are candidates, in chunk order,
+    // then sorted by value; the softmax denominator comes from the chunks'
+    // (max, sum) pairs rescaled to the global maximum; the top_k kept
+    // candidates are complete when their probability reaches top_p.
+    struct Cand {
+        float value;
+        int token;
+    };
+    std::vector<Cand> cand;
+    cand.reserve((size_t)nch * 2);
+    std::vector<float> cmax((size_t)nch, -1e30f), csum((size_t)nch, 0.0f);
+    float gmax = -1e30f;
+    for (int g = 0; g < nch; ++g) {
+        const int* o = &e->chunk_host[(size_t)g * 6];
+        for (int r = 0; r < 2; ++r) {
+            if (o[2 * r + 1] < 0) continue;  // a one-logit chunk has no second
+            const float v = (float)o[2 * r] / 256.0f;
+            cand.push_back(Cand{v, o[2 * r + 1]});
+            cmax[(size_t)g] = std::max(cmax[(size_t)g], v);
+            gmax = std::max(gmax, v);
+        }
+        const float mx = (float)o[4] / 256.0f;
+        cmax[(size_t)g] = std::max(cmax[(size_t)g], mx);
+        csum[(size_t)g] = (float)o[5] / 2048.0f;
+        gmax = std::max(gmax, mx);
+    }
+    std::sort(cand.begin(), cand.end(), [](const Cand& a, const Cand& b) { return a.value > b.value; });
+    const float T = std::max(0.0001f, temp);
+    float denom = 0.0f;
+    for (int g = 0; g < nch; ++g) denom += csum[(size_t)g] * expf((cmax[(size_t)g] - gmax) / T);
+    if ((int)cand.size() > topk) cand.resize((size_t)topk);
+    float cum = 0.0f;
+    for (const Cand& c : cand) cum += expf((c.value - gmax) / T) / denom;
+    for (size_t i = 0; i < cand.size(); ++i) {
+        value[i] = cand[i].value;
+        cand_token[i] = cand[i].token;
+    }
+    *n = (int)cand.size();
+    stats[0] = logf(denom) + gmax / T;  // logsumexp of v / T
+    stats[1] = gmax;
+    stats[2] = denom;
+    *complete = cum + 1e-6f >= top_p ? 1 : 0;
+    if (!*complete) {
+        // the reference falls back to the full read-back of the same pass
+        e->logits_tmp.resize((size_t)V);
+        if (hipMemcpy(e->logits_tmp.data(), e->logits, (size_t)V * 2, hipMemcpyDeviceToHost) != hipSuccess)
+            return fail(VGX_EHIP, "logits readback");
+        for (int i = 0; i < V; ++i) full[i] = (float)e->logits_tmp[(size_t)i] / 256.0f;
+    }
     return VGX_OK;
 }
 

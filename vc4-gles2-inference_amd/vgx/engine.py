@@ -29,6 +29,17 @@ _SIGS = {
     "vgx_engine_conv_layers": (_I, [_P]),
     "vgx_engine_set_graphs": (_I, [_P, _I]),
     "vgx_engine_load_prefix": (_I, [_P, ctypes.c_char_p, _P, _I, ctypes.POINTER(_I)]),
+    "vgx_engine_step_candidates": (_I, [_P, _I, _I, _I, ctypes.c_float, ctypes.c_float, _P, _P, _I,
+                                        ctypes.POINTER(_I), _P, ctypes.POINTER(_I), _P]),
+    "vgx_sampler_create": (_I, [ctypes.c_uint32, ctypes.POINTER(_P)]),
+    "vgx_sampler_free": (_I, [_P]),
+    "vgx_sample_logits": (_I, [_P, _P, _I, ctypes.c_float, ctypes.c_float, _I, ctypes.POINTER(_I),
+                               ctypes.POINTER(ctypes.c_float)]),
+    "vgx_argmax_report": (_I, [_P, _I, ctypes.POINTER(_I), ctypes.POINTER(ctypes.c_float)]),
+    "vgx_sample_candidates": (_I, [_P, _P, _P, _I, _I, ctypes.c_float, ctypes.c_float, ctypes.c_float, _I,
+                                   ctypes.POINTER(_I)]),
+    "vgx_apply_penalties": (_I, [_P, _I, _P, _I, ctypes.c_float, ctypes.c_float, ctypes.c_float, _I,
+                                 ctypes.c_float]),
     "vgx_engine_last_error": (ctypes.c_char_p, []),
 }
 _lib = None
@@ -130,6 +141,23 @@ class Engine:
                                              ctypes.byref(n)))
         return buf[:n.value].copy()
 
+    def step_candidates(self, token, pos, topk, temp, top_p):
+        """One position's top-k candidates (Session::step_candidates): a dict
+        with values, tokens, logsumexp, max_logit, denom, complete and, when
+        not complete, the full float logits."""
+        value = np.empty(topk, np.float32)
+        tok = np.empty(topk, np.int32)
+        full = np.empty(self.vocab, np.float32)
+        stats = np.empty(3, np.float32)
+        n, comp = ctypes.c_int(), ctypes.c_int()
+        _check(load().vgx_engine_step_candidates(self.h, int(token), int(pos), int(topk), float(temp), float(top_p),
+                                                 value.ctypes.data, tok.ctypes.data, topk, ctypes.byref(n),
+                                                 stats.ctypes.data, ctypes.byref(comp), full.ctypes.data))
+        k = n.value
+        return {"values": value[:k].copy(), "tokens": tok[:k].copy(), "logsumexp": float(stats[0]),
+                "max_logit": float(stats[1]), "denom": float(stats[2]), "complete": bool(comp.value),
+                "full": None if comp.value else full}
+
     def generate_batch(self, prompts, n_gen):
         """Greedy generation for the rows of prompts (nseq x n_prompt) in
         lockstep: (nseq x n_gen tokens, prefill_ms, decode_ms)."""
@@ -151,3 +179,57 @@ class Engine:
             self.close()
         except Exception:
             pass
+
+
+class Sampler:
+    """The host sampler (engine/src/sampling.cpp) with its own std::mt19937."""
+
+    def __init__(self, seed):
+        h = ctypes.c_void_p()
+        _check(load().vgx_sampler_create(ctypes.c_uint32(seed & 0xFFFFFFFF), ctypes.byref(h)))
+        self.h = h
+
+    def sample_logits(self, logits, temp, top_p, top_k=0):
+        """(token, log-probability within the kept set)."""
+        x = np.ascontiguousarray(logits, np.float32)
+        t, lp = ctypes.c_int(), ctypes.c_float()
+        _check(load().vgx_sample_logits(self.h, x.ctypes.data, x.size, float(temp), float(top_p), int(top_k),
+                                        ctypes.byref(t), ctypes.byref(lp)))
+        return t.value, lp.value
+
+    def sample_candidates(self, values, tokens, strict, logsumexp, temp, top_p, top_k):
+        v = np.ascontiguousarray(values, np.float32)
+        k = np.ascontiguousarray(tokens, np.int32)
+        t = ctypes.c_int()
+        _check(load().vgx_sample_candidates(self.h, v.ctypes.data, k.ctypes.data, v.size, int(bool(strict)),
+                                            float(logsumexp), float(temp), float(top_p), int(top_k),
+                                            ctypes.byref(t)))
+        return t.value
+
+    def close(self):
+        if self.h:
+            load().vgx_sampler_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def argmax_report(logits):
+    x = np.ascontiguousarray(logits, np.float32)
+    t, lp = ctypes.c_int(), ctypes.c_float()
+    _check(load().vgx_argmax_report(x.ctypes.data, x.size, ctypes.byref(t), ctypes.byref(lp)))
+    return t.value, lp.value
+
+
+def apply_penalties(logits, recent, repetition=1.0, frequency=0.0, presence=0.0, no_repeat_ngram=0, min_p=0.0):
+    """apply_sampling_penalties on a copy of logits."""
+    x = np.array(logits, np.float32)
+    r = np.ascontiguousarray(recent, np.int32)
+    _check(load().vgx_apply_penalties(x.ctypes.data, x.size, r.ctypes.data if r.size else None, r.size,
+                                      float(repetition), float(frequency), float(presence), int(no_repeat_ngram),
+                                      float(min_p)))
+    return x

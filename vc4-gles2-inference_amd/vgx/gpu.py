@@ -285,6 +285,14 @@ class GPU:
         _l.check(_l.load().vgx_argmax_rows(self.ctx, v.shape[0], v.shape[1], _ptr(v), _ptr(out)))
         return out
 
+    def logits_chunks(self, logits, temp):
+        """The candidate pass over a q16 logits row: an int32 tensor of
+        ceil(n / 16) x 6 chunk records (v1, i1, v2, i2, max, sum on 1/2048)."""
+        n = logits.numel()
+        out = torch.empty(((n + 15) // 16, 6), dtype=torch.int32, device=logits.device)
+        _l.check(_l.load().vgx_logits_chunks(self.ctx, _ptr(logits), n, float(temp), _ptr(out)))
+        return out
+
     # -- GEMV family
     def matvec(self, mat, x, res=None, out=None):
         """matvec_to / matvec_add: y = q16(W.x [+ res])."""

@@ -52,6 +52,7 @@ _SIGS = {
     "vgx_mat_clone": (_I, [_P, _P, ctypes.POINTER(_P)]),
     "vgx_mat_concat": (_I, [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(_P)]),
     "vgx_argmax_rows": (_I, [_P, _I, _I, _P, _P]),
+    "vgx_logits_chunks": (_I, [_P, _P, _I, ctypes.c_float, _P]),
     "vgx_mat_free": (_I, [_P]),
     "vgx_mat_shape": (_I, [_P, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "vgx_mat_weight_bytes": (ctypes.c_size_t, [_P]),
