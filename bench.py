@@ -339,19 +339,31 @@ def prefill_bench(runs):
 
 
 def decode_cpu_baseline(blob, prompt, steps):
-    """The float CPU path (oracle/model.py FModel: the reference's numpy
-    forward semantics on the dequantised container) for `steps` positions."""
+    """The float CPU path for `steps` positions: the reference's float forward
+    on the dequantised container weights (oracle/model.py FModel semantics),
+    run by the C/OpenMP float path (oracle/vgx_float.c), on every host core
+    this process may use and on one."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle as o
-    from model import FModel
+    from model import CFModel, float_lib
 
-    f = FModel(blob)
-    t0 = time.perf_counter()
-    for pos in range(steps):
-        f.step(int(prompt[pos % len(prompt)]), pos)
-    dt = time.perf_counter() - t0
-    return {"tokens_per_s": round(steps / dt, 2), "cores": o.threads(),
-            "sample": "%d positions of the float path (numpy fp32 BLAS, dequantised container weights)" % steps}
+    f = CFModel(blob)
+    lib = float_lib()
+    cores = lib.vgxf_threads()
+
+    def rate():
+        t0 = time.perf_counter()
+        for pos in range(steps):
+            f.step(int(prompt[pos % len(prompt)]), pos)
+        return steps / (time.perf_counter() - t0)
+
+    rate()  # first touch of the weights
+    all_cores = rate()
+    lib.vgxf_set_threads(1)
+    one = rate()
+    lib.vgxf_set_threads(cores)
+    return {"tokens_per_s": round(all_cores, 2), "cores": cores, "one_core_tokens_per_s": round(one, 2),
+            "sample": "%d positions from 0 of the float path (C, fp32 FMA dot products, OpenMP over rows, "
+                      "dequantised container weights)" % steps}
 
 
 def main():
@@ -367,7 +379,7 @@ def main():
     ap.add_argument("--skip-decode", action="store_true")
     ap.add_argument("--copy-mb", type=int, default=0, help="also time a device copy of this many MiB")
     ap.add_argument("--skip-stream-ref", action="store_true", help="skip the library read/copy bandwidth reference")
-    ap.add_argument("--cpu-decode-steps", type=int, default=16)
+    ap.add_argument("--cpu-decode-steps", type=int, default=32)
     ap.add_argument("--only", choices=["gemv", "decode", "prefill", "hybrid", "ternary", "ternary32", "attention"],
                     default=None,
                     help="run one leg (for profiling); the JSON line then carries that leg only")
@@ -549,8 +561,8 @@ def main():
         out["attention_c3"] = attention_bench()
     others = []
     if not args.skip_models:
-        others = [("decode_c4", hybrid_decode_bench(args.decode_runs), 8),
-                  ("decode_c5_batch1", ternary_decode_bench(args.decode_runs), 4)]
+        others = [("decode_c4", hybrid_decode_bench(args.decode_runs), 16),
+                  ("decode_c5_batch1", ternary_decode_bench(args.decode_runs), 8)]
         for key, (_b, _p, _t, res), _n in others:
             out[key] = res
         out["decode_c5_batch32"] = ternary_batch_bench(max(1, args.decode_runs // 2))

@@ -7,10 +7,13 @@ docs/checkpoint-container.md:62-271), independent of the product's.
 
 QModel.step follows Session::forward_gpu_hidden (engine/src/session.cpp:1459-1584)
 with the GPU kernels' numerics (oracle.py); FModel.step follows
-engine/tools/ref_forward.py:47-115 on the dequantised container weights, with
+engine/tools/ref_forward.py:47-115 on the dequantised container weights (CFModel
+runs the same forward through the C/OpenMP float path, oracle/vgx_float.c), with
 the engine's conventions (block RMSNorm eps from key 11 or 1e-5, q/k RMSNorm
 eps 1e-6, RoPE tables of Session, engine/src/session.cpp:188-202).
 """
+import ctypes
+import os
 import struct
 
 import numpy as np
@@ -291,3 +294,86 @@ class FModel(_Base):
             g, u = W["w1"] @ xn, W["w3"] @ xn
             x = x + W["w2"] @ ((g / (1 + np.exp(-g))) * u)
         return self.head @ self._rms(x, self.rms_final, self.eps)
+
+
+class _VgxfModel(ctypes.Structure):
+    _P = ctypes.c_void_p
+    _fields_ = [(n, ctypes.c_int) for n in ("dim", "hidden", "layers", "heads", "kv_heads", "head_dim", "vocab",
+                                            "seq", "rope_half", "qk_norm")] + \
+               [("eps", ctypes.c_float)] + \
+               [(n, ctypes.c_void_p) for n in ("is_conv", "qkv", "wo", "conv_in", "conv_out", "conv_w", "w1", "w3",
+                                               "w2", "rms_att", "rms_ffn", "rms_final", "qn", "kn", "rcos", "rsin",
+                                               "emb", "es", "head")]
+
+
+_FLIB = None
+
+
+def float_lib():
+    """oracle/lib/libvgx_float.so: the float path in C (oracle/vgx_float.c)."""
+    global _FLIB
+    if _FLIB is None:
+        path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libvgx_float.so")
+        if not os.path.exists(path):
+            raise RuntimeError("float-path library missing: run `make -C oracle` (%s)" % path)
+        L = ctypes.CDLL(path)
+        L.vgxf_state_new.restype = ctypes.c_void_p
+        L.vgxf_state_new.argtypes = [ctypes.c_void_p]
+        L.vgxf_state_free.argtypes = [ctypes.c_void_p]
+        L.vgxf_step.restype = ctypes.c_int
+        L.vgxf_step.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+        L.vgxf_threads.restype = ctypes.c_int
+        L.vgxf_set_threads.argtypes = [ctypes.c_int]
+        _FLIB = L
+    return _FLIB
+
+
+class CFModel(FModel):
+    """FModel's float forward run by the C/OpenMP float path (oracle/vgx_float.c)
+    on the same dequantised arrays: the CPU baseline of the decode benchmarks."""
+
+    def __init__(self, blob, seq=None):
+        super().__init__(blob, seq)
+        keep = []
+
+        def arr(a, dt=np.float32):
+            a = np.ascontiguousarray(a, dtype=dt)
+            keep.append(a)
+            return a.ctypes.data
+
+        def ptrs(key):
+            p = (ctypes.c_void_p * self.layers)(*[arr(W[key]) if key in W else None for W in self.W])
+            keep.append(p)
+            return ctypes.cast(p, ctypes.c_void_p)
+
+        cw = (ctypes.c_void_p * self.layers)(*[arr(w) if w is not None else None for w in self.conv_w])
+        keep.append(cw)
+        m = _VgxfModel(dim=self.dim, hidden=self.hidden, layers=self.layers, heads=self.heads,
+                       kv_heads=self.kv_heads, head_dim=self.hd, vocab=self.vocab, seq=self.seq,
+                       rope_half=int(bool(self.rope_half)), qk_norm=int(bool(self.qk_norm)), eps=self.eps)
+        m.is_conv = arr(np.array(self.is_conv, np.int32), np.int32)
+        for key in ("qkv", "wo", "conv_in", "conv_out", "w1", "w3", "w2"):
+            setattr(m, key, ptrs(key))
+        m.conv_w = ctypes.cast(cw, ctypes.c_void_p)
+        m.rms_att, m.rms_ffn, m.rms_final = arr(self.rms_att), arr(self.rms_ffn), arr(self.rms_final)
+        if self.qk_norm:
+            m.qn, m.kn = arr(self.qn), arr(self.kn)
+        m.rcos, m.rsin = arr(self.rcos), arr(self.rsin)
+        m.emb, m.es, m.head = arr(self.emb, np.int8), arr(self.es), arr(self.head)
+        self._keep, self._m = keep, m
+        self._st = float_lib().vgxf_state_new(ctypes.byref(m))
+        if not self._st:
+            raise MemoryError("vgxf_state_new")
+
+    def step(self, token, pos, logits=True):
+        out = np.empty(self.vocab, np.float32) if logits else None
+        rc = float_lib().vgxf_step(ctypes.byref(self._m), self._st, int(token), int(pos),
+                                   out.ctypes.data if logits else None)
+        if rc:
+            raise ValueError("vgxf_step: token or position out of range")
+        return out
+
+    def __del__(self):
+        if getattr(self, "_st", None):
+            float_lib().vgxf_state_free(self._st)
+            self._st = None

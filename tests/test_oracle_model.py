@@ -51,3 +51,22 @@ def test_qmodel_layer0_equals_its_pieces():
     xf = o.rmsnorm(h, o.quantize_act(recs[5][4].view(np.float32)), 1e-5)
     want = np.concatenate([o.store(t.rowval(xf)) for t in q.tiles])
     assert np.array_equal(got, want)
+
+
+def test_c_float_path_equals_numpy_float_path():
+    # the C/OpenMP float path (the decode benchmarks' CPU baseline) runs the
+    # numpy float forward: dense, hybrid-conv and ternary containers, one
+    # thread and all, differ only in fp32 summation order
+    from model import CFModel, float_lib
+    lib = float_lib()
+    cores = lib.vgxf_threads()
+    for spec, scheme in ((synth.tiny_spec(seq=32), "q8"), (synth.tiny_hybrid_spec(seq=32), "q4"),
+                         (synth.tiny_spec(seq=32, qk_norm=False), "t3")):
+        blob = synth.container(spec, scheme, seed=8)
+        for th in (1, cores):
+            lib.vgxf_set_threads(th)
+            f, c = FModel(blob), CFModel(blob)
+            for pos, t in enumerate(synth.prompt(24, spec.vocab, seed=2)):
+                lf, lc = f.step(int(t), pos), c.step(int(t), pos)
+                assert np.abs(lf - lc).max() <= 1e-5 * np.abs(lf).max()
+    lib.vgxf_set_threads(cores)
