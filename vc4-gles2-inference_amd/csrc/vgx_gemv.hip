@@ -64,6 +64,9 @@ __device__ __forceinline__ T shfl_xor(T v, int o) {
 // points of peak, MiniMind3 decode +1%).
 template <typename T>
 using gmem_t = __attribute__((address_space(1))) T;
+// LDS views, for rows the workgroup stages itself.
+template <typename T>
+using lmem_t = __attribute__((address_space(3))) T;
 template <typename T>
 __device__ __forceinline__ T gld(const T* p) {
     return *(const gmem_t<T>*)p;
@@ -80,6 +83,28 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 wload(const uint8_t* p) {
     const u32x4_t v = __builtin_nontemporal_load((const gmem_t<u32x4_t>*)p);
     return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// The first matrix descriptor of the launch, read field by field through the
+// kernel-argument segment (the launch descriptor is the kernel's only
+// argument, at offset 0): scalar loads at fixed offsets.  Reading it through
+// the by-value parameter would go through a generic pointer (the parameter's
+// address is taken), i.e. vector loads the first weight load must wait for.
+__device__ __forceinline__ MatDev kernarg_mat0() {
+    typedef __attribute__((address_space(4))) GemvLaunch karg_t;
+    const karg_t* K = (const karg_t*)__builtin_amdgcn_kernarg_segment_ptr();
+    MatDev m;
+    m.body = K->md[0].body;
+    m.wsr = K->md[0].wsr;
+    m.sm = K->md[0].sm;
+    m.ps = K->md[0].ps;
+    m.kind = K->md[0].kind;
+    m.rows = K->md[0].rows;
+    m.cols = K->md[0].cols;
+    m.out_off = K->md[0].out_off;
+    m.blk_off = K->md[0].blk_off;
+    m.pad0 = m.pad1 = 0;
+    return m;
 }
 
 // Which matrix / row block this block works on.
@@ -142,37 +167,47 @@ __device__ __forceinline__ uint32_t rms_elem(uint32_t xv16, uint32_t wv16, float
 }
 
 // Load 16 consecutive activations as q16 dwords: from int16, from f32 with
-// the host quantisation, or from int16 through RMSNorm (inv = the row's
-// inverse RMS, rw the q16 weight).  Columns >= K read as zero.
+// the host quantisation, or through RMSNorm from the workgroup's LDS copies of
+// x (xr) and the q16 norm weight (wr), inv = the row's inverse RMS.  Columns
+// >= K read as zero.
 template <int XM>
-__device__ __forceinline__ void load_x16(const GemvLaunch& L, int col, int K, float inv, uint32_t d[8]) {
+__device__ __forceinline__ void load_x16(const GemvLaunch& L, int col, int K, float inv, uint32_t d[8],
+                                         const lmem_t<int16_t>* xr, const lmem_t<int16_t>* wr) {
     const gmem_t<int16_t>* x = (const gmem_t<int16_t>*)L.x;
-    const gmem_t<int16_t>* rw = (const gmem_t<int16_t>*)L.rw;
+    if (XM == X_RMS) {
+        // from the workgroup's LDS copies of x and the norm weight
+        if (col + 16 <= K) {
+            const lmem_t<u32x4_t>* p = reinterpret_cast<const lmem_t<u32x4_t>*>(xr + col);
+            const lmem_t<u32x4_t>* q = reinterpret_cast<const lmem_t<u32x4_t>*>(wr + col);
+            const u32x4_t a = p[0], b = p[1], c = q[0], e = q[1];
+            const uint32_t xd[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            const uint32_t wd[8] = {c.x, c.y, c.z, c.w, e.x, e.y, e.z, e.w};
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                d[k] = rms_elem(xd[k] & 0xFFFFu, wd[k] & 0xFFFFu, inv) | (rms_elem(xd[k] >> 16, wd[k] >> 16, inv) << 16);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int c0 = col + 2 * k;
+                const uint32_t lo = c0 < K ? rms_elem((uint16_t)xr[c0], (uint16_t)wr[c0], inv) : 0u;
+                const uint32_t hi = c0 + 1 < K ? rms_elem((uint16_t)xr[c0 + 1], (uint16_t)wr[c0 + 1], inv) : 0u;
+                d[k] = lo | (hi << 16);
+            }
+        }
+        return;
+    }
     if (XM != X_F32) {
         if (col + 16 <= K) {
             const gmem_t<u32x4_t>* p = reinterpret_cast<const gmem_t<u32x4_t>*>(x + col);
             const u32x4_t a = p[0], b = p[1];
             d[0] = a.x; d[1] = a.y; d[2] = a.z; d[3] = a.w;
             d[4] = b.x; d[5] = b.y; d[6] = b.z; d[7] = b.w;
-            if (XM == X_RMS) {
-                const gmem_t<u32x4_t>* q = reinterpret_cast<const gmem_t<u32x4_t>*>(rw + col);
-                const u32x4_t c = q[0], e = q[1];
-                const uint32_t wd[8] = {c.x, c.y, c.z, c.w, e.x, e.y, e.z, e.w};
-#pragma unroll
-                for (int k = 0; k < 8; ++k)
-                    d[k] = rms_elem(d[k] & 0xFFFFu, wd[k] & 0xFFFFu, inv) |
-                           (rms_elem(d[k] >> 16, wd[k] >> 16, inv) << 16);
-            }
         } else {
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
                 int c0 = col + 2 * k;
                 uint32_t lo = c0 < K ? (uint16_t)x[c0] : 0u;
                 uint32_t hi = c0 + 1 < K ? (uint16_t)x[c0 + 1] : 0u;
-                if (XM == X_RMS) {
-                    lo = c0 < K ? rms_elem(lo, (uint16_t)rw[c0], inv) : 0u;
-                    hi = c0 + 1 < K ? rms_elem(hi, (uint16_t)rw[c0 + 1], inv) : 0u;
-                }
                 d[k] = lo | (hi << 16);
             }
         }
@@ -318,6 +353,17 @@ __global__ void __launch_bounds__(256) argmax_keys_kernel(const unsigned long lo
     }
 }
 
+// Dynamic LDS of a launch: the x planes (q8: 32 B per 16 columns; t3 and
+// q4: 64 B per 32 columns), then t3's level table or q4's per-group x sums,
+// then (X_RMS) the copies of x and of the norm weight, 16-byte aligned.
+__host__ __device__ inline size_t lds_bytes(int kind, int cols, int xm) {
+    size_t b = kind == VGX_Q8 ? (size_t)(cols / 16) * 32
+               : kind == VGX_T3 ? (size_t)(cols / 32) * 64 + 256 * 4
+                                : (size_t)(cols / 32) * 64 + (size_t)(cols / 32) * 4;
+    b = (b + 15) & ~(size_t)15;
+    return xm == X_RMS ? b + (size_t)((cols + 7) & ~7) * 4 : b;
+}
+
 // ---------------------------------------------------------------------------
 // The kernel.  One template per (format, lanes per row, rows per lane,
 // epilogue, input type).
@@ -328,7 +374,7 @@ __global__ void __launch_bounds__(256) argmax_keys_kernel(const unsigned long lo
 //   q4 : per 32-col group: xhe, xle, xho, xlo (16 B each)           -> 64 B/group
 //        plus X_g (int32) per group
 //   t3 : + 256 u32 level table
-template <int KIND, int LPR, int RI, int EPI, int XM>
+template <int KIND, int LPR, int RI, int EPI, int XM, bool ONE>
 __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
     extern __shared__ uint4 lds[];
     constexpr int RPI = 64 / LPR;
@@ -386,8 +432,17 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
         }
     };
     auto begin_tile = [&](int tile) {
-        const int mi = L.bpm > 0 ? tile / L.bpm : find_mat(L, tile);
-        M = L.nmat <= kInlineMats ? L.md[mi] : L.mats[mi];
+        // ONE, a single-matrix launch (every decode GEMV but the LM head):
+        // the descriptor at fixed kernel-argument offsets, scalar loads in
+        // one batch at entry, instead of a matrix search and a descriptor
+        // fetch through an index (measured: up to 0.8 us before the first
+        // weight load)
+        if (ONE) {
+            M = kernarg_mat0();
+        } else {
+            const int mi = L.bpm > 0 ? tile / L.bpm : find_mat(L, tile);
+            M = L.nmat <= kInlineMats ? L.md[mi] : L.mats[mi];
+        }
         units = KIND == VGX_T3 ? (M.rows + 1) / 2 : M.rows;
         unit0 = (tile - M.blk_off) * (kWaves * RPI * RI) + wave * (RPI * RI);
         body = M.body;
@@ -440,6 +495,23 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
         for (int b = threadIdx.x; b < 256; b += kThreads) lut[b] = t3_lut_entry((uint32_t)b);
     }
     if (KIND == VGX_Q4) xg = reinterpret_cast<int*>(lds + plane_u4);
+    // X_RMS: x and the norm weight are read from global memory once, 16 bytes
+    // of each per thread, into LDS (after the planes); the statistics and the
+    // normalised planes below read the copies (measured: the second global
+    // read of x and the weight cost ~1 us per launch on the decode shapes)
+    lmem_t<int16_t>* xr = nullptr;
+    lmem_t<int16_t>* wr = nullptr;
+    if (XM == X_RMS) {
+        xr = (lmem_t<int16_t>*)(reinterpret_cast<uint8_t*>(lds) + lds_bytes(KIND, K, X_I16));
+        wr = xr + ((K + 7) & ~7);
+        for (int i = threadIdx.x * 8; i < K; i += kThreads * 8) {
+            const u32x4_t a = gld(reinterpret_cast<const u32x4_t*>(L.x + i));
+            const u32x4_t b = gld(reinterpret_cast<const u32x4_t*>(L.rw + i));
+            *reinterpret_cast<lmem_t<u32x4_t>*>(xr + i) = a;
+            *reinterpret_cast<lmem_t<u32x4_t>*>(wr + i) = b;
+        }
+        __syncthreads();
+    }
     // RMSNorm statistics (rms_stats_split, engine/src/gpu_upload.cpp:280-365):
     // 32 partial sums of x^2 over contiguous slices of ceil(K/32) values, each
     // stored as floor(P/16 + 1/2); 8 lanes per slice.
@@ -451,7 +523,7 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
         for (int k = sub; k < per; k += 8) {
             const int i = p * per + k;
             if (i < K) {
-                const long long xi = gld(L.x + i);
+                const long long xi = xr[i];
                 P += xi * xi;
             }
         }
@@ -471,7 +543,7 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
         for (int c = threadIdx.x; c < nch; c += kThreads) {
             const int hh = (EPI == EPI_SPLIT && c >= L.split_chunk) ? 1 : 0;
             uint32_t d[8], xh[4], xl[4];
-            load_x16<XM>(L, c * 16, K, rinv, d);
+            load_x16<XM>(L, c * 16, K, rinv, d, xr, wr);
             planes16(d, xh, xl);
             lds[2 * c] = make_uint4(xh[0], xh[1], xh[2], xh[3]);
             lds[2 * c + 1] = make_uint4(xl[0], xl[1], xl[2], xl[3]);
@@ -481,9 +553,9 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
         for (int c = threadIdx.x; c < nch; c += kThreads) {
             const int hh = (EPI == EPI_SPLIT && c >= L.split_chunk) ? 1 : 0;
             uint32_t d[8], xh[4], xl[4], xh2[4], xl2[4];
-            load_x16<XM>(L, c * 32, K, rinv, d);
+            load_x16<XM>(L, c * 32, K, rinv, d, xr, wr);
             planes16(d, xh, xl);
-            load_x16<XM>(L, c * 32 + 16, K, rinv, d);
+            load_x16<XM>(L, c * 32 + 16, K, rinv, d, xr, wr);
             planes16(d, xh2, xl2);
             lds[4 * c + 0] = make_uint4(xh[0], xh[1], xh[2], xh[3]);
             lds[4 * c + 1] = make_uint4(xh2[0], xh2[1], xh2[2], xh2[3]);
@@ -497,8 +569,8 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
     } else {  // Q4
         for (int c = threadIdx.x; c < nch; c += kThreads) {
             uint32_t d[8], d2[8];
-            load_x16<XM>(L, c * 32, K, rinv, d);
-            load_x16<XM>(L, c * 32 + 16, K, rinv, d2);
+            load_x16<XM>(L, c * 32, K, rinv, d, xr, wr);
+            load_x16<XM>(L, c * 32 + 16, K, rinv, d2, xr, wr);
             uint32_t he[4], le[4], ho[4], lo[4];
             const uint32_t q0[4] = {d[0], d[1], d[2], d[3]}, q1[4] = {d[4], d[5], d[6], d[7]};
             const uint32_t q2[4] = {d2[0], d2[1], d2[2], d2[3]}, q3[4] = {d2[4], d2[5], d2[6], d2[7]};
@@ -864,10 +936,10 @@ __global__ void dequant_kernel(const MatDev M, float* out) {
 // Dispatch tables.
 using KernFn = void (*)(const GemvLaunch);
 
-template <int KIND, int EPI, int XM>
+template <int KIND, int EPI, int XM, bool ONE>
 KernFn pick_kernel(int lpr, int ri) {
 #define VGX_K(LP, R) \
-    if (lpr == LP && ri == R) return gemv_kernel<KIND, LP, R, EPI, XM>;
+    if (lpr == LP && ri == R) return gemv_kernel<KIND, LP, R, EPI, XM, ONE>;
     // the plan pairs 4 rows per lane with 8 or 16 lanes per row only
     VGX_K(8, 1) VGX_K(8, 4) VGX_K(16, 1) VGX_K(16, 4) VGX_K(32, 1) VGX_K(64, 1)
 #undef VGX_K
@@ -876,27 +948,33 @@ KernFn pick_kernel(int lpr, int ri) {
 
 // The (epilogue, input) pairs the entry points use.
 template <int KIND>
-KernFn pick_epi(int epi, int xm, int lpr, int ri) {
+KernFn pick_epi(int epi, int xm, int lpr, int ri, bool one) {
+    // single-matrix launches: the plain, split, gate and f32 epilogues;
+    // groups: store (plain or through RMSNorm), f32 and the fused argmax
+    if (one) {
+        switch (epi) {
+            case EPI_STORE:
+                return xm == X_RMS ? pick_kernel<KIND, EPI_STORE, X_RMS, true>(lpr, ri)
+                                   : pick_kernel<KIND, EPI_STORE, X_I16, true>(lpr, ri);
+            case EPI_STORE_F32: return pick_kernel<KIND, EPI_STORE_F32, X_F32, true>(lpr, ri);
+            case EPI_GATE:
+                return xm == X_RMS ? pick_kernel<KIND, EPI_GATE, X_RMS, true>(lpr, ri)
+                                   : pick_kernel<KIND, EPI_GATE, X_I16, true>(lpr, ri);
+            case EPI_SPLIT: return xm == X_I16 ? pick_kernel<KIND, EPI_SPLIT, X_I16, true>(lpr, ri) : nullptr;
+        }
+        return nullptr;
+    }
     switch (epi) {
         case EPI_STORE:
-            return xm == X_RMS ? pick_kernel<KIND, EPI_STORE, X_RMS>(lpr, ri)
-                               : pick_kernel<KIND, EPI_STORE, X_I16>(lpr, ri);
-        case EPI_STORE_F32: return pick_kernel<KIND, EPI_STORE_F32, X_F32>(lpr, ri);
-        case EPI_GATE:
-            return xm == X_RMS ? pick_kernel<KIND, EPI_GATE, X_RMS>(lpr, ri)
-                               : pick_kernel<KIND, EPI_GATE, X_I16>(lpr, ri);
-        case EPI_SPLIT: return xm == X_I16 ? pick_kernel<KIND, EPI_SPLIT, X_I16>(lpr, ri) : nullptr;
+            return xm == X_RMS ? pick_kernel<KIND, EPI_STORE, X_RMS, false>(lpr, ri)
+                               : pick_kernel<KIND, EPI_STORE, X_I16, false>(lpr, ri);
+        case EPI_STORE_F32: return pick_kernel<KIND, EPI_STORE_F32, X_F32, false>(lpr, ri);
         case EPI_STORE_ARGMAX:
-            return xm == X_RMS ? pick_kernel<KIND, EPI_STORE_ARGMAX, X_RMS>(lpr, ri) : nullptr;
+            return xm == X_RMS ? pick_kernel<KIND, EPI_STORE_ARGMAX, X_RMS, false>(lpr, ri) : nullptr;
     }
     return nullptr;
 }
 
-size_t lds_bytes(int kind, int cols) {
-    if (kind == VGX_Q8) return (size_t)(cols / 16) * 32;
-    if (kind == VGX_T3) return (size_t)(cols / 32) * 64 + 256 * 4;
-    return (size_t)(cols / 32) * 64 + (size_t)(cols / 32) * 4;
-}
 
 }  // namespace
 
@@ -940,13 +1018,14 @@ int vgx_gemv_launch(const GemvLaunch& L, hipStream_t s) {
                          : L.argmax_out ? EPI_STORE_ARGMAX : EPI_STORE;
     const int xm = L.xf ? X_F32 : L.rw ? X_RMS : X_I16;
     if (epi == EPI_STORE_ARGMAX && !L.argmax_key) return vgx_fail(VGX_EINVAL, "gemv: argmax without key slots");
+    const bool one = L.nmat == 1 && epi != EPI_STORE_ARGMAX;  // the argmax runs over groups only
     switch (L.kind) {
-        case VGX_Q8: fn = pick_epi<VGX_Q8>(epi, xm, L.lpr, L.ri); break;
-        case VGX_Q4: fn = pick_epi<VGX_Q4>(epi, xm, L.lpr, L.ri); break;
-        case VGX_T3: fn = pick_epi<VGX_T3>(epi, xm, L.lpr, L.ri); break;
+        case VGX_Q8: fn = pick_epi<VGX_Q8>(epi, xm, L.lpr, L.ri, one); break;
+        case VGX_Q4: fn = pick_epi<VGX_Q4>(epi, xm, L.lpr, L.ri, one); break;
+        case VGX_T3: fn = pick_epi<VGX_T3>(epi, xm, L.lpr, L.ri, one); break;
     }
     if (!fn) return vgx_fail(VGX_EINVAL, "gemv: no kernel for this shape");
-    const size_t shm = lds_bytes(L.kind, L.cols);
+    const size_t shm = lds_bytes(L.kind, L.cols, xm);
     if (shm > 160 * 1024) return vgx_fail(VGX_EINVAL, "gemv: activation row too long for LDS");
     if (L.blocks <= 0) return vgx_fail(VGX_EINVAL, "gemv: empty launch");
     const int grid = L.grid > 0 && L.grid < L.blocks ? L.grid : L.blocks;
