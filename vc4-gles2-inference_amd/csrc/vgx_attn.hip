@@ -47,7 +47,7 @@ struct AttnDev {
     int vR;      // chunks per round of the weighted-V pass
     int nchmax;  // chunks of a full cache
     // LDS byte offsets
-    int o_wmax, o_newv, o_kpk, o_qhw, o_qlw, o_sc, o_ep, o_csum, o_vpart, o_acc, o_vst;
+    int o_wmax, o_vpk, o_kpk, o_qhw, o_qlw, o_sc, o_ep, o_csum, o_vpart, o_acc, o_vst;
 };
 
 struct vgx_attn {
@@ -110,9 +110,26 @@ __device__ __forceinline__ void rope_pair(int rope_half, int hd, int i, int& j, 
 }
 
 typedef short short2_t __attribute__((ext_vector_type(2)));
+
 // A native 4-word vector: arrays of it stay in registers where arrays of the
 // HIP uint4 struct were demoted to scratch.
 typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+
+// A buffer resource over the rows 0 .. nrows-1 of one head's K or V slice
+// (base: the slice in row 0).  A buffer load past the resource's byte count
+// returns zero and makes no memory access, so the lanes of positions at or
+// past npos read nothing and need no branch.  Third-word value: the raw
+// 32-bit buffer format of the gfx9 family.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const uint8_t* base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), (short)0, bytes, 0x00020000);
+}
+
+// Pins a loaded value into registers at this point.  A select between a
+// load and a constant is otherwise lowered to a branch around the load, and a
+// load under a branch is waited for before the next one issues.
+__device__ __forceinline__ void keep(int& x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void keep(int4& x) { asm volatile("" : "+v"(x.x), "+v"(x.y), "+v"(x.z), "+v"(x.w)); }
+__device__ __forceinline__ void keep(u32x4_t& x) { asm volatile("" : "+v"(x)); }
 
 __device__ __forceinline__ int lo16(unsigned w) { return (int)(short)(w & 0xffffu); }
 __device__ __forceinline__ int hi16(unsigned w) { return (int)w >> 16; }
@@ -172,30 +189,52 @@ __device__ __forceinline__ int v_field(unsigned w, int e) {
 // The V rows of one round of the weighted-V pass (chunks c0 .. c0+vR-1),
 // staged through LDS in 16-byte vectors: vector g = tid + k*kThreads of the
 // round is vector g % (vW/4) of row g / (vW/4).  Rows at or past npos are
-// clamped to row npos-1 (their values are never used).
-__device__ __forceinline__ void v_stage_load(const AttnDev& A, const uint8_t* vhead, int c0, int npos,
+// not read (vrs covers rows 0..npos-1; they stage as zeros, and their weight
+// is zero): at a short context most of the round is past npos, and its loads
+// would fill the memory pipeline for nothing.
+__device__ __forceinline__ void v_stage_load(const AttnDev& A, __amdgpu_buffer_rsrc_t vrs, int c0,
                                              u32x4_t (&v)[kVPre]) {
     const int W4 = A.vW / 4;
 #pragma unroll
     for (int k = 0; k < kVPre; ++k) {
         const int g = (int)threadIdx.x + k * kThreads;
         const int t = g / W4, e4 = g - t * W4;
-        const int row = min(c0 * kChunk + t, npos - 1);
-        v[k] = *reinterpret_cast<const u32x4_t*>(vhead + (size_t)row * A.row_bytes + 16 * e4);
+        const int row = min(c0 * kChunk + t, A.seq);
+        v[k] = __builtin_amdgcn_raw_buffer_load_b128(vrs, row * A.row_bytes + 16 * e4, 0, 0);
     }
 }
 
 // ... and into the V pass's order: row r*kChunk + u, 32-bit word w of the
-// round at vstage[u*kThreads + r*vW + w].
-__device__ __forceinline__ void v_stage_store(const AttnDev& A, unsigned* vstage, const u32x4_t (&v)[kVPre]) {
+// round at vstage[u*kThreads + r*vW + w].  vown (a launch that appends): the
+// packed V of row npos-1, which replaces that row's cache contents (being
+// written by this launch) and the clamped rows past it.
+__device__ __forceinline__ void v_stage_store(const AttnDev& A, unsigned* vstage, const u32x4_t (&v)[kVPre], int c0,
+                                              int npos, const uint8_t* vown) {
     const int W4 = A.vW / 4;
+    u32x4_t x[kVPre];
+#pragma unroll
+    for (int k = 0; k < kVPre; ++k) x[k] = v[k];
+    if (vown) {
+        u32x4_t o[kVPre];
+#pragma unroll
+        for (int k = 0; k < kVPre; ++k) {
+            const int g = (int)threadIdx.x + k * kThreads;
+            o[k] = *reinterpret_cast<const u32x4_t*>(vown + 16 * (g % W4));
+        }
+#pragma unroll
+        for (int k = 0; k < kVPre; ++k) {
+            const int t = ((int)threadIdx.x + k * kThreads) / W4;
+            keep(o[k]);
+            x[k] = c0 * kChunk + t >= npos - 1 ? o[k] : x[k];
+        }
+    }
 #pragma unroll
     for (int k = 0; k < kVPre; ++k) {
         const int g = (int)threadIdx.x + k * kThreads;
         const int t = g / W4, e4 = g - t * W4;
         if (t < A.vR * kChunk) {
             const int r = t / kChunk, u = t - r * kChunk;
-            *reinterpret_cast<u32x4_t*>(vstage + u * kThreads + r * A.vW + 4 * e4) = v[k];
+            *reinterpret_cast<u32x4_t*>(vstage + u * kThreads + r * A.vW + 4 * e4) = x[k];
         }
     }
 }
@@ -207,6 +246,15 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
                                                         int do_write, int do_attend, size_t seq_stride,
                                                         int pos_step, const int* pos_ptr) {
     extern __shared__ __align__(16) uint8_t smem[];
+    // Every kernel argument in scalar registers before the first branch: the
+    // argument loads then issue as one batch instead of one round trip at
+    // each place of first use.
+    asm volatile("" ::"s"(kv), "s"(rtab), "s"(qn), "s"(kn), "s"(qkv), "s"(out), "s"(pos0), "s"(do_write),
+                 "s"(do_attend), "s"(seq_stride), "s"(pos_step), "s"(pos_ptr));
+    asm volatile("" ::"s"(A.dim), "s"(A.kv_heads), "s"(A.hd), "s"(A.seq), "s"(A.rope_half), "s"(A.qk_norm),
+                 "s"(A.group), "s"(A.row_bytes), "s"(A.lpp), "s"(A.vW), "s"(A.vR), "s"(A.nchmax), "s"(A.o_wmax),
+                 "s"(A.o_vpk), "s"(A.o_kpk), "s"(A.o_qhw), "s"(A.o_qlw), "s"(A.o_sc), "s"(A.o_ep), "s"(A.o_csum),
+                 "s"(A.o_vpart), "s"(A.o_acc), "s"(A.o_vst));
     constexpr int E = KVB == 16 ? 2 : 4;  // values per 32-bit word
     constexpr int KP = kKPre<KVB>;
     const int hd = A.hd, G = A.group, kv_dim = A.kv_heads * hd;
@@ -234,12 +282,13 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     const bool own_row = do_write != 0;  // row pos comes from LDS, not from HBM
 
     int* wmax = reinterpret_cast<int*>(smem + A.o_wmax);        // kThreads/64
-    int* newv = reinterpret_cast<int*>(smem + A.o_newv);        // hd
+    uint8_t* vpk = smem + A.o_vpk;                              // row pos's packed V slice
     uint8_t* kpk = smem + A.o_kpk;                              // row pos's packed K slice
     int* qhw = reinterpret_cast<int*>(smem + A.o_qhw);          // hd/E words
     int* qlw = reinterpret_cast<int*>(smem + A.o_qlw);          // hd/E words
     int16_t* sc = reinterpret_cast<int16_t*>(smem + A.o_sc);    // seq
-    float* ep = reinterpret_cast<float*>(smem + A.o_ep);        // nchmax*kChunk
+    // nchmax*kChunk: the exponentials (+0.0 past npos), then the V weights
+    double* ep = reinterpret_cast<double*>(smem + A.o_ep);
     double* csum = reinterpret_cast<double*>(smem + A.o_csum);  // nchmax
     double* vpart = reinterpret_cast<double*>(smem + A.o_vpart);  // vR*hd
     double* acc = reinterpret_cast<double*>(smem + A.o_acc);    // hd
@@ -259,9 +308,11 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     // lanes per position, vectors sj, sj+lpp, ...) and its share of the
     // first round's V rows (16-byte vectors, row-major), which go to LDS in
     // the V pass's order (vstage slot u*kThreads + r*W + w: row r*kChunk + u,
-    // 32-bit word w).  The loads are unconditional, from clamped in-range
-    // addresses, and unused values are discarded afterwards: a predicated
-    // load would be waited for before the next one is issued.
+    // 32-bit word w).  The element loads are unconditional, from clamped
+    // in-range addresses, and unused values are discarded afterwards (a
+    // select between a load and a constant would become a branch whose load
+    // is waited for before the next one issues).  The K and V row loads are
+    // buffer loads bounded to the rows below npos.
     const bool el = tid < hd;
     const int ie = min(tid, hd - 1);
     int j, ti;
@@ -284,14 +335,23 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     const int W = hd / E, vr = tid / W, vw = tid - vr * W;
     uint4 kreg[KP];
     u32x4_t vreg[kVPre];
+    // rows 0..npos-1 of this head's K and V slices
+    const __amdgpu_buffer_rsrc_t krs = rows_rsrc(khead, npos * A.row_bytes);
+    const __amdgpu_buffer_rsrc_t vrs = rows_rsrc(vhead, npos * A.row_bytes);
     {
-        const int t = tid / lpp;
-        const int tk = t < npos ? t : 0;
-        const uint4* src = reinterpret_cast<const uint4*>(khead + (size_t)tk * A.row_bytes);
+        // only the lanes of a scored position read its K row
+        const int t = min(tid / lpp, npos);
 #pragma unroll
-        for (int k = 0; k < KP; ++k) kreg[k] = src[min(sj + k * lpp, nv - 1)];
+        for (int k = 0; k < KP; ++k)
+            kreg[k] = __builtin_bit_cast(
+                uint4, __builtin_amdgcn_raw_buffer_load_b128(krs, t * A.row_bytes + 16 * min(sj + k * lpp, nv - 1), 0, 0));
     }
-    v_stage_load(A, vhead, 0, npos, vreg);
+    v_stage_load(A, vrs, 0, vreg);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        keep(ke[c]);
+        keep(qe[c]);
+    }
 
     // sums of squares of the K head and the query head (exact), whole in
     // every lane: lane l holds elements l, l+64, l+128, l+192
@@ -330,7 +390,7 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
             kv_put<KVB>(row, kv_dim + kvh * hd + tid, qv);
         }
         kv_put<KVB>(kpk, tid, q);
-        newv[tid] = qv;
+        kv_put<KVB>(vpk, tid, qv);
     }
     if (!do_attend) return;
 
@@ -351,7 +411,6 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
         const float o = first ? (qv * co) - (b * sn) : (b * sn) + (qv * co);
         q_split<KVB>(q16_round(o * 256.0f), tid, qhw, qlw);
     }
-    v_stage_store(A, vstage, vreg);
     __syncthreads();
 
     // --- scores (att_score): exact dot, times 1/sqrt(hd), 1/1024 grid; lpp
@@ -366,15 +425,19 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     int ones[KP];
 #pragma unroll
     for (int k = 0; k < KP; ++k) {
-        const int v = sj + k * lpp;
-        const int vc = min(v, nv - 1);
-        const bool in = v < nv;
-        const int4 a = reinterpret_cast<const int4*>(qhw)[vc], b = reinterpret_cast<const int4*>(qlw)[vc];
-        qa[k] = in ? a : make_int4(0, 0, 0, 0);
-        qb[k] = in ? b : make_int4(0, 0, 0, 0);
+        const int vc = min(sj + k * lpp, nv - 1);
+        qa[k] = reinterpret_cast<const int4*>(qhw)[vc];
+        qb[k] = reinterpret_cast<const int4*>(qlw)[vc];
+    }
+#pragma unroll
+    for (int k = 0; k < KP; ++k) {
+        const bool in = sj + k * lpp < nv;
+        keep(qa[k]);
+        keep(qb[k]);
+        qa[k] = in ? qa[k] : make_int4(0, 0, 0, 0);
+        qb[k] = in ? qb[k] : make_int4(0, 0, 0, 0);
         ones[k] = in ? 0x01010101 : 0;
     }
-    const uint4* own4 = reinterpret_cast<const uint4*>(kpk);
     int m = -32768;
     for (int it = 0;; ++it) {
         const int t = tid / lpp + it * P;
@@ -389,13 +452,15 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
 #pragma unroll
             for (int k = 0; k < KP; ++k) w[k] = src[min(sj + k * lpp, nv - 1)];
         }
-        // the own position's K is the LDS copy (its cache row is being written)
-        const bool own = own_row && t == pos;
+        // the own position's K is the LDS copy (its cache row is being
+        // written): one branch, taken by the lanes of one position
+        if (own_row && t == pos) {
+            const uint4* own4 = reinterpret_cast<const uint4*>(kpk);
 #pragma unroll
-        for (int k = 0; k < KP; ++k) {
-            const uint4 o = own4[min(sj + k * lpp, nv - 1)];
-            dot_vec<KVB>(qa[k], qb[k], ones[k], own ? o : w[k], sh, sl, sk);
+            for (int k = 0; k < KP; ++k) w[k] = own4[min(sj + k * lpp, nv - 1)];
         }
+#pragma unroll
+        for (int k = 0; k < KP; ++k) dot_vec<KVB>(qa[k], qb[k], ones[k], w[k], sh, sl, sk);
         long long d = 256ll * sh + sl;
         if (KVB == 8) d += 128ll * sk;
         for (int o = 1; o < lpp; o <<= 1) d += __shfl_xor(d, o, 64);
@@ -407,6 +472,9 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
             m = max(m, (int)f);
         }
     }
+    // the first round's V rows (loaded at the start) into LDS
+    const uint8_t* vown = own_row ? vpk : nullptr;
+    v_stage_store(A, vstage, vreg, 0, npos, vown);
     for (int o = 32; o >= 1; o >>= 1) m = max(m, __shfl_xor(m, o, 64));
     if (lane == 0) wmax[wave] = m;
     __syncthreads();
@@ -417,25 +485,21 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
 #pragma unroll
     for (int w = 0; w < kThreads / 64; ++w) mi = max(mi, wmax[w]);
     const float mx = (float)mi / 1024.0f;
-    for (int t = tid; t < npos; t += kThreads) ep[t] = exp_d((float)sc[t] / 1024.0f - mx);
+    // exponentials to the end of the last chunk, +0.0 past npos: adding +0.0
+    // leaves a sum of non-negative terms unchanged, so the sums below run
+    // over whole chunks without a branch
+    for (int t = tid; t < nch * kChunk; t += kThreads)
+        ep[t] = t < npos ? (double)exp_d((float)sc[t] / 1024.0f - mx) : 0.0;
     __syncthreads();
     for (int c = tid; c < nch; c += kThreads) {
-        const int n = min(kChunk, npos - c * kChunk);
-        const float4* e4 = reinterpret_cast<const float4*>(ep + c * kChunk);
-        float e[kChunk];
-#pragma unroll
-        for (int k = 0; k < kChunk / 4; ++k) {
-            const float4 f = e4[k];
-            e[4 * k] = f.x;
-            e[4 * k + 1] = f.y;
-            e[4 * k + 2] = f.z;
-            e[4 * k + 3] = f.w;
-        }
-        // adding +0.0 leaves a sum of non-negative terms unchanged: the
-        // positions past npos are selected out without a branch
+        const double2* e2 = reinterpret_cast<const double2*>(ep + c * kChunk);
         double cs = 0.0;
 #pragma unroll
-        for (int u = 0; u < kChunk; ++u) cs += u < n ? (double)e[u] : 0.0;
+        for (int k = 0; k < kChunk / 2; ++k) {
+            const double2 f = e2[k];
+            cs += f.x;
+            cs += f.y;
+        }
         csum[c] = cs;
     }
     __syncthreads();
@@ -458,51 +522,38 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
 
     // --- weighted V (att_v): rounds of vR chunks; a thread sums E elements
     // (one 32-bit word) of one chunk, each in position order, then the
-    // round's chunk sums join the running total in chunk order
-    // a += p*v with v = q*vunit: p (24-bit mantissa) times q (at most 16
-    // bits) is exact in double, so fma(p*vunit, q, a) rounds exactly as the
-    // add of the product does
-    const float vunit = KVB == 16 ? 1.0f / 2048.0f : 1.0f / 16.0f;
-    const double vunit_d = vunit;
+    // round's chunk sums join the running total in chunk order.
+    // The weight of position t, p = e*iv (float) times the V grid unit, is
+    // formed once: a += p*v with v = q*vunit, and p (24-bit mantissa) times
+    // q (at most 16 bits) is exact in double, so fma(p*vunit, q, a) rounds
+    // exactly as the add of the product does.  Past npos the weight is +0.0:
+    // a + 0*q is a (a is never -0), so every slot runs without a branch.
+    const double vunit_d = KVB == 16 ? 1.0 / 2048.0 : 1.0 / 16.0;
+    for (int t = tid; t < nch * kChunk; t += kThreads)
+        ep[t] = t < npos ? (double)((float)ep[t] * iv) * vunit_d : 0.0;
+    __syncthreads();
     for (int c0 = 0; c0 < nch; c0 += A.vR) {
         const int nr = min(A.vR, nch - c0);
         if (c0 > 0) {
             // a later round: its rows through the same LDS slots
-            v_stage_load(A, vhead, c0, npos, vreg);
-            v_stage_store(A, vstage, vreg);
+            v_stage_load(A, vrs, c0, vreg);
+            v_stage_store(A, vstage, vreg, c0, npos, vown);
             __syncthreads();
         }
         if (vr < nr) {
-            const int t0 = (c0 + vr) * kChunk, t1 = min(t0 + kChunk, npos);
-            const int tend = (own_row && t1 == npos) ? t1 - 1 : t1;
-            const int n = tend - t0;
+            const int t0 = (c0 + vr) * kChunk;
             double a[E];
 #pragma unroll
             for (int e = 0; e < E; ++e) a[e] = 0.0;
-            const float4* e4 = reinterpret_cast<const float4*>(ep + t0);
+            const double2* w2 = reinterpret_cast<const double2*>(ep + t0);
 #pragma unroll
-            for (int k = 0; k < kChunk / 4; ++k) {
-                const float4 f = e4[k];
-                const float pe[4] = {f.x, f.y, f.z, f.w};
-                unsigned wv[4];
+            for (int k = 0; k < kChunk / 2; ++k) {
+                const double2 w = w2[k];
+                const unsigned v0 = vstage[(2 * k) * kThreads + tid], v1 = vstage[(2 * k + 1) * kThreads + tid];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) wv[u] = vstage[(4 * k + u) * kThreads + tid];
-                // a position past the chunk's end gets weight +0.0: a + 0*q is a
-                // (a is never -0), so every slot runs without a branch
+                for (int e = 0; e < E; ++e) a[e] = fma(w.x, (double)v_field<KVB>(v0, e), a[e]);
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const double pp = 4 * k + u < n ? (double)(pe[u] * iv) * vunit_d : 0.0;
-#pragma unroll
-                    for (int e = 0; e < E; ++e) a[e] = fma(pp, (double)v_field<KVB>(wv[u], e), a[e]);
-                }
-            }
-            if (tend != t1) {
-                const float p = ep[pos] * iv;
-#pragma unroll
-                for (int e = 0; e < E; ++e) {
-                    const float v = (float)newv[vw * E + e] * vunit;
-                    a[e] += (double)p * (double)v;
-                }
+                for (int e = 0; e < E; ++e) a[e] = fma(w.y, (double)v_field<KVB>(v1, e), a[e]);
             }
 #pragma unroll
             for (int e = 0; e < E; ++e) vpart[vr * hd + vw * E + e] = a[e];
@@ -543,12 +594,12 @@ size_t attn_layout(AttnDev& A) {
         return (int)o;
     };
     A.o_wmax = take(4 * (size_t)(kThreads / 64));
-    A.o_newv = take(4 * (size_t)hd);
+    A.o_vpk = take((size_t)hd * A.kv_bits / 8);
     A.o_kpk = take((size_t)hd * A.kv_bits / 8);
     A.o_qhw = take(4 * (size_t)(hd / E));
     A.o_qlw = take(4 * (size_t)(hd / E));
     A.o_sc = take(2 * (size_t)A.seq);
-    A.o_ep = take(4 * (size_t)A.nchmax * kChunk);
+    A.o_ep = take(8 * (size_t)A.nchmax * kChunk);
     A.o_csum = take(8 * (size_t)A.nchmax);
     A.o_vpart = take(8 * (size_t)A.vR * hd);
     A.o_acc = take(8 * (size_t)hd);
