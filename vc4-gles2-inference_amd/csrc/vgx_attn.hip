@@ -33,9 +33,6 @@ constexpr int kChunk = 32;  // positions per chunk of the summation order
 // 16-byte K vectors a lane holds for one scored position (int16 / int8 cache)
 template <int KVB>
 constexpr int kKPre = KVB == 16 ? 8 : 4;
-// 16-byte V vectors a thread stages per round (vR*vW <= kThreads words per
-// row position, kChunk positions per chunk)
-constexpr int kVPre = kChunk / 4;
 
 }  // namespace
 
@@ -43,11 +40,11 @@ struct AttnDev {
     int dim, heads, kv_heads, hd, seq, kv_bits, rope_half, qk_norm, group;
     int row_bytes;
     int lpp;     // lanes per scored position (a power of two)
-    int vW;      // 32-bit words per V row slice of one head
-    int vR;      // chunks per round of the weighted-V pass
+    int vG;      // waves per chunk of the weighted-V pass (64 elements each)
+    int vC;      // chunks per round of the weighted-V pass
     int nchmax;  // chunks of a full cache
     // LDS byte offsets
-    int o_wmax, o_vpk, o_kpk, o_qhw, o_qlw, o_sc, o_ep, o_csum, o_vpart, o_acc, o_vst;
+    int o_wmax, o_vpk, o_kpk, o_qhw, o_qlw, o_sc, o_ep, o_csum, o_vpart, o_acc;
 };
 
 struct vgx_attn {
@@ -111,10 +108,6 @@ __device__ __forceinline__ void rope_pair(int rope_half, int hd, int i, int& j, 
 
 typedef short short2_t __attribute__((ext_vector_type(2)));
 
-// A native 4-word vector: arrays of it stay in registers where arrays of the
-// HIP uint4 struct were demoted to scratch.
-typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
-
 // A buffer resource over the rows 0 .. nrows-1 of one head's K or V slice
 // (base: the slice in row 0).  A buffer load past the resource's byte count
 // returns zero and makes no memory access, so the lanes of positions at or
@@ -129,11 +122,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const uint8_t* base,
 // load under a branch is waited for before the next one issues.
 __device__ __forceinline__ void keep(int& x) { asm volatile("" : "+v"(x)); }
 __device__ __forceinline__ void keep(int4& x) { asm volatile("" : "+v"(x.x), "+v"(x.y), "+v"(x.z), "+v"(x.w)); }
-__device__ __forceinline__ void keep(u32x4_t& x) { asm volatile("" : "+v"(x)); }
-
-__device__ __forceinline__ int lo16(unsigned w) { return (int)(short)(w & 0xffffu); }
-__device__ __forceinline__ int hi16(unsigned w) { return (int)w >> 16; }
-__device__ __forceinline__ int byte_s(unsigned w, int k) { return ((int)(w << (24 - 8 * k))) >> 24; }
 
 // The query split into bytes for the packed integer dot products: q = 256*qh
 // + ql with qh in [-128, 127] and ql in [0, 255].  Word w of qhw / qlw holds
@@ -179,64 +167,55 @@ __device__ __forceinline__ void dot_vec(const int4 a, const int4 b, int ones, co
     }
 }
 
-// Value e of a 32-bit word of a V row: int16 (KVB 16) or int8 (KVB 8).
+// The V values of one chunk for one lane's element vi: position c*kChunk + u
+// in vch[u].  vrs covers rows 0..npos-1: a row at or past npos reads nothing
+// and gives zero (its weight is zero too).  An idle wave passes a chunk past
+// the cache.
 template <int KVB>
-__device__ __forceinline__ int v_field(unsigned w, int e) {
-    if (KVB == 16) return e == 0 ? lo16(w) : hi16(w);
-    return byte_s(w, e);
-}
-
-// The V rows of one round of the weighted-V pass (chunks c0 .. c0+vR-1),
-// staged through LDS in 16-byte vectors: vector g = tid + k*kThreads of the
-// round is vector g % (vW/4) of row g / (vW/4).  Rows at or past npos are
-// not read (vrs covers rows 0..npos-1; they stage as zeros, and their weight
-// is zero): at a short context most of the round is past npos, and its loads
-// would fill the memory pipeline for nothing.
-__device__ __forceinline__ void v_stage_load(const AttnDev& A, __amdgpu_buffer_rsrc_t vrs, int c0,
-                                             u32x4_t (&v)[kVPre]) {
-    const int W4 = A.vW / 4;
+__device__ __forceinline__ void v_chunk_load(const AttnDev& A, __amdgpu_buffer_rsrc_t vrs, int c, int vi,
+                                             int (&vch)[kChunk]) {
 #pragma unroll
-    for (int k = 0; k < kVPre; ++k) {
-        const int g = (int)threadIdx.x + k * kThreads;
-        const int t = g / W4, e4 = g - t * W4;
-        const int row = min(c0 * kChunk + t, A.seq);
-        v[k] = __builtin_amdgcn_raw_buffer_load_b128(vrs, row * A.row_bytes + 16 * e4, 0, 0);
+    for (int u = 0; u < kChunk; ++u) {
+        const int off = min(c * kChunk + u, A.seq) * A.row_bytes + vi * (KVB / 8);
+        if (KVB == 16) vch[u] = (int)(int16_t)__builtin_amdgcn_raw_buffer_load_b16(vrs, off, 0, 0);
+        else vch[u] = (int)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(vrs, off, 0, 0);
     }
 }
 
-// ... and into the V pass's order: row r*kChunk + u, 32-bit word w of the
-// round at vstage[u*kThreads + r*vW + w].  vown (a launch that appends): the
-// packed V of row npos-1, which replaces that row's cache contents (being
-// written by this launch) and the clamped rows past it.
-__device__ __forceinline__ void v_stage_store(const AttnDev& A, unsigned* vstage, const u32x4_t (&v)[kVPre], int c0,
-                                              int npos, const uint8_t* vown) {
-    const int W4 = A.vW / 4;
-    u32x4_t x[kVPre];
-#pragma unroll
-    for (int k = 0; k < kVPre; ++k) x[k] = v[k];
-    if (vown) {
-        u32x4_t o[kVPre];
-#pragma unroll
-        for (int k = 0; k < kVPre; ++k) {
-            const int g = (int)threadIdx.x + k * kThreads;
-            o[k] = *reinterpret_cast<const u32x4_t*>(vown + 16 * (g % W4));
-        }
-#pragma unroll
-        for (int k = 0; k < kVPre; ++k) {
-            const int t = ((int)threadIdx.x + k * kThreads) / W4;
-            keep(o[k]);
-            x[k] = c0 * kChunk + t >= npos - 1 ? o[k] : x[k];
-        }
-    }
-#pragma unroll
-    for (int k = 0; k < kVPre; ++k) {
-        const int g = (int)threadIdx.x + k * kThreads;
-        const int t = g / W4, e4 = g - t * W4;
-        if (t < A.vR * kChunk) {
-            const int r = t / kChunk, u = t - r * kChunk;
-            *reinterpret_cast<u32x4_t*>(vstage + u * kThreads + r * A.vW + 4 * e4) = x[k];
-        }
-    }
+// Lane exchanges within rows of 16 lanes (DPP): quad_perm [1,0,3,2], quad_perm
+// [2,3,0,1], row_half_mirror, row_mirror.  After the four steps of a
+// reduction every lane of a row holds the row's result; the four rows are
+// joined through readlane.  Called with every lane of the wave active.
+template <int CTRL>
+__device__ __forceinline__ int dpp(int x) { return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xF, 0xF, false); }
+template <int CTRL>
+__device__ __forceinline__ double dpp(double x) {
+    const unsigned long long b = __builtin_bit_cast(unsigned long long, x);
+    const unsigned lo = (unsigned)dpp<CTRL>((int)(unsigned)b), hi = (unsigned)dpp<CTRL>((int)(unsigned)(b >> 32));
+    return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+__device__ __forceinline__ double readlane_d(double x, int l) {
+    const unsigned long long b = __builtin_bit_cast(unsigned long long, x);
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, l);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(b >> 32), l);
+    return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+__device__ __forceinline__ int wave_max(int x) {
+    x = max(x, dpp<0xB1>(x));
+    x = max(x, dpp<0x4E>(x));
+    x = max(x, dpp<0x141>(x));
+    x = max(x, dpp<0x140>(x));
+    return max(max(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16)),
+               max(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48)));
+}
+// The sum over the wave of integers held in doubles, every partial sum below
+// 2^53: exact, so the order of the additions does not matter.
+__device__ __forceinline__ double wave_sum_exact(double x) {
+    x += dpp<0xB1>(x);
+    x += dpp<0x4E>(x);
+    x += dpp<0x141>(x);
+    x += dpp<0x140>(x);
+    return (readlane_d(x, 0) + readlane_d(x, 16)) + (readlane_d(x, 32) + readlane_d(x, 48));
 }
 
 template <int KVB>
@@ -252,9 +231,9 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     asm volatile("" ::"s"(kv), "s"(rtab), "s"(qn), "s"(kn), "s"(qkv), "s"(out), "s"(pos0), "s"(do_write),
                  "s"(do_attend), "s"(seq_stride), "s"(pos_step), "s"(pos_ptr));
     asm volatile("" ::"s"(A.dim), "s"(A.kv_heads), "s"(A.hd), "s"(A.seq), "s"(A.rope_half), "s"(A.qk_norm),
-                 "s"(A.group), "s"(A.row_bytes), "s"(A.lpp), "s"(A.vW), "s"(A.vR), "s"(A.nchmax), "s"(A.o_wmax),
+                 "s"(A.group), "s"(A.row_bytes), "s"(A.lpp), "s"(A.vG), "s"(A.vC), "s"(A.nchmax), "s"(A.o_wmax),
                  "s"(A.o_vpk), "s"(A.o_kpk), "s"(A.o_qhw), "s"(A.o_qlw), "s"(A.o_sc), "s"(A.o_ep), "s"(A.o_csum),
-                 "s"(A.o_vpart), "s"(A.o_acc), "s"(A.o_vst));
+                 "s"(A.o_vpart), "s"(A.o_acc));
     constexpr int E = KVB == 16 ? 2 : 4;  // values per 32-bit word
     constexpr int KP = kKPre<KVB>;
     const int hd = A.hd, G = A.group, kv_dim = A.kv_heads * hd;
@@ -290,9 +269,8 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     // nchmax*kChunk: the exponentials (+0.0 past npos), then the V weights
     double* ep = reinterpret_cast<double*>(smem + A.o_ep);
     double* csum = reinterpret_cast<double*>(smem + A.o_csum);  // nchmax
-    double* vpart = reinterpret_cast<double*>(smem + A.o_vpart);  // vR*hd
+    double* vpart = reinterpret_cast<double*>(smem + A.o_vpart);  // vC*hd
     double* acc = reinterpret_cast<double*>(smem + A.o_acc);    // hd
-    unsigned* vstage = reinterpret_cast<unsigned*>(smem + A.o_vst);  // kChunk*kThreads
 
     const uint8_t* khead = kv + (size_t)kvh * hd * (KVB / 8);
     const uint8_t* vhead = kv + (size_t)(kv_dim + kvh * hd) * (KVB / 8);
@@ -305,10 +283,9 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     // so that their latencies overlap: this thread's element i = tid of q, K,
     // V with its RoPE partner j, the rotation, the norm weights; the elements
     // of the sums of squares; the K vectors of its first scored position (lpp
-    // lanes per position, vectors sj, sj+lpp, ...) and its share of the
-    // first round's V rows (16-byte vectors, row-major), which go to LDS in
-    // the V pass's order (vstage slot u*kThreads + r*W + w: row r*kChunk + u,
-    // 32-bit word w).  The element loads are unconditional, from clamped
+    // lanes per position, vectors sj, sj+lpp, ...) and the V values of its
+    // element in its wave's chunk of the first round of the weighted-V pass
+    // (below).  The element loads are unconditional, from clamped
     // in-range addresses, and unused values are discarded afterwards (a
     // select between a load and a constant would become a branch whose load
     // is waited for before the next one issues).  The K and V row loads are
@@ -332,9 +309,13 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     }
     const int nv = hd * KVB / 128;  // 16-byte vectors per K row slice
     const int lpp = A.lpp, sj = tid & (lpp - 1), P = kThreads / lpp;
-    const int W = hd / E, vr = tid / W, vw = tid - vr * W;
+    // weighted-V lanes: wave w takes chunk slot w / vG of each round and the
+    // elements 64*(w % vG) + lane of the head
+    // (slot is wave-uniform; readfirstlane lets the compiler see it)
+    const int slot = __builtin_amdgcn_readfirstlane(wave / A.vG);
+    const int ve = (wave - slot * A.vG) * 64 + lane, vi = min(ve, hd - 1);
     uint4 kreg[KP];
-    u32x4_t vreg[kVPre];
+    int vch[kChunk];  // V of element vi at the chunk's positions
     // rows 0..npos-1 of this head's K and V slices
     const __amdgpu_buffer_rsrc_t krs = rows_rsrc(khead, npos * A.row_bytes);
     const __amdgpu_buffer_rsrc_t vrs = rows_rsrc(vhead, npos * A.row_bytes);
@@ -346,27 +327,28 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
             kreg[k] = __builtin_bit_cast(
                 uint4, __builtin_amdgcn_raw_buffer_load_b128(krs, t * A.row_bytes + 16 * min(sj + k * lpp, nv - 1), 0, 0));
     }
-    v_stage_load(A, vrs, 0, vreg);
+    // the K loads first: the scores wait for them, not for the V loads after
+    asm volatile("" ::: "memory");
+    v_chunk_load<KVB>(A, vrs, slot < A.vC ? slot : A.nchmax, vi, vch);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         keep(ke[c]);
         keep(qe[c]);
     }
 
-    // sums of squares of the K head and the query head (exact), whole in
-    // every lane: lane l holds elements l, l+64, l+128, l+192
-    long long ssk = 0, ssq = 0;
+    // sums of squares of the K head and the query head (exact integers in
+    // doubles, below 2^39), whole in every wave: lane l holds elements l,
+    // l+64, l+128, l+192
+    double ssk = 0.0, ssq = 0.0;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         const bool in = lane + 64 * c < hd;
         const int kc = in ? ke[c] : 0, qc = in ? qe[c] : 0;
-        ssk += (long long)(kc * kc);
-        ssq += (long long)(qc * qc);
+        ssk += (double)(kc * kc);
+        ssq += (double)(qc * qc);
     }
-    for (int o = 32; o >= 1; o >>= 1) {
-        ssk += __shfl_xor(ssk, o, 64);
-        ssq += __shfl_xor(ssq, o, 64);
-    }
+    ssk = wave_sum_exact(ssk);
+    ssq = wave_sum_exact(ssq);
     const float co = (float)rc / 4096.0f, sn = (float)rs / 4096.0f;
 
     // --- KV pack of position pos (att_kv_rope)
@@ -421,6 +403,8 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     // The lane's query words are the same for every position: held in
     // registers, zeroed for a vector past the row, so the dot products below
     // run on every vector slot without branches.
+    int m = -32768;
+    if (tid / lpp < npos) {  // the threads of a scored position
     int4 qa[KP], qb[KP];
     int ones[KP];
 #pragma unroll
@@ -438,7 +422,6 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
         qb[k] = in ? qb[k] : make_int4(0, 0, 0, 0);
         ones[k] = in ? 0x01010101 : 0;
     }
-    int m = -32768;
     for (int it = 0;; ++it) {
         const int t = tid / lpp + it * P;
         if (t >= npos) break;
@@ -472,10 +455,8 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
             m = max(m, (int)f);
         }
     }
-    // the first round's V rows (loaded at the start) into LDS
-    const uint8_t* vown = own_row ? vpk : nullptr;
-    v_stage_store(A, vstage, vreg, 0, npos, vown);
-    for (int o = 32; o >= 1; o >>= 1) m = max(m, __shfl_xor(m, o, 64));
+    }
+    m = wave_max(m);
     if (lane == 0) wmax[wave] = m;
     __syncthreads();
 
@@ -505,13 +486,12 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     __syncthreads();
     float iv;
     {
+        // lane l reads chunk sum l; the wave adds them in chunk order
         double sum = 0.0;
-        for (int c0 = 0; c0 < nch; c0 += 8) {
-            double cv[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) cv[k] = csum[min(c0 + k, A.nchmax - 1)];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) sum += c0 + k < nch ? cv[k] : 0.0;
+        for (int c0 = 0; c0 < nch; c0 += 64) {
+            const double cv = csum[min(c0 + lane, A.nchmax - 1)];
+            const int nn = min(64, nch - c0);
+            for (int k = 0; k < nn; ++k) sum += readlane_d(cv, k);
         }
         const float fs = (float)sum;
         float qs = floorf(fs * 32.0f + 0.5f);
@@ -520,43 +500,38 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
         iv = sd > 0.0f ? 1.0f / sd : 0.0f;
     }
 
-    // --- weighted V (att_v): rounds of vR chunks; a thread sums E elements
-    // (one 32-bit word) of one chunk, each in position order, then the
-    // round's chunk sums join the running total in chunk order.
-    // The weight of position t, p = e*iv (float) times the V grid unit, is
-    // formed once: a += p*v with v = q*vunit, and p (24-bit mantissa) times
-    // q (at most 16 bits) is exact in double, so fma(p*vunit, q, a) rounds
-    // exactly as the add of the product does.  Past npos the weight is +0.0:
-    // a + 0*q is a (a is never -0), so every slot runs without a branch.
+    // --- weighted V (att_v): rounds of vC chunks, one chunk per vG waves, a
+    // lane per element of the head; each lane sums its element over the
+    // chunk's positions in position order, then the round's chunk sums join
+    // the running total in chunk order.
+    // The weight of position t, p = e*iv (float) times the V grid unit: a +=
+    // p*v with v = q*vunit, and p (24-bit mantissa) times q (at most 16 bits)
+    // is exact in double, so fma(p*vunit, q, a) rounds exactly as the add of
+    // the product does.  Lane u < kChunk forms the weight of the chunk's
+    // position u; the wave reads it through readlane.  Positions past npos
+    // have weight zero and are skipped (a + 0*q is a).
     const double vunit_d = KVB == 16 ? 1.0 / 2048.0 : 1.0 / 16.0;
-    for (int t = tid; t < nch * kChunk; t += kThreads)
-        ep[t] = t < npos ? (double)((float)ep[t] * iv) * vunit_d : 0.0;
-    __syncthreads();
-    for (int c0 = 0; c0 < nch; c0 += A.vR) {
-        const int nr = min(A.vR, nch - c0);
-        if (c0 > 0) {
-            // a later round: its rows through the same LDS slots
-            v_stage_load(A, vrs, c0, vreg);
-            v_stage_store(A, vstage, vreg, c0, npos, vown);
-            __syncthreads();
-        }
-        if (vr < nr) {
-            const int t0 = (c0 + vr) * kChunk;
-            double a[E];
+    for (int c0 = 0; c0 < nch; c0 += A.vC) {
+        const int nr = min(A.vC, nch - c0);
+        // the next round's V values load while this round is summed
+        const bool more = c0 + A.vC < nch;
+        int vnx[kChunk];
+        if (more) v_chunk_load<KVB>(A, vrs, slot < A.vC ? c0 + A.vC + slot : A.nchmax, vi, vnx);
+        if (slot < nr) {
+            const int c = c0 + slot;
+            const int tl = c * kChunk + (lane & (kChunk - 1));
+            const double w = tl < npos ? (double)((float)ep[tl] * iv) * vunit_d : 0.0;
+            // the last position of a launch that appends is pos: its V comes
+            // from the LDS copy (its cache row is being written)
+            const bool ownc = own_row && c == nch - 1;
+            const int n = min(kChunk, npos - c * kChunk);  // positions of the chunk below npos
+            const int nh = __builtin_amdgcn_readfirstlane(ownc ? n - 1 : n);
+            double a = 0.0;
 #pragma unroll
-            for (int e = 0; e < E; ++e) a[e] = 0.0;
-            const double2* w2 = reinterpret_cast<const double2*>(ep + t0);
-#pragma unroll
-            for (int k = 0; k < kChunk / 2; ++k) {
-                const double2 w = w2[k];
-                const unsigned v0 = vstage[(2 * k) * kThreads + tid], v1 = vstage[(2 * k + 1) * kThreads + tid];
-#pragma unroll
-                for (int e = 0; e < E; ++e) a[e] = fma(w.x, (double)v_field<KVB>(v0, e), a[e]);
-#pragma unroll
-                for (int e = 0; e < E; ++e) a[e] = fma(w.y, (double)v_field<KVB>(v1, e), a[e]);
-            }
-#pragma unroll
-            for (int e = 0; e < E; ++e) vpart[vr * hd + vw * E + e] = a[e];
+            for (int u = 0; u < kChunk; ++u)
+                if (u < nh) a = fma(readlane_d(w, u), (double)vch[u], a);
+            if (ownc) a = fma(readlane_d(w, n - 1), (double)kv_get<KVB>(vpk, vi), a);
+            if (ve < hd) vpart[slot * hd + ve] = a;
         }
         __syncthreads();
         const bool last = c0 + nr >= nch;
@@ -565,7 +540,7 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
             for (int r0 = 0; r0 < nr; r0 += 8) {
                 double pv[8];
 #pragma unroll
-                for (int k = 0; k < 8; ++k) pv[k] = vpart[min(r0 + k, A.vR - 1) * hd + i];
+                for (int k = 0; k < 8; ++k) pv[k] = vpart[min(r0 + k, A.vC - 1) * hd + i];
 #pragma unroll
                 for (int k = 0; k < 8; ++k) s += r0 + k < nr ? pv[k] : 0.0;
             }
@@ -573,6 +548,10 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
             else acc[i] = s;
         }
         if (!last) __syncthreads();
+        if (more) {
+#pragma unroll
+            for (int u = 0; u < kChunk; ++u) vch[u] = vnx[u];
+        }
     }
 }
 
@@ -585,8 +564,8 @@ size_t attn_layout(AttnDev& A) {
     A.lpp = 1;
     while (A.lpp * kp < nv) A.lpp *= 2;
     A.nchmax = (A.seq + kChunk - 1) / kChunk;
-    A.vW = hd / E;
-    A.vR = kThreads / A.vW;
+    A.vG = (hd + 63) / 64;
+    A.vC = (kThreads / 64) / A.vG;
     size_t off = 0;
     auto take = [&](size_t bytes) {
         const size_t o = off;
@@ -601,9 +580,8 @@ size_t attn_layout(AttnDev& A) {
     A.o_sc = take(2 * (size_t)A.seq);
     A.o_ep = take(8 * (size_t)A.nchmax * kChunk);
     A.o_csum = take(8 * (size_t)A.nchmax);
-    A.o_vpart = take(8 * (size_t)A.vR * hd);
+    A.o_vpart = take(8 * (size_t)A.vC * hd);
     A.o_acc = take(8 * (size_t)hd);
-    A.o_vst = take(4 * (size_t)kChunk * kThreads);
     return off;
 }
 
