@@ -262,9 +262,19 @@ int vgx_attn_decode_batch(vgx_attn* a, int layer, int pos0, int ntok, const int1
  *   the cache; the host cannot check it).
  * vgx_decode_advance: hist[*pos + 1] = *token (when inside hist_len), then
  *   ++*pos; one thread, so a replayed step leaves the next one's position
- *   and the token history in place. */
+ *   and the token history in place.
+ * vgx_logits_argmax_step: vgx_logits_argmax_rms, then in the same reduction
+ *   launch the step's tail: the advance above with the chosen token, and
+ *   that token's q8 embedding row (vgx_embed_q8: emb, emb_scale, vocab, dim)
+ *   into x_next, the next step's input (it may be x: the head's launch has
+ *   read x before the reduction launch starts).  Two launches
+ *   fewer per step than vgx_logits_argmax_rms + vgx_decode_advance +
+ *   vgx_embed_q8, with the same results. */
 int vgx_attn_block_at(vgx_attn* a, int layer, const int* pos_dev, const int16_t* qkv, int16_t* out);
 int vgx_decode_advance(vgx_ctx* ctx, int* pos, const int* token, int* hist, int hist_len);
+int vgx_logits_argmax_step(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, const int16_t* rms_w, float eps,
+                           int16_t* logits, int* token, int* pos, int* hist, int hist_len, const int8_t* emb,
+                           const float* emb_scale, int vocab, int dim, int16_t* x_next);
 
 /* ---- several sequences in lockstep (batched greedy decode).  No counterpart
  * in the reference, which decodes one sequence; each sequence's results are

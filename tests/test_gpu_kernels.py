@@ -274,6 +274,44 @@ def test_logits_argmax_rms(gpu, tile):
     assert int(host(token)[0]) == 0
 
 
+def test_logits_argmax_step_matches_separate_launches(gpu):
+    # the decode step's tail in the argmax reduction launch: the same token,
+    # history, position and next embedding as logits_argmax_rms followed by
+    # decode_advance and embed_q8; the next input may be the head's own input
+    rng = np.random.default_rng(83)
+    vocab, dim = 3000, 256
+    wh = rng.standard_normal((vocab, dim)).astype(np.float32) * 0.05
+    tiles = []
+    for st in range(0, vocab, mmcf.LOGITS_GRID):
+        q, unit, plane = mmcf.q8_per_row(wh[st:st + mmcf.LOGITS_GRID])
+        tiles.append(mmcf.Matrix("q8", q.shape[0], dim, (q.view(np.uint8) ^ 0x80).ravel(), unit, True, plane))
+    g = gpu.group([gpu.upload(t) for t in tiles])
+    emb = torch.from_numpy(rng.integers(-128, 128, size=(vocab, dim), dtype=np.int8)).cuda()
+    emb_scale = torch.from_numpy(rng.uniform(0.001, 0.05, vocab).astype(np.float32)).cuda()
+    hist_len = 16
+    for k, p in enumerate((0, 5, hist_len - 2, hist_len - 1)):
+        print("argmax step case", k, "pos", p, flush=True)
+        x, w = _rms_case(rng, dim, 200 * (k + 1))
+        logits = torch.empty(vocab, dtype=torch.int16, device="cuda")
+        token = torch.empty(1, dtype=torch.int32, device="cuda")
+        g.logits_argmax_rms(dev(x), dev(w), 1e-5, logits, token)
+        pos_a = torch.tensor([p], dtype=torch.int32, device="cuda")
+        hist_a = torch.arange(hist_len, dtype=torch.int32, device="cuda")
+        gpu.decode_advance(pos_a, token, hist_a)
+        x_a = gpu.embed_q8(emb, emb_scale, token)
+        xb = dev(x)
+        logits_b = torch.empty(vocab, dtype=torch.int16, device="cuda")
+        token_b = torch.empty(1, dtype=torch.int32, device="cuda")
+        pos_b = torch.tensor([p], dtype=torch.int32, device="cuda")
+        hist_b = torch.arange(hist_len, dtype=torch.int32, device="cuda")
+        g.logits_argmax_step(xb, dev(w), 1e-5, logits_b, token_b, pos_b, hist_b, emb, emb_scale, xb)
+        assert np.array_equal(host(logits_b), host(logits))
+        assert int(host(token_b)[0]) == int(host(token)[0])
+        assert int(host(pos_b)[0]) == int(host(pos_a)[0]) == p + 1
+        assert np.array_equal(host(hist_b), host(hist_a))
+        assert np.array_equal(host(xb), host(x_a))
+
+
 def test_rms_entry_point_refusals(gpu):
     rng = np.random.default_rng(91)
     m = q8_matrix(rng, 64, 64)

@@ -451,7 +451,8 @@ int vgx_group_free(vgx_group* g) {
 int vgx_group_rows(const vgx_group* g) { return g ? g->rows : 0; }
 
 static int launch_group(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, const float* xf, void* y,
-                        const int16_t* rw = nullptr, float eps = 0.0f, int* argmax_out = nullptr) {
+                        const int16_t* rw = nullptr, float eps = 0.0f, int* argmax_out = nullptr,
+                        const StepTail* tail = nullptr) {
     if (!ctx || !g || !y || (!x && !xf)) return vgx_fail(VGX_EINVAL, "gemv_group: NULL argument");
     if (!aligned16(x ? (const void*)x : (const void*)xf))
         return vgx_fail(VGX_EINVAL, "gemv_group: x must be 16-byte aligned");
@@ -479,6 +480,7 @@ static int launch_group(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, cons
     L.argmax_key = g->keys;
     L.nkeys = g->nkeys;
     L.total_rows = g->rows;
+    if (tail) L.tail = *tail;
     return vgx_gemv_launch(L, ctx->stream);
 }
 
@@ -515,6 +517,18 @@ int vgx_logits_argmax_rms(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, co
     if (!token || !logits) return vgx_fail(VGX_EINVAL, "vgx_logits_argmax_rms: NULL output");
     if (!rms_w) return vgx_fail(VGX_EINVAL, "vgx_logits_argmax_rms: NULL RMSNorm weight");
     return launch_group(ctx, g, x, nullptr, logits, rms_w, eps, token);
+}
+
+int vgx_logits_argmax_step(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, const int16_t* rms_w, float eps,
+                           int16_t* logits, int* token, int* pos, int* hist, int hist_len, const int8_t* emb,
+                           const float* emb_scale, int vocab, int dim, int16_t* x_next) {
+    if (!token || !logits) return vgx_fail(VGX_EINVAL, "vgx_logits_argmax_step: NULL output");
+    if (!rms_w) return vgx_fail(VGX_EINVAL, "vgx_logits_argmax_step: NULL RMSNorm weight");
+    if (!pos || !hist || !emb || !emb_scale || !x_next)
+        return vgx_fail(VGX_EINVAL, "vgx_logits_argmax_step: NULL step argument");
+    if (hist_len <= 0 || vocab <= 0 || dim <= 0) return vgx_fail(VGX_EINVAL, "vgx_logits_argmax_step: empty shape");
+    const StepTail t{pos, hist, hist_len, emb, emb_scale, vocab, dim, x_next};
+    return launch_group(ctx, g, x, nullptr, logits, rms_w, eps, token, &t);
 }
 
 // ---------------------------------------------------------------------------

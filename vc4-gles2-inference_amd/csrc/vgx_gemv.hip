@@ -337,8 +337,10 @@ __device__ __forceinline__ void argmax_tail(const GemvLaunch& L, unsigned long l
 
 // The largest of n keys (the first maximum of the rows they cover), one
 // workgroup: its row index into *out.
-__global__ void __launch_bounds__(256) argmax_keys_kernel(const unsigned long long* keys, int n, int* out) {
+__global__ void __launch_bounds__(256) argmax_keys_kernel(const unsigned long long* keys, int n, int* out,
+                                                          const StepTail T) {
     __shared__ unsigned long long s_k[4];
+    __shared__ int s_tok;
     unsigned long long key = 0ull;
     for (int i = threadIdx.x; i < n; i += blockDim.x) key = keys[i] > key ? keys[i] : key;
     for (int o = 32; o >= 1; o >>= 1) {
@@ -349,7 +351,30 @@ __global__ void __launch_bounds__(256) argmax_keys_kernel(const unsigned long lo
     __syncthreads();
     if (threadIdx.x == 0) {
         for (int k = 1; k < 4; ++k) key = s_k[k] > key ? s_k[k] : key;
-        *out = (int)(0xFFFFFFFFu - (unsigned)(key & 0xFFFFFFFFull));
+        const int tok = (int)(0xFFFFFFFFu - (unsigned)(key & 0xFFFFFFFFull));
+        *out = tok;
+        if (T.pos) {
+            // the decode step's bookkeeping: the token joins the history at
+            // position *pos + 1, and the position advances
+            const int p = *T.pos;
+            if (p + 1 >= 0 && p + 1 < T.hist_len) T.hist[p + 1] = tok;
+            *T.pos = p + 1;
+            s_tok = tok;
+        }
+    }
+    if (!T.pos) return;
+    __syncthreads();
+    // the next step's input: the token's embedding row, as embed_q8_kernel
+    // forms it (Session::embedding, engine/src/session.cpp:362-365)
+    int tok = s_tok;
+    if (tok < 0) tok = 0;
+    if (tok >= T.vocab) tok = T.vocab - 1;
+    const float sc = T.emb_scale[tok];
+    for (int i = threadIdx.x; i < T.dim; i += blockDim.x) {
+        const float v = (float)T.emb[(size_t)tok * T.dim + i] * sc;
+        float r = __builtin_rintf(v * 256.0f);
+        r = fminf(fmaxf(r, -32768.0f), 32767.0f);
+        T.x[i] = (int16_t)r;
     }
 }
 
@@ -1033,7 +1058,7 @@ int vgx_gemv_launch(const GemvLaunch& L, hipStream_t s) {
     hipLaunchKernelGGL(fn, dim3(grid), dim3(kThreads), shm, s, L);
     VGX_LAUNCH_CHECK("gemv launch");
     if (epi == EPI_STORE_ARGMAX) {
-        hipLaunchKernelGGL(argmax_keys_kernel, dim3(1), dim3(256), 0, s, L.argmax_key, grid, L.argmax_out);
+        hipLaunchKernelGGL(argmax_keys_kernel, dim3(1), dim3(256), 0, s, L.argmax_key, grid, L.argmax_out, L.tail);
         VGX_LAUNCH_CHECK("argmax keys launch");
     }
     return VGX_OK;

@@ -93,6 +93,19 @@ enum GemvX { X_I16 = 0, X_F32 = 1, X_RMS = 2 };
 // the kernel arguments, so no workgroup waits on a descriptor load.
 constexpr int kInlineMats = 8;
 
+// The tail of a greedy decode step, run by the argmax reduction when pos is
+// set: hist[*pos + 1] = the token, ++*pos, and the token's q8 embedding row
+// into x (the next step's input).
+struct StepTail {
+    int* pos;
+    int* hist;
+    int hist_len;
+    const int8_t* emb;
+    const float* emb_scale;
+    int vocab, dim;
+    int16_t* x;
+};
+
 struct GemvLaunch {
     MatDev md[kInlineMats];  // descriptors by value (nmat <= kInlineMats)
     MatDev md3;           // W3 by value (EPI_GATE)
@@ -115,6 +128,7 @@ struct GemvLaunch {
     unsigned long long* argmax_key;  // EPI_STORE_ARGMAX: one key slot per workgroup (nkeys of them)
     int nkeys;
     int total_rows;       // EPI_STORE_ARGMAX: length of the output
+    StepTail tail;        // EPI_STORE_ARGMAX: the decode step's tail (pos nullptr: none)
 };
 
 int vgx_gemv_plan(int kind, int rows, int cols, int num_cu, int* lpr, int* ri, int* rows_per_block);

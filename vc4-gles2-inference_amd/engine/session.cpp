@@ -333,13 +333,16 @@ struct vgx_engine {
     // layer.
     // pos_dev: the position is read from device memory instead (the step a
     // graph replays; never position 0).
+    // step_tail (the replayed step): h already holds the token's embedding,
+    // and the argmax launch also advances *pos_dev, appends the token to the
+    // history and embeds it into h for the next replay.
     int forward(const int* token_dev, int pos, bool want_logits, int* next_dev, vgx_attn* A,
-                const int* pos_dev = nullptr) {
+                int* pos_dev = nullptr, bool step_tail = false) {
         int st;
         const int D = m.dim;
         const float eps = m.rms_eps;
         if (!pos_dev && pos == 0 && conv && (st = vgx_conv_reset(conv))) return st;  // a new sequence
-        if ((st = vgx_embed_q8(ctx, emb, emb_scale, m.vocab, D, token_dev, h))) return st;
+        if (!step_tail && (st = vgx_embed_q8(ctx, emb, emb_scale, m.vocab, D, token_dev, h))) return st;
         for (int l = 0; l < m.layers; ++l) {
             Layer& ly = L[l];
             if (is_conv(l)) {
@@ -360,6 +363,9 @@ struct vgx_engine {
             if (st) return st;
         }
         if (!want_logits) return VGX_OK;
+        if (step_tail)
+            return vgx_logits_argmax_step(ctx, head, h, rms_final, eps, logits, next_dev, pos_dev, toks, seq, emb,
+                                          emb_scale, m.vocab, D, h);
         return vgx_logits_argmax_rms(ctx, head, h, rms_final, eps, logits, next_dev);
     }
 
@@ -416,10 +422,12 @@ struct vgx_engine {
         return VGX_OK;
     }
 
-    // The decode step captured once: forward() on the token at tok_cur and the
-    // position at pos_dev, its argmax back into tok_cur, then
-    // toks[pos + 1] = tok_cur and ++pos.  Every argument is fixed, so one
-    // instantiation serves every token of every later generation.
+    // The decode step captured once: forward() on the token at tok_cur (its
+    // embedding already in h) and the position at pos_dev, its argmax back into
+    // tok_cur, toks[pos + 1] = tok_cur, ++pos and the new token's embedding
+    // into h, the last three in the argmax reduction's launch.  Every argument
+    // is fixed, so one instantiation serves every token of every later
+    // generation; the first replay needs h filled by the caller.
     int ensure_step_graph() {
         if (step_exec) return VGX_OK;
         int st;
@@ -427,8 +435,7 @@ struct vgx_engine {
         hipStream_t s = static_cast<hipStream_t>(vgx_ctx_stream(ctx));
         if (hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed) != hipSuccess)
             return fail(VGX_EHIP, "decode graph: begin capture");
-        st = forward(tok_cur, 0, true, tok_cur, attn, pos_dev);
-        if (!st) st = vgx_decode_advance(ctx, pos_dev, tok_cur, toks, seq);
+        st = forward(tok_cur, 0, true, tok_cur, attn, pos_dev, true);
         hipGraph_t g = nullptr;
         const hipError_t ec = hipStreamEndCapture(s, &g);
         if (st || ec != hipSuccess) {
@@ -685,6 +692,8 @@ int vgx_engine_generate_from(vgx_engine* e, const int* prompt, int n_prompt, int
         if (hipMemcpyAsync(e->tok_cur, gen, sizeof(int), hipMemcpyDeviceToDevice, s) != hipSuccess ||
             hipMemcpyAsync(e->pos_dev, &e->pos_host, sizeof(int), hipMemcpyHostToDevice, s) != hipSuccess)
             return fail(VGX_EHIP, "decode graph: state upload");
+        // the first replay's input; each replay embeds the next one's
+        if ((st = vgx_embed_q8(e->ctx, e->emb, e->emb_scale, e->m.vocab, e->m.dim, e->tok_cur, e->h))) return st;
         for (int i = 1; i < n_gen; ++i)
             if (hipGraphLaunch(e->step_exec, s) != hipSuccess) return fail(VGX_EHIP, "decode graph: launch");
     } else {

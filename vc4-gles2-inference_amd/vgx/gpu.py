@@ -85,6 +85,16 @@ class Group:
                                                   _ptr(logits), _ptr(token)))
         return logits, token
 
+    def logits_argmax_step(self, x, rms_w, eps, logits, token, pos, hist, emb, emb_scale, x_next):
+        """logits_argmax_rms, then in the reduction launch hist[pos + 1] =
+        token, ++pos and the token's q8 embedding row into x_next."""
+        vocab, dim = emb.shape
+        _l.check(_l.load().vgx_logits_argmax_step(self.gpu.ctx, self.h, _ptr(x), _ptr(rms_w), float(eps),
+                                                   _ptr(logits), _ptr(token), _ptr(pos), _ptr(hist),
+                                                   int(hist.numel()), _ptr(emb), _ptr(emb_scale), vocab, dim,
+                                                   _ptr(x_next)))
+        return logits, token
+
     def free(self):
         if self.h:
             _l.load().vgx_group_free(self.h)
@@ -365,6 +375,10 @@ class GPU:
         out = out if out is not None else torch.empty(w1.rows, dtype=torch.int16, device=x.device)
         _l.check(_l.load().vgx_ffn_gate_rms(self.ctx, w1.h, w3.h, _ptr(x), _ptr(rms_w), float(eps), hs, _ptr(out)))
         return out
+
+    def decode_advance(self, pos, token, hist):
+        """hist[pos + 1] = token (inside hist), then ++pos; device scalars."""
+        _l.check(_l.load().vgx_decode_advance(self.ctx, _ptr(pos), _ptr(token), _ptr(hist), int(hist.numel())))
 
     def embed_q8(self, emb, emb_scale, token, out=None):
         vocab, dim = emb.shape

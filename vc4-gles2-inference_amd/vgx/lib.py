@@ -96,6 +96,7 @@ _SIGS = {
     "vgx_attn_block_seqs": (_I, [_P, _I, _I, _I, _P, _P]),
     "vgx_attn_block_at": (_I, [_P, _I, _P, _P, _P]),
     "vgx_decode_advance": (_I, [_P, _P, _P, _P, _I]),
+    "vgx_logits_argmax_step": (_I, [_P, _P, _P, _P, ctypes.c_float, _P, _P, _P, _P, _I, _P, _P, _I, _I, _P]),
     "vgx_kv_row_bytes": (_I, [_P]),
     "vgx_kv_read_rows": (_I, [_P, _I, _I, _I, _P]),
     "vgx_kv_write_rows": (_I, [_P, _I, _I, _I, _P]),
