@@ -509,7 +509,7 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     // is exact in double, so fma(p*vunit, q, a) rounds exactly as the add of
     // the product does.  Lane u < kChunk forms the weight of the chunk's
     // position u; the wave reads it through readlane.  Positions past npos
-    // have weight zero and are skipped (a + 0*q is a).
+    // have weight zero (a + 0*q is a), so all 32 slots run without a branch.
     const double vunit_d = KVB == 16 ? 1.0 / 2048.0 : 1.0 / 16.0;
     for (int c0 = 0; c0 < nch; c0 += A.vC) {
         const int nr = min(A.vC, nch - c0);
@@ -523,14 +523,16 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
             const double w = tl < npos ? (double)((float)ep[tl] * iv) * vunit_d : 0.0;
             // the last position of a launch that appends is pos: its V comes
             // from the LDS copy (its cache row is being written)
-            const bool ownc = own_row && c == nch - 1;
-            const int n = min(kChunk, npos - c * kChunk);  // positions of the chunk below npos
-            const int nh = __builtin_amdgcn_readfirstlane(ownc ? n - 1 : n);
+            if (own_row && c == nch - 1) {
+                const int own = kv_get<KVB>(vpk, vi);
+                const int uo = npos - 1 - c * kChunk;
+#pragma unroll
+                for (int u = 0; u < kChunk; ++u) vch[u] = u == uo ? own : vch[u];
+            }
+            // every slot, without a branch: past npos the weight is zero
             double a = 0.0;
 #pragma unroll
-            for (int u = 0; u < kChunk; ++u)
-                if (u < nh) a = fma(readlane_d(w, u), (double)vch[u], a);
-            if (ownc) a = fma(readlane_d(w, n - 1), (double)kv_get<KVB>(vpk, vi), a);
+            for (int u = 0; u < kChunk; ++u) a = fma(readlane_d(w, u), (double)vch[u], a);
             if (ve < hd) vpart[slot * hd + ve] = a;
         }
         __syncthreads();
