@@ -115,6 +115,43 @@ def test_attention_rails(gpu, bits, hd):
     A.free()
 
 
+@pytest.mark.parametrize("bits,hd", [(8, 96), (16, 128), (8, 128), (16, 256), (8, 256)])
+def test_attention_long_contexts(gpu, bits, hd):
+    """Contexts of several rounds of the weighted-V pass (and, above head_dim
+    64, the two-elements-per-lane plan it switches to there), over random
+    cached rows, through both the appending and the reading entry points."""
+    heads, kvh, seq = 4, 2, 320
+    dim = heads * hd
+    rng = np.random.default_rng(bits * 7 + hd)
+    rc, rs = o.rope_cos_sin(10000.0, hd, seq)
+    rtab = o.rope_table(rc, rs)
+    qn = rng.uniform(0.5, 1.5, (1, hd)).astype(np.float32)
+    kn = rng.uniform(0.5, 1.5, (1, hd)).astype(np.float32)
+    A = gpu.attention(dim=dim, heads=heads, kv_heads=kvh, head_dim=hd, seq=seq, layers=1, kv_bits=bits,
+                      rope_half=1, qk_norm=1, rope_cos=rc, rope_sin=rs, q_norm=qn, k_norm=kn)
+    c = o.attn_cfg(dim, heads, kvh, hd, seq, bits, 1, 1)
+    qnq, knq = o.quantize_act(qn[0]), o.quantize_act(kn[0])
+    rb = o.kv_row_bytes(c)
+    n = seq - 1
+    if bits == 16:  # the texel layout: big-endian int16, values within the q16 KV grid's usual range
+        rows = rng.integers(-6000, 6000, size=(n, rb // 2)).astype(">i2").view(np.uint8).reshape(-1)
+    else:
+        rows = rng.integers(-128, 128, size=(n, rb)).astype(np.int8).view(np.uint8).reshape(-1)
+    for pos in (32, 129, 200, 257, n):
+        print("long context bits=%d hd=%d pos=%d" % (bits, hd, pos), flush=True)
+        kv = np.zeros(seq * rb, np.uint8)
+        kv[:pos * rb] = rows[:pos * rb]
+        A.write_rows(0, 0, rows[:pos * rb].copy())
+        qkv = np.clip(rng.standard_normal(dim + 2 * kvh * hd) * 600, -32768, 32767).astype(np.int16)
+        want = o.attn_block(c, qkv, qnq, knq, rtab, pos, kv)
+        got = A.block(0, pos, dev(qkv))
+        torch.cuda.synchronize()
+        assert np.array_equal(got.cpu().numpy(), want), pos
+        # the reading entry point, over the row the append wrote, agrees
+        assert np.array_equal(A.decode(0, pos, dev(qkv)).cpu().numpy(), want), pos
+    A.free()
+
+
 @pytest.mark.parametrize("bits", [16, 8])
 def test_attention_sequences_in_lockstep(gpu, bits):
     """vgx_attn_block_seqs: nseq sequences at the same position, each on its

@@ -40,8 +40,10 @@ struct AttnDev {
     int dim, heads, kv_heads, hd, seq, kv_bits, rope_half, qk_norm, group;
     int row_bytes;
     int lpp;     // lanes per scored position (a power of two)
-    int vG;      // waves per chunk of the weighted-V pass (64 elements each)
-    int vC;      // chunks per round of the weighted-V pass
+    // the weighted-V lane plan with one element per lane (vG1 waves per chunk,
+    // vC1 chunks per round) and with two (vG2, vC2; taken above head_dim 64
+    // when the context needs more than one round of the first)
+    int vG1, vC1, vG2, vC2;
     int nchmax;  // chunks of a full cache
     // LDS byte offsets
     int o_wmax, o_vpk, o_kpk, o_qhw, o_qlw, o_sc, o_ep, o_csum, o_vpart, o_acc;
@@ -167,20 +169,35 @@ __device__ __forceinline__ void dot_vec(const int4 a, const int4 b, int ones, co
     }
 }
 
-// The V values of one chunk for one lane's element vi: position c*kChunk + u
-// in vch[u].  vrs covers rows 0..npos-1: a row at or past npos reads nothing
-// and gives zero (its weight is zero too).  An idle wave passes a chunk past
-// the cache.
+// The V values of one chunk for one lane's elements vi (and vi+1 when vE is
+// 2), as stored (16- or 8-bit fields, the first element low): position
+// c*kChunk + u in vch[u].  vrs covers rows 0..npos-1: a row at or past npos
+// reads nothing and gives zero (its weight is zero too).  An idle wave
+// passes a chunk past the cache.
 template <int KVB>
-__device__ __forceinline__ void v_chunk_load(const AttnDev& A, __amdgpu_buffer_rsrc_t vrs, int c, int vi,
+__device__ __forceinline__ void v_chunk_load(const AttnDev& A, __amdgpu_buffer_rsrc_t vrs, int vE, int c, int vi,
                                              int (&vch)[kChunk]) {
+    if (vE == 2) {
 #pragma unroll
-    for (int u = 0; u < kChunk; ++u) {
-        const int off = min(c * kChunk + u, A.seq) * A.row_bytes + vi * (KVB / 8);
-        if (KVB == 16) vch[u] = (int)(int16_t)__builtin_amdgcn_raw_buffer_load_b16(vrs, off, 0, 0);
-        else vch[u] = (int)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(vrs, off, 0, 0);
+        for (int u = 0; u < kChunk; ++u) {
+            const int off = min(c * kChunk + u, A.seq) * A.row_bytes + vi * (KVB / 8);
+            if (KVB == 16) vch[u] = (int)__builtin_amdgcn_raw_buffer_load_b32(vrs, off, 0, 0);
+            else vch[u] = (int)__builtin_amdgcn_raw_buffer_load_b16(vrs, off, 0, 0);
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < kChunk; ++u) {
+            const int off = min(c * kChunk + u, A.seq) * A.row_bytes + vi * (KVB / 8);
+            if (KVB == 16) vch[u] = (int)__builtin_amdgcn_raw_buffer_load_b16(vrs, off, 0, 0);
+            else vch[u] = (int)__builtin_amdgcn_raw_buffer_load_b8(vrs, off, 0, 0);
+        }
     }
 }
+// The first and second element of a loaded V field.
+template <int KVB>
+__device__ __forceinline__ int v_lo(int p) { return KVB == 16 ? (int)(int16_t)(p & 0xffff) : (int)(int8_t)(p & 0xff); }
+template <int KVB>
+__device__ __forceinline__ int v_hi(int p) { return KVB == 16 ? (p >> 16) : (int)(int8_t)((p >> 8) & 0xff); }
 
 // Lane exchanges within rows of 16 lanes (DPP): quad_perm [1,0,3,2], quad_perm
 // [2,3,0,1], row_half_mirror, row_mirror.  After the four steps of a
@@ -231,7 +248,8 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     asm volatile("" ::"s"(kv), "s"(rtab), "s"(qn), "s"(kn), "s"(qkv), "s"(out), "s"(pos0), "s"(do_write),
                  "s"(do_attend), "s"(seq_stride), "s"(pos_step), "s"(pos_ptr));
     asm volatile("" ::"s"(A.dim), "s"(A.kv_heads), "s"(A.hd), "s"(A.seq), "s"(A.rope_half), "s"(A.qk_norm),
-                 "s"(A.group), "s"(A.row_bytes), "s"(A.lpp), "s"(A.vG), "s"(A.vC), "s"(A.nchmax), "s"(A.o_wmax),
+                 "s"(A.group), "s"(A.row_bytes), "s"(A.lpp), "s"(A.vG1), "s"(A.vC1), "s"(A.vG2), "s"(A.vC2),
+                 "s"(A.nchmax), "s"(A.o_wmax),
                  "s"(A.o_vpk), "s"(A.o_kpk), "s"(A.o_qhw), "s"(A.o_qlw), "s"(A.o_sc), "s"(A.o_ep), "s"(A.o_csum),
                  "s"(A.o_vpart), "s"(A.o_acc));
     constexpr int E = KVB == 16 ? 2 : 4;  // values per 32-bit word
@@ -310,12 +328,14 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     const int nv = hd * KVB / 128;  // 16-byte vectors per K row slice
     const int lpp = A.lpp, sj = tid & (lpp - 1), P = kThreads / lpp;
     // weighted-V lanes: wave w takes chunk slot w / vG of each round and the
-    // elements 64*(w % vG) + lane of the head
+    // elements vE*(64*(w % vG) + lane) .. +vE-1 of the head
     // (slot is wave-uniform; readfirstlane lets the compiler see it)
-    const int slot = __builtin_amdgcn_readfirstlane(wave / A.vG);
-    const int ve = (wave - slot * A.vG) * 64 + lane, vi = min(ve, hd - 1);
+    const bool wide = A.vC2 > A.vC1 && nch > A.vC1;
+    const int vE = wide ? 2 : 1, vG = wide ? A.vG2 : A.vG1, vC = wide ? A.vC2 : A.vC1;
+    const int slot = __builtin_amdgcn_readfirstlane(wave / vG);
+    const int ve = ((wave - slot * vG) * 64 + lane) * vE, vi = min(ve, hd - vE);
     uint4 kreg[KP];
-    int vch[kChunk];  // V of element vi at the chunk's positions
+    int vch[kChunk];  // V of elements vi.. at the chunk's positions, as stored
     // rows 0..npos-1 of this head's K and V slices
     const __amdgpu_buffer_rsrc_t krs = rows_rsrc(khead, npos * A.row_bytes);
     const __amdgpu_buffer_rsrc_t vrs = rows_rsrc(vhead, npos * A.row_bytes);
@@ -329,7 +349,7 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     }
     // the K loads first: the scores wait for them, not for the V loads after
     asm volatile("" ::: "memory");
-    v_chunk_load<KVB>(A, vrs, slot < A.vC ? slot : A.nchmax, vi, vch);
+    v_chunk_load<KVB>(A, vrs, vE, slot < vC ? slot : A.nchmax, vi, vch);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         keep(ke[c]);
@@ -501,9 +521,9 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     }
 
     // --- weighted V (att_v): rounds of vC chunks, one chunk per vG waves, a
-    // lane per element of the head; each lane sums its element over the
-    // chunk's positions in position order, then the round's chunk sums join
-    // the running total in chunk order.
+    // lane per element (two above head_dim 64) of the head; each lane sums
+    // its elements over the chunk's positions in position order, then the
+    // round's chunk sums join the running total in chunk order.
     // The weight of position t, p = e*iv (float) times the V grid unit: a +=
     // p*v with v = q*vunit, and p (24-bit mantissa) times q (at most 16 bits)
     // is exact in double, so fma(p*vunit, q, a) rounds exactly as the add of
@@ -511,12 +531,12 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     // position u; the wave reads it through readlane.  Positions past npos
     // have weight zero (a + 0*q is a), so all 32 slots run without a branch.
     const double vunit_d = KVB == 16 ? 1.0 / 2048.0 : 1.0 / 16.0;
-    for (int c0 = 0; c0 < nch; c0 += A.vC) {
-        const int nr = min(A.vC, nch - c0);
+    for (int c0 = 0; c0 < nch; c0 += vC) {
+        const int nr = min(vC, nch - c0);
         // the next round's V values load while this round is summed
-        const bool more = c0 + A.vC < nch;
+        const bool more = c0 + vC < nch;
         int vnx[kChunk];
-        if (more) v_chunk_load<KVB>(A, vrs, slot < A.vC ? c0 + A.vC + slot : A.nchmax, vi, vnx);
+        if (more) v_chunk_load<KVB>(A, vrs, vE, slot < vC ? c0 + vC + slot : A.nchmax, vi, vnx);
         if (slot < nr) {
             const int c = c0 + slot;
             const int tl = c * kChunk + (lane & (kChunk - 1));
@@ -524,16 +544,31 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
             // the last position of a launch that appends is pos: its V comes
             // from the LDS copy (its cache row is being written)
             if (own_row && c == nch - 1) {
-                const int own = kv_get<KVB>(vpk, vi);
+                const int own = vE == 2 ? (KVB == 16 ? (int)*reinterpret_cast<const uint32_t*>(vpk + vi * 2)
+                                                       : (int)*reinterpret_cast<const uint16_t*>(vpk + vi))
+                                          : (KVB == 16 ? (int)*reinterpret_cast<const uint16_t*>(vpk + vi * 2)
+                                                       : (int)vpk[vi]);
                 const int uo = npos - 1 - c * kChunk;
 #pragma unroll
                 for (int u = 0; u < kChunk; ++u) vch[u] = u == uo ? own : vch[u];
             }
             // every slot, without a branch: past npos the weight is zero
-            double a = 0.0;
+            double a = 0.0, b = 0.0;
+            if (vE == 2) {
 #pragma unroll
-            for (int u = 0; u < kChunk; ++u) a = fma(readlane_d(w, u), (double)vch[u], a);
-            if (ve < hd) vpart[slot * hd + ve] = a;
+                for (int u = 0; u < kChunk; ++u) {
+                    const double wu = readlane_d(w, u);
+                    a = fma(wu, (double)v_lo<KVB>(vch[u]), a);
+                    b = fma(wu, (double)v_hi<KVB>(vch[u]), b);
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < kChunk; ++u) a = fma(readlane_d(w, u), (double)v_lo<KVB>(vch[u]), a);
+            }
+            if (ve < hd) {
+                vpart[slot * hd + ve] = a;
+                if (vE == 2) vpart[slot * hd + ve + 1] = b;
+            }
         }
         __syncthreads();
         const bool last = c0 + nr >= nch;
@@ -542,7 +577,7 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
             for (int r0 = 0; r0 < nr; r0 += 8) {
                 double pv[8];
 #pragma unroll
-                for (int k = 0; k < 8; ++k) pv[k] = vpart[min(r0 + k, A.vC - 1) * hd + i];
+                for (int k = 0; k < 8; ++k) pv[k] = vpart[min(r0 + k, vC - 1) * hd + i];
 #pragma unroll
                 for (int k = 0; k < 8; ++k) s += r0 + k < nr ? pv[k] : 0.0;
             }
@@ -566,8 +601,10 @@ size_t attn_layout(AttnDev& A) {
     A.lpp = 1;
     while (A.lpp * kp < nv) A.lpp *= 2;
     A.nchmax = (A.seq + kChunk - 1) / kChunk;
-    A.vG = (hd + 63) / 64;
-    A.vC = (kThreads / 64) / A.vG;
+    A.vG1 = (hd + 63) / 64;
+    A.vC1 = (kThreads / 64) / A.vG1;
+    A.vG2 = hd > 64 ? (hd + 127) / 128 : A.vG1;
+    A.vC2 = (kThreads / 64) / A.vG2;
     size_t off = 0;
     auto take = [&](size_t bytes) {
         const size_t o = off;
@@ -582,7 +619,7 @@ size_t attn_layout(AttnDev& A) {
     A.o_sc = take(2 * (size_t)A.seq);
     A.o_ep = take(8 * (size_t)A.nchmax * kChunk);
     A.o_csum = take(8 * (size_t)A.nchmax);
-    A.o_vpart = take(8 * (size_t)A.vC * hd);
+    A.o_vpart = take(8 * (size_t)(A.vC1 > A.vC2 ? A.vC1 : A.vC2) * hd);
     A.o_acc = take(8 * (size_t)hd);
     return off;
 }
