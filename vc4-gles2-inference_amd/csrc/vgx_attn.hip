@@ -7,8 +7,10 @@
 // appends, the first query head of each KV head's group packs this position's
 // K (qk-norm, RoPE) and V into the layer's KV row, and every head of the group
 // rebuilds the same packed values in LDS for its own position.  Scores and
-// exponentials run one position per thread; the K row of a position is read
-// as 16-byte vectors.  The two double-precision sums (sum of
+// exponentials run one position per thread (or per lpp lanes); the K row of a
+// position is read as 16-byte vectors.  The weighted V sum runs a wave per
+// chunk of positions and a lane per element (or two), with the V values read
+// straight into registers.  The two double-precision sums (sum of
 // exp, sum over t of p*v) use a fixed order -- chunks of kChunk positions,
 // each summed in position order, then the chunk sums in chunk order -- and the
 // oracle sums in the same order, so the output is reproducible bit for bit.
