@@ -10,7 +10,11 @@ with the GPU kernels' numerics (oracle.py); FModel.step follows
 engine/tools/ref_forward.py:47-115 on the dequantised container weights (CFModel
 runs the same forward through the C/OpenMP float path, oracle/vgx_float.c), with
 the engine's conventions (block RMSNorm eps from key 11 or 1e-5, q/k RMSNorm
-eps 1e-6, RoPE tables of Session, engine/src/session.cpp:188-202).
+eps 1e-6, RoPE tables of Session, engine/src/session.cpp:188-202).  With the
+reference tools' conventions (qk_eps=None, tied_head=True) FModel reproduces
+engine/tools/ref_generate.py, ref_forward.py and mmcf_hf.py
+residual_peaks_lfm2 within fp32 summation order on vectors those tools wrote
+(tests/test_float_pin.py, tests/golden/make_float_vectors.py).
 """
 import ctypes
 import os
@@ -216,10 +220,19 @@ class QModel(_Base):
 
 
 class FModel(_Base):
-    """The float CPU path on the dequantised container weights."""
+    """The float CPU path on the dequantised container weights.
 
-    def __init__(self, blob, seq=None):
+    qk_eps: the q/k RMSNorm eps.  The engine uses 1e-6
+    (engine/src/shaders_attn.cpp:259-268); the reference's float tools use the
+    block eps for both (engine/tools/ref_forward.py:75-78,
+    engine/tools/ref_generate.py:88-90), which qk_eps=None selects.
+    tied_head: the LM head is the float embedding itself (emb * es), as those
+    tools compute logits (`x @ emb.T`, ref_forward.py:113); the default is the
+    container's q8 head tiles, which is what the engine multiplies by."""
+
+    def __init__(self, blob, seq=None, qk_eps=1e-6, tied_head=False):
         super().__init__(blob, seq)
+        self.qk_eps = self.eps if qk_eps is None else qk_eps
         # key 15's 2^k on w2 only undoes the hidden's q16 store scale, which
         # the float path does not apply
         self.W = []
@@ -228,7 +241,10 @@ class FModel(_Base):
             L = dict(L, w2=_Mat(w2.kind, w2.rows, w2.cols, w2.body, w2.scale, w2.prebiased, w2.plane,
                                 w2.s16, w2.m16, 1.0))
             self.W.append({k: m.dequant() for k, m in L.items()})
-        self.head = np.concatenate([t.dequant() for t in self.tiles])
+        if tied_head:
+            self.head = self.emb.astype(np.float32) * self.es[:, None]
+        else:
+            self.head = np.concatenate([t.dequant() for t in self.tiles])
         self.kc = np.zeros((self.layers, self.seq, self.kv_heads, self.hd), np.float32)
         self.vc = np.zeros_like(self.kc)
         self.cstate = np.zeros((self.layers, 2, self.dim), np.float32)  # B*x of pos-2, pos-1
@@ -242,6 +258,11 @@ class FModel(_Base):
         out[..., 0::2] = x[..., 0::2] * c - x[..., 1::2] * s
         out[..., 1::2] = x[..., 1::2] * c + x[..., 0::2] * s
         return out
+
+    def _per_q_head(self, kv):
+        """[t, kv_heads, hd] -> [t, heads, hd]: query head h reads KV head
+        h // (heads / kv_heads) (GQA, ref_forward.py:85-86)."""
+        return np.repeat(kv, self.heads // self.kv_heads, axis=1)
 
     @staticmethod
     def _rms(x, w, eps):
@@ -261,7 +282,9 @@ class FModel(_Base):
         st[0], st[1] = st[1], bx
         return W["conv_out"] @ (c * cv)
 
-    def step(self, token, pos):
+    def step(self, token, pos, trace=None):
+        """Logits of position pos; trace (a list, optional) receives the
+        residual after each layer."""
         if pos == 0:
             self.cstate[:] = 0
         x = self.emb[token].astype(np.float32) * self.es[token]
@@ -272,19 +295,19 @@ class FModel(_Base):
                 xn = self._rms(x, self.rms_ffn[l], self.eps)
                 g, u = W["w1"] @ xn, W["w3"] @ xn
                 x = x + W["w2"] @ ((g / (1 + np.exp(-g))) * u)
+                if trace is not None:
+                    trace.append(x.copy())
                 continue
             qkv = W["qkv"] @ xn
             q = qkv[:self.dim].reshape(self.heads, self.hd)
             k = qkv[self.dim:self.dim + self.kv_dim].reshape(self.kv_heads, self.hd)
             v = qkv[self.dim + self.kv_dim:].reshape(self.kv_heads, self.hd)
             if self.qk_norm:
-                q = self._rms(q, self.qn[l], 1e-6)
-                k = self._rms(k, self.kn[l], 1e-6)
+                q = self._rms(q, self.qn[l], self.qk_eps)
+                k = self._rms(k, self.kn[l], self.qk_eps)
             q, k = self._rope(q, pos), self._rope(k, pos)
             self.kc[l, pos], self.vc[l, pos] = k, v
-            rep = self.heads // self.kv_heads
-            K = np.repeat(self.kc[l, :pos + 1], rep, axis=1)
-            V = np.repeat(self.vc[l, :pos + 1], rep, axis=1)
+            K, V = self._per_q_head(self.kc[l, :pos + 1]), self._per_q_head(self.vc[l, :pos + 1])
             sc = np.einsum("hd,thd->ht", q, K) / np.sqrt(self.hd)
             p = np.exp(sc - sc.max(axis=1, keepdims=True))
             p /= p.sum(axis=1, keepdims=True)
@@ -293,6 +316,8 @@ class FModel(_Base):
             xn = self._rms(x, self.rms_ffn[l], self.eps)
             g, u = W["w1"] @ xn, W["w3"] @ xn
             x = x + W["w2"] @ ((g / (1 + np.exp(-g))) * u)
+            if trace is not None:
+                trace.append(x.copy())
         return self.head @ self._rms(x, self.rms_final, self.eps)
 
 
