@@ -129,6 +129,12 @@ int vgx_group_free(vgx_group* g);
 int vgx_group_rows(const vgx_group* g);
 int vgx_gemv_group(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, int16_t* y);
 int vgx_gemv_group_f32(vgx_ctx* ctx, const vgx_group* g, const float* x, float* y);
+/* The launch plan a GEMV over W (or over the group g, which is one launch)
+ * takes: lanes of a wave that share a row, and rows each lane owns.  No
+ * counterpart in the reference, whose draw geometry is fixed by the shader;
+ * it lets a caller check which kernel variant a shape runs on. */
+int vgx_gemv_plan_info(vgx_ctx* ctx, const vgx_mat* W, int* lanes_per_row, int* rows_per_lane);
+int vgx_group_plan_info(const vgx_group* g, int* lanes_per_row, int* rows_per_lane);
 /* The logits pass followed by argmax_token's first-maximum rule
  * (engine/src/sampling.cpp:160-162): `token` (device int) receives the
  * index into the concatenated rows; `logits` (device, may be NULL) the q16 rows. */

@@ -115,12 +115,20 @@ def test_attention_rails(gpu, bits, hd):
     A.free()
 
 
-@pytest.mark.parametrize("bits,hd", [(8, 96), (16, 128), (8, 128), (16, 256), (8, 256)])
-def test_attention_long_contexts(gpu, bits, hd):
+LONG = [(8, 96, 4, 2, 320, (32, 129, 200, 257, 319)), (16, 128, 4, 2, 320, (32, 129, 200, 257, 319)),
+        (8, 128, 4, 2, 320, (32, 129, 200, 257, 319)), (16, 256, 4, 2, 320, (32, 129, 200, 257, 319)),
+        (8, 256, 4, 2, 320, (32, 129, 200, 257, 319)),
+        # MiniMind3 q4 / KV q8 at SEQ 768: 8 Q / 4 KV heads of 96, to the last row
+        (8, 96, 8, 4, 768, (383, 511, 640, 767)),
+        # MiniMind3 q8 / KV q16 at SEQ 768
+        (16, 96, 8, 4, 768, (300, 767))]
+
+
+@pytest.mark.parametrize("bits,hd,heads,kvh,seq,positions", LONG)
+def test_attention_long_contexts(gpu, bits, hd, heads, kvh, seq, positions):
     """Contexts of several rounds of the weighted-V pass (and, above head_dim
     64, the two-elements-per-lane plan it switches to there), over random
     cached rows, through both the appending and the reading entry points."""
-    heads, kvh, seq = 4, 2, 320
     dim = heads * hd
     rng = np.random.default_rng(bits * 7 + hd)
     rc, rs = o.rope_cos_sin(10000.0, hd, seq)
@@ -137,7 +145,7 @@ def test_attention_long_contexts(gpu, bits, hd):
         rows = rng.integers(-6000, 6000, size=(n, rb // 2)).astype(">i2").view(np.uint8).reshape(-1)
     else:
         rows = rng.integers(-128, 128, size=(n, rb)).astype(np.int8).view(np.uint8).reshape(-1)
-    for pos in (32, 129, 200, 257, n):
+    for pos in positions:
         print("long context bits=%d hd=%d pos=%d" % (bits, hd, pos), flush=True)
         kv = np.zeros(seq * rb, np.uint8)
         kv[:pos * rb] = rows[:pos * rb]

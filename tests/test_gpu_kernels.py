@@ -381,3 +381,40 @@ def test_mat_concat_gemm_and_argmax_rows(gpu, kind):
         cat2 = gpu.concat([mats[0], odd])
         want = np.concatenate([o.store(oracle_rowval(tiles[0], X[0])), o.store(oracle_rowval(odd_t, X[0]))])
         assert np.array_equal(host(gpu.gemm(cat2, dev(X[:1])))[0], want)
+
+
+# The bandwidth-bound plans: a launch of >= 16 waves per CU takes 4 rows per
+# lane, with 16 (q8, K <= 1024) or 8 (q8, K > 1024) lanes a row, and 8 (q4,
+# up to 48 groups) or 16 (q4, more) -- the kernels the cold GEMV sweep times.
+# Each case is a group of equal-shape copies (one launch) and, where one matrix
+# is large enough by itself, a single-matrix launch; both the q16 and the f32
+# entry points, bit-exact against the oracle.
+BIG = [("q8", 768, 768, 24, (16, 4)), ("q8", 768, 2432, 8, (8, 4)),
+       ("q4", 768, 768, 48, (8, 4)), ("q4", 768, 2432, 11, (16, 4))]
+
+
+@pytest.mark.parametrize("kind,rows,cols,copies,plan", BIG)
+def test_gemv_bandwidth_plans(gpu, kind, rows, cols, copies, plan):
+    rng = np.random.default_rng(rows + cols + copies)
+    mats = [(q8_matrix if kind == "q8" else q4_matrix)(rng, rows, cols) for _ in range(copies)]
+    Ws = [gpu.upload(m) for m in mats]
+    G = gpu.group(Ws)
+    assert G.plan() == plan
+    for full in (False, True):
+        x = rand_x(rng, cols, full)
+        v = np.concatenate([oracle_rowval(m, x) for m in mats])
+        assert np.array_equal(host(G.gemv(dev(x))), o.store(v)), full
+    xf = rng.standard_normal(cols).astype(np.float32)
+    v = np.concatenate([oracle_rowval(m, o.quantize_act(xf)) for m in mats])
+    assert np.array_equal(host(G.gemv_f32(dev(xf))), o.store_f32(v))
+    G.free()
+    # as many rows in one matrix: a single-matrix launch of the same plan
+    one = (q8_matrix if kind == "q8" else q4_matrix)(rng, rows * copies, cols)
+    W1 = gpu.upload(one)
+    assert gpu.plan(W1) == plan
+    x = rand_x(rng, cols, True)
+    res = rand_x(rng, one.rows)
+    v = oracle_rowval(one, x)
+    assert np.array_equal(host(gpu.matvec(W1, dev(x), dev(res))), o.store(v, res))
+    v = oracle_rowval(one, o.quantize_act(xf))
+    assert np.array_equal(host(gpu.matvec_f32(W1, dev(xf))), o.store_f32(v))

@@ -450,6 +450,22 @@ int vgx_group_free(vgx_group* g) {
 
 int vgx_group_rows(const vgx_group* g) { return g ? g->rows : 0; }
 
+int vgx_gemv_plan_info(vgx_ctx* ctx, const vgx_mat* W, int* lanes_per_row, int* rows_per_lane) {
+    if (!ctx || !W) return vgx_fail(VGX_EINVAL, "vgx_gemv_plan_info: NULL argument");
+    int lpr, ri, rpb;
+    vgx_gemv_plan(W->d.kind, W->d.rows, W->d.cols, ctx->num_cu, &lpr, &ri, &rpb);
+    if (lanes_per_row) *lanes_per_row = lpr;
+    if (rows_per_lane) *rows_per_lane = ri;
+    return VGX_OK;
+}
+
+int vgx_group_plan_info(const vgx_group* g, int* lanes_per_row, int* rows_per_lane) {
+    if (!g) return vgx_fail(VGX_EINVAL, "vgx_group_plan_info: NULL group");
+    if (lanes_per_row) *lanes_per_row = g->lpr;
+    if (rows_per_lane) *rows_per_lane = g->ri;
+    return VGX_OK;
+}
+
 static int launch_group(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, const float* xf, void* y,
                         const int16_t* rw = nullptr, float eps = 0.0f, int* argmax_out = nullptr,
                         const StepTail* tail = nullptr) {

@@ -279,6 +279,11 @@ struct vgx_engine {
             }
         }
         if ((st = vgx_group_create(ctx, (int)head_tiles.size(), head_tiles.data(), &head))) return st;
+        // the logits buffers hold vocab rows and a token id indexes the
+        // concatenated tiles, so the tiles must cover exactly the vocabulary
+        if (vgx_group_rows(head) != m.vocab)
+            return fail(VGX_EINVAL, "the logits tiles hold " + std::to_string(vgx_group_rows(head)) +
+                                        " rows for a vocabulary of " + std::to_string(m.vocab));
         // attention state: Session's rope tables (engine/src/session.cpp:188-202)
         const int half = hd / 2;
         std::vector<float>& rc = rope_c;

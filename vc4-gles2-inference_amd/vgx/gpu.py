@@ -60,6 +60,12 @@ class Group:
         _l.check(_l.load().vgx_gemv_group(self.gpu.ctx, self.h, _ptr(x), _ptr(out)))
         return out
 
+    def plan(self):
+        """(lanes per row, rows per lane) of this group's launch."""
+        lpr, ri = ctypes.c_int(), ctypes.c_int()
+        _l.check(_l.load().vgx_group_plan_info(self.h, ctypes.byref(lpr), ctypes.byref(ri)))
+        return lpr.value, ri.value
+
     def gemv_f32(self, x, out=None):
         out = out if out is not None else torch.empty(self.rows, dtype=torch.float32, device=x.device)
         _l.check(_l.load().vgx_gemv_group_f32(self.gpu.ctx, self.h, _ptr(x), _ptr(out)))
@@ -309,6 +315,12 @@ class GPU:
         out = out if out is not None else torch.empty(mat.rows, dtype=torch.int16, device=x.device)
         _l.check(_l.load().vgx_gemv(self.ctx, mat.h, _ptr(x), _ptr(res), _ptr(out)))
         return out
+
+    def plan(self, mat):
+        """(lanes per row, rows per lane) of a GEMV launch over mat."""
+        lpr, ri = ctypes.c_int(), ctypes.c_int()
+        _l.check(_l.load().vgx_gemv_plan_info(self.ctx, mat.h, ctypes.byref(lpr), ctypes.byref(ri)))
+        return lpr.value, ri.value
 
     def matvec_f32(self, mat, x, out=None):
         out = out if out is not None else torch.empty(mat.rows, dtype=torch.float32, device=x.device)

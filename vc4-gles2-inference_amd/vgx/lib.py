@@ -63,6 +63,8 @@ _SIGS = {
     "vgx_group_create": (_I, [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(_P)]),
     "vgx_group_free": (_I, [_P]),
     "vgx_group_rows": (_I, [_P]),
+    "vgx_gemv_plan_info": (_I, [_P, _P, ctypes.POINTER(_I), ctypes.POINTER(_I)]),
+    "vgx_group_plan_info": (_I, [_P, ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "vgx_gemv_group": (_I, [_P, _P, _P, _P]),
     "vgx_gemv_group_f32": (_I, [_P, _P, _P, _P]),
     "vgx_logits_argmax": (_I, [_P, _P, _P, _P, _P]),
