@@ -189,6 +189,17 @@ int vgx_gemv_group_rms(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, const
                        int16_t* y);
 int vgx_logits_argmax_rms(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, const int16_t* rms_w, float eps,
                           int16_t* logits, int* token);
+/* vgx_logits_argmax_rms with the workgroups' key slots in a static device
+ * array of 4096 slots (32 KiB per device, resolved at vgx_ctx_create) instead
+ * of the group's own: no counterpart in the reference; for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops).  The call allocates nothing.  A launch needing more workgroups than
+ * there are slots is refused (VGX_ERANGE; the LM-head launch takes at most 4
+ * per CU).  Every call on one device shares the array: calls that overlap on
+ * one GPU (other streams, other threads) race; every slot a call reads is
+ * written by that call first. */
+int vgx_logits_argmax_rms_noalloc(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, const int16_t* rms_w,
+                                  float eps, int16_t* logits, int* token);
 
 /* ---- batched prefill: ntok consecutive positions per launch, every row the
  * exact result of the batch-1 entry point on that token.  Replaces

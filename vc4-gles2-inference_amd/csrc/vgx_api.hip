@@ -2,14 +2,39 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
 #include "vgx_internal.h"
 
+// Key slots of vgx_logits_argmax_rms_noalloc: one u64 per workgroup of its
+// LM-head launch, in static device memory instead of the group's allocation.
+// Each device holds its own copy until the process ends; host code uses only
+// the per-device address hipGetSymbolAddress returns (in host code the
+// array's name is a stand-in, not a device address).
+static constexpr int kScratchKeys = 4096;  // 32 KiB per device
+static __device__ __align__(256) unsigned long long scratch[kScratchKeys];
+
 namespace {
 thread_local std::string g_last_error;
+
+std::mutex g_scratch_mu;
+std::vector<unsigned long long*> g_scratch_dev;  // by device ordinal
+
+int scratch_keys_for(int device, unsigned long long** out) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if ((int)g_scratch_dev.size() <= device) g_scratch_dev.resize((size_t)device + 1, nullptr);
+    if (!g_scratch_dev[device]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return vgx_hip_fail(e, "hipGetSymbolAddress(scratch)");
+        g_scratch_dev[device] = static_cast<unsigned long long*>(p);
+    }
+    *out = g_scratch_dev[device];
+    return VGX_OK;
 }
+}  // namespace
 
 int vgx_fail(int status, const std::string& msg) {
     g_last_error = msg;
@@ -51,9 +76,13 @@ int vgx_ctx_create(int device, vgx_ctx** out) {
     VGX_HIP(hipSetDevice(device));
     hipDeviceProp_t prop;
     VGX_HIP(hipGetDeviceProperties(&prop, device));
+    unsigned long long* keys = nullptr;
+    const int st = scratch_keys_for(device, &keys);  // with the device current
+    if (st != VGX_OK) return st;
     vgx_ctx* c = new vgx_ctx();
     c->device = device;
     c->num_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+    c->scratch_keys = keys;
     hipError_t e = hipStreamCreate(&c->own);
     if (e != hipSuccess) {
         delete c;
@@ -468,7 +497,7 @@ int vgx_group_plan_info(const vgx_group* g, int* lanes_per_row, int* rows_per_la
 
 static int launch_group(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, const float* xf, void* y,
                         const int16_t* rw = nullptr, float eps = 0.0f, int* argmax_out = nullptr,
-                        const StepTail* tail = nullptr) {
+                        const StepTail* tail = nullptr, bool static_keys = false) {
     if (!ctx || !g || !y || (!x && !xf)) return vgx_fail(VGX_EINVAL, "gemv_group: NULL argument");
     if (!aligned16(x ? (const void*)x : (const void*)xf))
         return vgx_fail(VGX_EINVAL, "gemv_group: x must be 16-byte aligned");
@@ -493,8 +522,11 @@ static int launch_group(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, cons
     L.rw = rw;
     L.eps = eps;
     L.argmax_out = argmax_out;
-    L.argmax_key = g->keys;
-    L.nkeys = g->nkeys;
+    L.argmax_key = static_keys ? ctx->scratch_keys : g->keys;
+    L.nkeys = static_keys ? kScratchKeys : g->nkeys;
+    if (static_keys && L.grid > kScratchKeys)
+        return vgx_fail(VGX_ERANGE, "vgx_logits_argmax_rms_noalloc: the launch takes " + std::to_string(L.grid) +
+                                        " workgroups, the static key slots hold " + std::to_string(kScratchKeys));
     L.total_rows = g->rows;
     if (tail) L.tail = *tail;
     return vgx_gemv_launch(L, ctx->stream);
@@ -533,6 +565,14 @@ int vgx_logits_argmax_rms(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, co
     if (!token || !logits) return vgx_fail(VGX_EINVAL, "vgx_logits_argmax_rms: NULL output");
     if (!rms_w) return vgx_fail(VGX_EINVAL, "vgx_logits_argmax_rms: NULL RMSNorm weight");
     return launch_group(ctx, g, x, nullptr, logits, rms_w, eps, token);
+}
+
+int vgx_logits_argmax_rms_noalloc(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, const int16_t* rms_w,
+                                  float eps, int16_t* logits, int* token) {
+    if (!token || !logits) return vgx_fail(VGX_EINVAL, "vgx_logits_argmax_rms_noalloc: NULL output");
+    if (!rms_w) return vgx_fail(VGX_EINVAL, "vgx_logits_argmax_rms_noalloc: NULL RMSNorm weight");
+    if (!ctx || !ctx->scratch_keys) return vgx_fail(VGX_EINVAL, "vgx_logits_argmax_rms_noalloc: no context");
+    return launch_group(ctx, g, x, nullptr, logits, rms_w, eps, token, nullptr, true);
 }
 
 int vgx_logits_argmax_step(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, const int16_t* rms_w, float eps,

@@ -55,6 +55,9 @@ struct vgx_ctx {
     int num_cu = 256;
     hipStream_t own = nullptr;
     hipStream_t stream = nullptr;
+    // this device's address of the library's static key-slot array (the
+    // no-allocation argmax entry point), resolved once per device at create
+    unsigned long long* scratch_keys = nullptr;
 };
 
 struct vgx_mat {

@@ -74,6 +74,7 @@ _SIGS = {
     "vgx_ffn_gate_rms": (_I, [_P, _P, _P, _P, _P, ctypes.c_float, _I, _P]),
     "vgx_gemv_group_rms": (_I, [_P, _P, _P, _P, ctypes.c_float, _P]),
     "vgx_logits_argmax_rms": (_I, [_P, _P, _P, _P, ctypes.c_float, _P, _P]),
+    "vgx_logits_argmax_rms_noalloc": (_I, [_P, _P, _P, _P, ctypes.c_float, _P, _P]),
     "vgx_gemm": (_I, [_P, _P, _I, _P, _P, _P]),
     "vgx_gemm_add_split": (_I, [_P, _P, _I, _I, _P, _P, _P]),
     "vgx_ffn_gate_batch": (_I, [_P, _P, _P, _I, _P, _I, _P]),
