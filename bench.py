@@ -154,6 +154,9 @@ def cpu_baseline(seconds):
                       "%.1f s on 1 thread" % (passes, dt, cores, passes1, dt1)}
 
 
+GRAPHS = True  # decode steps replayed as one HIP graph (--no-graphs: individual launches)
+
+
 def model_decode(name, spec, scheme, kv_bits, n_prompt, n_gen, runs):
     """A seeded synthetic model through the engine: n_prompt prompt tokens
     (batched prefill) then n_gen greedy tokens; decode tokens/s over the
@@ -165,6 +168,7 @@ def model_decode(name, spec, scheme, kv_bits, n_prompt, n_gen, runs):
     blob = synth.container(spec, scheme, seed=0, q8_row=True)
     prompt = synth.prompt(n_prompt, spec.vocab, seed=0)
     eng = Engine(blob, kv_bits=kv_bits)
+    eng.set_graphs(GRAPHS)
     eng.generate(prompt, n_gen)
     pf, dc, toks = [], [], None
     for _ in range(runs):
@@ -176,7 +180,7 @@ def model_decode(name, spec, scheme, kv_bits, n_prompt, n_gen, runs):
     return blob, prompt, toks, {
         "model": name, "prompt": n_prompt, "gen": n_gen, "seq": spec.seq, "kv": "q%d" % kv_bits,
         "tokens_per_s": round(1000.0 / ms_tok, 1), "ms_per_token": round(ms_tok, 4),
-        "prefill_ms": round(float(np.median(pf)), 3), "runs": runs}
+        "prefill_ms": round(float(np.median(pf)), 3), "runs": runs, "graphs": GRAPHS}
 
 
 def decode_bench(runs):
@@ -384,6 +388,8 @@ def main():
                     default=None,
                     help="run one leg (for profiling); the JSON line then carries that leg only")
     ap.add_argument("--prefill-runs", type=int, default=5)
+    ap.add_argument("--no-graphs", action="store_true",
+                    help="decode legs issue each step's launches instead of replaying a HIP graph")
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--skip-models", action="store_true", help="skip the C4 hybrid and C5 ternary decode legs")
     ap.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "BENCH_LOG"),
@@ -392,6 +398,8 @@ def main():
     if args.pmc_summary:
         print(json.dumps(pmc_summary(*args.pmc_summary), indent=1))
         return
+    global GRAPHS
+    GRAPHS = not args.no_graphs
     if args.gpus != 1:
         print("bench.py measures one GPU: the decode path runs on a single device; --gpus %d is not measured"
               % args.gpus, file=sys.stderr)

@@ -225,6 +225,17 @@ int vgx_gemm_add_split(vgx_ctx* ctx, const vgx_mat* W, int split, int ntok, cons
 int vgx_ffn_gate_batch(vgx_ctx* ctx, const vgx_mat* W1, const vgx_mat* W3, int ntok, const int16_t* x, int hs,
                        int16_t* h);
 int vgx_rmsnorm_batch(vgx_ctx* ctx, int ntok, int dim, const int16_t* x, const int16_t* w, float eps, int16_t* y);
+/* RMSNorm fused into the GEMM that consumes it: per token,
+ *   vgx_gemm_rms            vgx_rmsnorm (rms_w, eps) then vgx_gemm
+ *   vgx_ffn_gate_batch_rms  vgx_rmsnorm (rms_w, eps) then vgx_ffn_gate_batch
+ * in one launch with identical results; the normalised rows are not written
+ * out.  The pairs they replace in Session::step_group
+ * (engine/src/session.cpp:1741-1795): the attention norm and the qkv draw,
+ * the FFN norm and the gate.  rms_w: cols q16 values, 16-byte aligned. */
+int vgx_gemm_rms(vgx_ctx* ctx, const vgx_mat* W, int ntok, const int16_t* x, const int16_t* rms_w, float eps,
+                 const int16_t* res, int16_t* y);
+int vgx_ffn_gate_batch_rms(vgx_ctx* ctx, const vgx_mat* W1, const vgx_mat* W3, int ntok, const int16_t* x,
+                           const int16_t* rms_w, float eps, int hs, int16_t* h);
 int vgx_embed_q8_batch(vgx_ctx* ctx, const int8_t* emb, const float* emb_scale, int vocab, int dim, int ntok,
                        const int* tokens, int16_t* x);
 

@@ -84,6 +84,39 @@ def test_ffn_gate_batch(gpu, kind, rows, cols):
             assert np.array_equal(got[t], want), (hs, t)
 
 
+@pytest.mark.parametrize("kind,rows,cols,ntok", [("t3", 1280, 1024, 32), ("q8", 1536, 768, 256), ("q4", 1536, 768, 37),
+                                                 ("q8", 3072, 1024, 5), ("t3", 33, 96, 32), ("q8", 73, 64, 40)])
+def test_gemm_rms(gpu, kind, rows, cols, ntok):
+    """RMSNorm fused into the GEMM: per token the oracle's rmsnorm then its
+    batch-1 row values, bit for bit, with and without a residual."""
+    rng = np.random.default_rng(rows + cols + ntok)
+    m = MK[kind](rng, rows, cols)
+    W = gpu.upload(m)
+    x = np.clip(rng.standard_normal((ntok, cols)) * 900, -32768, 32767).astype(np.int16)
+    x[0, :] = 32767  # a row at the rail
+    w = o.quantize_act(rng.uniform(0.5, 1.5, cols).astype(np.float32))
+    res = x_rows(rng, ntok, rows)
+    got = host(gpu.gemm_rms(W, dev(x), dev(w), 1e-5))
+    got_r = host(gpu.gemm_rms(W, dev(x), dev(w), 1e-5, res=dev(res)))
+    for t in range(ntok):
+        v = oracle_rowval(m, o.rmsnorm(x[t], w, 1e-5))
+        assert np.array_equal(got[t], o.store(v)), t
+        assert np.array_equal(got_r[t], o.store(v, res[t])), t
+
+
+@pytest.mark.parametrize("kind,rows,cols,ntok", [("t3", 4096, 1024, 32), ("q4", 1216, 768, 64), ("q8", 2432, 768, 9)])
+def test_ffn_gate_batch_rms(gpu, kind, rows, cols, ntok):
+    rng = np.random.default_rng(rows + ntok)
+    m1, m3 = MK[kind](rng, rows, cols), MK[kind](rng, rows, cols)
+    W1, W3 = gpu.upload(m1), gpu.upload(m3)
+    x = np.clip(rng.standard_normal((ntok, cols)) * 700, -32768, 32767).astype(np.int16)
+    w = o.quantize_act(rng.uniform(0.5, 1.5, cols).astype(np.float32))
+    got = host(gpu.ffn_gate_batch_rms(W1, W3, dev(x), dev(w), 1e-5, 1))
+    for t in range(ntok):
+        xn = o.rmsnorm(x[t], w, 1e-5)
+        assert np.array_equal(got[t], o.gate(oracle_rowval(m1, xn), oracle_rowval(m3, xn), 1)), t
+
+
 def test_rmsnorm_and_embed_batch(gpu):
     rng = np.random.default_rng(5)
     x = np.clip(rng.standard_normal((19, 768)) * 900, -32768, 32767).astype(np.int16)

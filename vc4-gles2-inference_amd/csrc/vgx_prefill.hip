@@ -18,14 +18,22 @@
 // so  sum w*x = 256*sum w*xh + sum w*(xl - 128) + 128*sum w, every term an
 // exact integer (|partial| <= 128*128*K < 2^31 for K <= 32768).
 //
-// A workgroup owns a 32-token x 32-row output tile; its 4 waves take a
-// contiguous quarter of the k-steps each, load each step's operands one step
-// ahead, and wave 0 adds the other waves' partial sums (exact integers; for
-// q4 doubles, in wave order) before the epilogue.  Epilogues restate the batch-1 GEMV's fp32
-// expressions: q16 store (+ residual, one rounding), the SwiGLU gate over W1
-// and W3, and the two-half residual add of the split w2.  q4 applies its
-// per-group fp32 terms after each 32-column group (one MFMA k-step = one
-// group) and sums them in double in group order, as the oracle does.
+// A workgroup owns a 32-token x 32-row output tile; its NW waves (4, or 8
+// for a launch of few tiles and long rows: the decode batch) take contiguous
+// runs of the k-steps.  A wave works in rounds of 4 k-steps: the round's
+// activation block (32 tokens x 128 columns) arrives with coalesced loads and
+// passes through the wave's LDS block into the matrix-core layout, while the
+// weight operands stream from global memory 4 steps ahead.  Loading the A
+// operands straight into the matrix-core layout made every load instruction
+// touch 32 token rows 2 bytes x cols apart; on MI355X that cost up to 3.4 us
+// per 32-token launch.  Wave 0 adds the other waves' partial sums (exact
+// integers; for q4 doubles, in wave order) before the epilogue.  Epilogues
+// restate the batch-1 GEMV's fp32 expressions: q16 store (+ residual, one
+// rounding), the SwiGLU gate over W1 and W3, and the two-half residual add of
+// the split w2.  q4 applies its per-group fp32 terms after each 32-column
+// group (one MFMA k-step = one group) and sums them in double.  The RMS
+// variants normalise the activation rows on the way into LDS, with the
+// statistics formed in the workgroup (GPU::rmsnorm's rounding).
 #include <cmath>
 #include <string>
 
@@ -38,8 +46,6 @@ namespace {
 typedef signed char i8x16 __attribute__((ext_vector_type(16)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
 constexpr int kTile = 32;  // tokens and weight rows per wave tile
 
 enum BatchEpi { BEPI_STORE = 0, BEPI_GATE = 1, BEPI_SPLIT = 2 };
@@ -54,6 +60,8 @@ struct GemmLaunch {
     int ldy;
     int hs;                 // gate: hidden store exponent
     int split;              // split: first column of the second half
+    const int16_t* rw;      // RMS prologue: the q16 norm weight (cols values)
+    float eps;              // RMS prologue: epsilon
 };
 
 union Op {
@@ -78,6 +86,16 @@ __device__ __forceinline__ i32x16 mfma(const Op& a, const Op& b, const i32x16& c
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(a.v, b.v, c, 0, 0, 0);
 }
 
+// GPU::rmsnorm's output element (engine/src/gpu_upload.cpp:280-365):
+// q16(x * inv * w) with the shader's floor(v + 0.5) store; the same
+// expression as the batch-1 GEMV's fused prologue.
+__device__ __forceinline__ uint32_t rms_elem(uint32_t xv16, uint32_t wv16, float inv) {
+    const float xv = (float)(int16_t)xv16 / 256.0f;
+    const float wv = (float)(int16_t)wv16 / 256.0f;
+    const float v = (xv * inv) * wv;
+    return (uint32_t)(uint16_t)(int16_t)q16_round(v * 256.0f);
+}
+
 // A operands: 16 q16 activations (two 16-byte loads of one token row) as the
 // high-byte plane and the low-byte plane minus 128; xsum = their exact sum.
 // ok = false gives zeros.
@@ -97,17 +115,15 @@ __device__ __forceinline__ void x_planes(const uint4 a, const uint4 b, bool ok, 
     xsum = ok ? 256 * sh + (int)sl : 0;
 }
 
-// Four 2-bit t3 codes (one byte) as four int8 levels: bit 0 = |level|,
-// bit 1 = sign (engine/tools/mmcf_hf.py:168-199).
+// Four 2-bit t3 codes (one byte, code j at bits 2j..2j+1) as four int8
+// levels: bit 0 = |level|, bit 1 = sign (engine/tools/mmcf_hf.py:168-199);
+// code 2 (a sign without magnitude) is level 0.  Each code is spread to its
+// own byte, then level = |l| ^ ((sign & |l|) * 0xFE): 0x01 or 0xFF.
 __device__ __forceinline__ uint32_t t3_levels(uint32_t b) {
-    uint32_t r = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t c = (b >> (2 * j)) & 3u;
-        const uint32_t lv = c == 1u ? 0x01u : (c == 3u ? 0xFFu : 0x00u);
-        r |= lv << (8 * j);
-    }
-    return r;
+    const uint32_t x = (b | (b << 6) | (b << 12) | (b << 18)) & 0x03030303u;
+    const uint32_t m = x & 0x01010101u;
+    const uint32_t sg = (x >> 1) & m;
+    return m ^ (sg * 0xFEu);
 }
 
 // The bytes of weight row n, columns k0..k0+15: 16 (q8) or 8 (q4, t3, in .x
@@ -169,16 +185,75 @@ __device__ __forceinline__ float gate_value(float v1, float v3, int hs) {
     return o * 256.0f;
 }
 
-template <int KIND, int EPI>
-__global__ void __launch_bounds__(kThreads) gemm_kernel(const GemmLaunch G) {
+// The inverse RMS of each of the workgroup's token rows (rms_stats_split,
+// engine/src/gpu_upload.cpp:280-365, as the batch-1 GEMV's fused prologue
+// forms it): 32 partial sums of x^2 over contiguous slices of ceil(K/32)
+// values, each stored as floor(P/16 + 1/2), their exact total tot, then
+// inv = 1 / sqrt((tot/4096)/K + eps).  One (token, slice) pair a thread.
+template <int NT>
+__device__ __forceinline__ void rms_stats(const GemmLaunch& G, int t0, unsigned long long* s_tot, float* s_inv) {
+    const int K = G.cols;
+    const int per = (K + 31) / 32;
+    if (threadIdx.x < kTile) s_tot[threadIdx.x] = 0ull;
+    __syncthreads();
+    for (int pr = threadIdx.x; pr < kTile * 32; pr += NT) {
+        const int tt = pr >> 5, sl = pr & 31;
+        const int t = t0 + tt;
+        if (t >= G.ntok) continue;
+        const int16_t* xr = G.x + (size_t)t * G.ldx;
+        const int c0 = sl * per, c1 = min(c0 + per, K);
+        long long P = 0;
+        if ((per & 7) == 0) {
+            for (int c = c0; c < c1; c += 8) {
+                const uint4 v = *reinterpret_cast<const uint4*>(xr + c);
+                const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const long long a = (int16_t)(d[k] & 0xFFFFu), b = (int16_t)(d[k] >> 16);
+                    P += a * a + b * b;
+                }
+            }
+        } else {
+            for (int c = c0; c < c1; ++c) {
+                const long long a = xr[c];
+                P += a * a;
+            }
+        }
+        atomicAdd(&s_tot[tt], (unsigned long long)((P + 8) >> 4));
+    }
+    __syncthreads();
+    if (threadIdx.x < kTile) {
+        const long long tot = (long long)s_tot[threadIdx.x];
+        const float ss = (float)tot / 4096.0f;
+        s_inv[threadIdx.x] = (float)(1.0 / sqrt((double)(ss / (float)K + G.eps)));
+    }
+    __syncthreads();
+}
+
+// One workgroup: a 32-token x 32-weight-row output tile.  Its NW waves take
+// contiguous runs of the k-steps (32 columns each); every wave keeps the raw
+// operand bytes of its next NPF steps in flight, and the waves' exact partial
+// sums (doubles for q4, added in wave order) meet in wave 0, RC accumulator
+// registers a round, before the epilogue.  NW = 4 when the launch has many
+// tiles; 8 when it has few (the decode batch of up to 32 sequences), so that
+// each wave walks fewer steps.  RMS: the input rows go through RMSNorm first,
+// the statistics formed in the workgroup.
+template <int KIND, int EPI, int NW, bool RMS>
+__global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmLaunch G) {
+    constexpr int NT = 64 * NW;
     constexpr int NA = EPI == BEPI_STORE ? 1 : 2;  // accumulator sets: W1/W3 or the two halves
-    // Waves 1..3 hand their partial sums to wave 0 through LDS, lane-major:
-    // q8/t3 [wave-1][set][ch 0..15, cl 0..15][lane] int32 plus the weight
-    // sums; q4 [wave-1][set][r][lane] double.
-    constexpr int kRedInts = (kWaves - 1) * NA * 32 * 64 + (kWaves - 1) * NA * 64;
-    constexpr int kRedBytes = KIND == VGX_Q4 ? (kWaves - 1) * NA * 16 * 64 * 8 : kRedInts * 4;
-    __shared__ __align__(16) unsigned char s_red[kRedBytes];
-    __shared__ int s_xg[kWaves][kTile];  // q4: this step's group sum of x per token
+    constexpr int RC = 16 / NA;                    // accumulator registers a reduction round
+    constexpr int NPF = 4;                         // k-steps a round
+    // LDS: each wave's activation block for a round (32 tokens x NPF steps of
+    // 32 columns, int16: 256 bytes a token), reused for the reduction once
+    // every wave is past its last round
+    extern __shared__ __align__(16) unsigned char s_dyn[];
+    __shared__ int s_ws[NW - 1][NA][64];
+    __shared__ int s_xg[NW][kTile];  // q4: this step's group sum of x per token
+    __shared__ unsigned long long s_tot[kTile];
+    __shared__ float s_inv[kTile];
+    constexpr int XROW = NPF * kTile * 2;  // bytes of a token's row in the block
+    constexpr int XB = kTile * XROW;
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -192,11 +267,9 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(const GemmLaunch G) {
     const int t = t0 + li;  // this lane's token row (A operand)
     const bool nok = n < M.rows;
     const bool tok = t < G.ntok;
-    const int16_t* xrow = G.x + (size_t)(tok ? t : 0) * G.ldx;
     const int nsteps = (K + kTile - 1) / kTile;
-    // the four waves of a workgroup share one 32 x 32 output tile and take a
-    // contiguous quarter of the k-steps each
-    const int s_beg = (nsteps * wave) / kWaves, s_end = (nsteps * (wave + 1)) / kWaves;
+    const int s_beg = (nsteps * wave) / NW, s_end = (nsteps * (wave + 1)) / NW;
+    unsigned char* s_xw = s_dyn + (size_t)wave * XB;
 
     i32x16 ch[NA], cl[NA];
     double dacc[NA][16];
@@ -211,27 +284,19 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(const GemmLaunch G) {
     }
     const float ps = M.ps, ps3 = G.M3.ps;
 
-    // A step's operands: the raw bytes of the lane's NPF next steps are in
+    // Weight operands: the raw bytes of the lane's NPF next steps are in
     // flight together (each step's loads go out NPF steps ahead of its
     // multiply), from clamped in-range addresses, unconditionally -- a
     // predicated load would be waited for before the next one is issued --
-    // and out-of-range tokens, rows and columns become zeros when the bytes
-    // are turned into operands.
-    struct Ops {
-        Op xh, xl, w, w3;
-        int xs, ws, ws3;
-        uint32_t sm, sm3;
-    };
+    // and out-of-range rows and columns become zeros when the bytes are
+    // turned into operands.
     struct Raw {
-        uint4 xa, xb, w, w3;
+        uint4 w, w3;
         uint32_t sm, sm3;
     };
     const int nn = nok ? n : M.rows - 1;
     auto raw_load = [&](int s, Raw& r) {
         const int k0 = min(s * kTile + half * 16, K - 16);
-        const uint4* p = reinterpret_cast<const uint4*>(xrow + k0);
-        r.xa = p[0];
-        r.xb = p[1];
         r.w = w_raw<KIND>(M, nn, k0, K);
         if (EPI == BEPI_GATE) r.w3 = w_raw<KIND>(G.M3, nn, k0, K);
         if (KIND == VGX_Q4) {
@@ -239,137 +304,197 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(const GemmLaunch G) {
             if (EPI == BEPI_GATE) r.sm3 = G.M3.sm[(size_t)nn * (K >> 5) + s];
         }
     };
-    auto process = [&](int s, const Raw& r, Ops& o) {
-        const int k0 = s * kTile + half * 16;
-        const bool kok = k0 < K;
-        x_planes(r.xa, r.xb, tok && kok, o.xh, o.xl, o.xs);
-        w_planes<KIND>(r.w, n, nok && kok, o.w, o.ws);
-        o.ws3 = 0;
-        if (EPI == BEPI_GATE) w_planes<KIND>(r.w3, n, nok && kok, o.w3, o.ws3);
-        if (KIND == VGX_Q4) {
-            o.sm = nok ? r.sm : 0u;
-            o.sm3 = (EPI == BEPI_GATE && nok) ? r.sm3 : 0u;
+    // Activation operands: a round's block (the wave's NPF steps for the 32
+    // tokens) is read with coalesced loads -- instruction i, lane l: token
+    // 4i + l/16, the 16-byte piece l%16 of its 256 bytes -- and stored in the
+    // wave's LDS block with piece q of token row r at q ^ (r & 7), so the 8
+    // lanes of a matrix-core read group (rows r..r+7) hit 8 bank groups.
+    // Tokens past ntok read the last token (their operands are zeroed).
+    const int pc = lane & 15;
+    auto x_load = [&](int s0, uint4 (&v)[8], uint4& wv) {
+        const int col = min(s0 * kTile + pc * 8, K - 8);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int tt = min(t0 + 4 * i + (lane >> 4), G.ntok - 1);
+            v[i] = *reinterpret_cast<const uint4*>(G.x + (size_t)tt * G.ldx + col);
+        }
+        if (RMS) wv = *reinterpret_cast<const uint4*>(G.rw + col);
+    };
+    auto x_store = [&](const uint4 (&v)[8], const uint4& wv) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = 4 * i + (lane >> 4);
+            uint4 d = v[i];
+            if (RMS) {
+                const float inv = s_inv[r];
+                const uint32_t xd[4] = {d.x, d.y, d.z, d.w};
+                const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
+                uint32_t o[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    o[k] = rms_elem(xd[k] & 0xFFFFu, wd[k] & 0xFFFFu, inv) |
+                           (rms_elem(xd[k] >> 16, wd[k] >> 16, inv) << 16);
+                d = make_uint4(o[0], o[1], o[2], o[3]);
+            }
+            *reinterpret_cast<uint4*>(s_xw + r * XROW + ((pc ^ (r & 7)) << 4)) = d;
         }
     };
-    constexpr int NPF = 4;
+
+    // the activation block of round r + 1 and the weights NPF steps ahead
+    // are loaded while round r is multiplied (a second round in flight cost
+    // more in occupancy than it hid)
     Raw rb[NPF];
+    uint4 xn[8], wn = make_uint4(0u, 0u, 0u, 0u);
     if (s_beg < s_end) {
+        x_load(s_beg, xn, wn);
 #pragma unroll
         for (int j = 0; j < NPF; ++j) raw_load(min(s_beg + j, s_end - 1), rb[j]);
     }
-    for (int s0 = s_beg; s0 < s_end; s0 += NPF)
+    if (RMS) rms_stats<NT>(G, t0, s_tot, s_inv);
+    auto do_round = [&](int s0, uint4 (&xv)[8], uint4& wv, Raw* rr) {
+        x_store(xv, wv);
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        if (s0 + NPF < s_end) x_load(s0 + NPF, xv, wv);
 #pragma unroll
-    for (int j = 0; j < NPF; ++j) {
-        const int s = s0 + j;
-        if (s >= s_end) break;
-        Ops cur;
-        process(s, rb[j], cur);
-        raw_load(min(s + NPF, s_end - 1), rb[j]);
-        const int k0 = s * kTile + half * 16;
-        if (KIND != VGX_Q4) {
-            if (EPI == BEPI_SPLIT) {
-                // a lane's 16 columns lie on one side of the split (split % 16 == 0)
-                const bool lo_side = k0 < G.split;
-                Op zh, zl;
-                for (int i = 0; i < 4; ++i) { zh.d[i] = 0u; zl.d[i] = 0u; }
-                ch[0] = mfma(lo_side ? cur.xh : zh, cur.w, ch[0]);
-                cl[0] = mfma(lo_side ? cur.xl : zl, cur.w, cl[0]);
-                ch[NA - 1] = mfma(lo_side ? zh : cur.xh, cur.w, ch[NA - 1]);
-                cl[NA - 1] = mfma(lo_side ? zl : cur.xl, cur.w, cl[NA - 1]);
-                if (lo_side) wsum[0] += cur.ws; else wsum[NA - 1] += cur.ws;
+        for (int j = 0; j < NPF; ++j) {
+            const int s = s0 + j;
+            if (s >= s_end) break;
+            const int k0 = s * kTile + half * 16;
+            const bool kok = k0 < K;
+            const int q0 = 4 * j + 2 * half;
+            const unsigned char* row = s_xw + li * XROW;
+            const uint4 x0 = *reinterpret_cast<const uint4*>(row + ((q0 ^ (li & 7)) << 4));
+            const uint4 x1 = *reinterpret_cast<const uint4*>(row + (((q0 + 1) ^ (li & 7)) << 4));
+            Op xh, xl, w, w3;
+            int xs, ws, ws3 = 0;
+            x_planes(x0, x1, tok && kok, xh, xl, xs);
+            w_planes<KIND>(rr[j].w, n, nok && kok, w, ws);
+            if (EPI == BEPI_GATE) w_planes<KIND>(rr[j].w3, n, nok && kok, w3, ws3);
+            const uint32_t sm = (KIND == VGX_Q4 && nok) ? rr[j].sm : 0u;
+            const uint32_t sm3 = (KIND == VGX_Q4 && EPI == BEPI_GATE && nok) ? rr[j].sm3 : 0u;
+            raw_load(min(s + NPF, s_end - 1), rr[j]);
+            if (KIND != VGX_Q4) {
+                if (EPI == BEPI_SPLIT) {
+                    // a lane's 16 columns lie on one side of the split (split % 16 == 0)
+                    const bool lo_side = k0 < G.split;
+                    Op zh, zl;
+                    for (int i = 0; i < 4; ++i) { zh.d[i] = 0u; zl.d[i] = 0u; }
+                    ch[0] = mfma(lo_side ? xh : zh, w, ch[0]);
+                    cl[0] = mfma(lo_side ? xl : zl, w, cl[0]);
+                    ch[NA - 1] = mfma(lo_side ? zh : xh, w, ch[NA - 1]);
+                    cl[NA - 1] = mfma(lo_side ? zl : xl, w, cl[NA - 1]);
+                    if (lo_side) wsum[0] += ws; else wsum[NA - 1] += ws;
+                } else {
+                    ch[0] = mfma(xh, w, ch[0]);
+                    cl[0] = mfma(xl, w, cl[0]);
+                    wsum[0] += ws;
+                    if (EPI == BEPI_GATE) {
+                        ch[NA - 1] = mfma(xh, w3, ch[NA - 1]);
+                        cl[NA - 1] = mfma(xl, w3, cl[NA - 1]);
+                        wsum[NA - 1] += ws3;
+                    }
+                }
             } else {
-                ch[0] = mfma(cur.xh, cur.w, ch[0]);
-                cl[0] = mfma(cur.xl, cur.w, cl[0]);
-                wsum[0] += cur.ws;
-                if (EPI == BEPI_GATE) {
-                    ch[NA - 1] = mfma(cur.xh, cur.w3, ch[NA - 1]);
-                    cl[NA - 1] = mfma(cur.xl, cur.w3, cl[NA - 1]);
-                    wsum[NA - 1] += cur.ws3;
-                }
-            }
-        } else {
-            // one step = one 32-column group g = s: D = sum n*x exactly (|D| <
-            // 2^24), then the shader's fp32 term (s16*ps)*D + (m16*ps)*X,
-            // summed in double
-            const i32x16 zero = {};
-            const int xg = cur.xs + __shfl_xor(cur.xs, 32, 64);  // token li's group sum
-            if (half == 0) s_xg[wave][li] = xg;
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            int X[16];
+                // one step = one 32-column group g = s: D = sum n*x exactly (|D| <
+                // 2^24), then the shader's fp32 term (s16*ps)*D + (m16*ps)*X,
+                // summed in double
+                const i32x16 zero = {};
+                const int xg = xs + __shfl_xor(xs, 32, 64);  // token li's group sum
+                if (half == 0) s_xg[wave][li] = xg;
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                int X[16];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) X[r] = s_xg[wave][8 * (r >> 2) + 4 * half + (r & 3)];
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            const int nmat = EPI == BEPI_GATE ? 2 : 1;
-            const int side = (EPI == BEPI_SPLIT && s * kTile >= G.split) ? 1 : 0;
+                for (int r = 0; r < 16; ++r) X[r] = s_xg[wave][8 * (r >> 2) + 4 * half + (r & 3)];
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                const int nmat = EPI == BEPI_GATE ? 2 : 1;
+                const int side = (EPI == BEPI_SPLIT && s * kTile >= G.split) ? 1 : 0;
 #pragma unroll
-            for (int mm = 0; mm < nmat; ++mm) {
-                const Op& wv = mm == 0 ? cur.w : cur.w3;
-                const float pss = mm == 0 ? ps : ps3;
-                const i32x16 dh = mfma(cur.xh, wv, zero);
-                const i32x16 dl = mfma(cur.xl, wv, zero);
-                const int wl = mm == 0 ? cur.ws : cur.ws3;
-                const int wg = wl + __shfl_xor(wl, 32, 64);
-                const uint32_t sm = mm == 0 ? cur.sm : cur.sm3;
-                const float sa = (float)(int16_t)(sm & 0xFFFFu) * pss;
-                const float ma = (float)(int16_t)(sm >> 16) * pss;
-                const int slot = EPI == BEPI_GATE ? mm : side;
+                for (int mm = 0; mm < nmat; ++mm) {
+                    const Op& wo = mm == 0 ? w : w3;
+                    const float pss = mm == 0 ? ps : ps3;
+                    const i32x16 dh = mfma(xh, wo, zero);
+                    const i32x16 dl = mfma(xl, wo, zero);
+                    const int wl = mm == 0 ? ws : ws3;
+                    const int wg = wl + __shfl_xor(wl, 32, 64);
+                    const uint32_t smm = mm == 0 ? sm : sm3;
+                    const float sa = (float)(int16_t)(smm & 0xFFFFu) * pss;
+                    const float ma = (float)(int16_t)(smm >> 16) * pss;
+                    const int slot = EPI == BEPI_GATE ? mm : side;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int D = 256 * dh[r] + dl[r] + 128 * wg;
-                    const float t1 = sa * (float)D;
-                    const float t2 = ma * (float)X[r];
-                    const float tt = t1 + t2;
-                    dacc[slot][r] += (double)tt;
+                    for (int r = 0; r < 16; ++r) {
+                        const int D = 256 * dh[r] + dl[r] + 128 * wg;
+                        const float t1 = sa * (float)D;
+                        const float t2 = ma * (float)X[r];
+                        const float tt = t1 + t2;
+                        dacc[slot][r] += (double)tt;
+                    }
                 }
             }
         }
-    }
 
-    // waves 1..3 hand over; wave 0 adds the partials in wave order and stores
-    if (wave > 0) {
-        if (KIND == VGX_Q4) {
-            double* p = reinterpret_cast<double*>(s_red) + (size_t)(wave - 1) * NA * 16 * 64;
+        // this round's reads of the block are done before the next round's stores
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    };
+    for (int s0 = s_beg; s0 < s_end; s0 += NPF) do_round(s0, xn, wn, rb);
+    __syncthreads();  // every wave is past its blocks: the LDS becomes the reduction buffer
+    unsigned char* s_red = s_dyn;
+
+    // the waves' partial sums meet in wave 0, RC accumulator registers a
+    // round, added in wave order (exact integers; for q4 the doubles)
 #pragma unroll
-            for (int a = 0; a < NA; ++a)
+    for (int r0 = 0; r0 < 16; r0 += RC) {
+        if (wave > 0) {
+            if (KIND == VGX_Q4) {
+                double* p = reinterpret_cast<double*>(s_red) + (size_t)(wave - 1) * NA * RC * 64;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) p[(a * 16 + r) * 64 + lane] = dacc[a][r];
-        } else {
-            int* p = reinterpret_cast<int*>(s_red) + (size_t)(wave - 1) * NA * 32 * 64;
-            int* pw = reinterpret_cast<int*>(s_red) + (size_t)(kWaves - 1) * NA * 32 * 64 + (wave - 1) * NA * 64;
+                for (int a = 0; a < NA; ++a)
 #pragma unroll
-            for (int a = 0; a < NA; ++a) {
+                    for (int c = 0; c < RC; ++c) p[(a * RC + c) * 64 + lane] = dacc[a][r0 + c];
+            } else {
+                int* p = reinterpret_cast<int*>(s_red) + (size_t)(wave - 1) * NA * 2 * RC * 64;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    p[(a * 32 + r) * 64 + lane] = ch[a][r];
-                    p[(a * 32 + 16 + r) * 64 + lane] = cl[a][r];
-                }
-                pw[a * 64 + lane] = wsum[a];
+                for (int a = 0; a < NA; ++a)
+#pragma unroll
+                    for (int c = 0; c < RC; ++c) {
+                        p[(a * 2 * RC + c) * 64 + lane] = ch[a][r0 + c];
+                        p[(a * 2 * RC + RC + c) * 64 + lane] = cl[a][r0 + c];
+                    }
             }
         }
+        __syncthreads();
+        if (wave == 0) {
+            for (int wv = 1; wv < NW; ++wv) {
+                if (KIND == VGX_Q4) {
+                    const double* p = reinterpret_cast<const double*>(s_red) + (size_t)(wv - 1) * NA * RC * 64;
+#pragma unroll
+                    for (int a = 0; a < NA; ++a)
+#pragma unroll
+                        for (int c = 0; c < RC; ++c) dacc[a][r0 + c] += p[(a * RC + c) * 64 + lane];
+                } else {
+                    const int* p = reinterpret_cast<const int*>(s_red) + (size_t)(wv - 1) * NA * 2 * RC * 64;
+#pragma unroll
+                    for (int a = 0; a < NA; ++a)
+#pragma unroll
+                        for (int c = 0; c < RC; ++c) {
+                            ch[a][r0 + c] += p[(a * 2 * RC + c) * 64 + lane];
+                            cl[a][r0 + c] += p[(a * 2 * RC + RC + c) * 64 + lane];
+                        }
+                }
+            }
+        }
+        __syncthreads();
     }
-    __syncthreads();
+    if (KIND != VGX_Q4) {
+        if (wave > 0)
+#pragma unroll
+            for (int a = 0; a < NA; ++a) s_ws[wave - 1][a][lane] = wsum[a];
+        __syncthreads();
+        if (wave == 0)
+            for (int wv = 1; wv < NW; ++wv)
+#pragma unroll
+                for (int a = 0; a < NA; ++a) wsum[a] += s_ws[wv - 1][a][lane];
+    }
     if (wave != 0) return;
-    for (int wv = 1; wv < kWaves; ++wv) {
-        if (KIND == VGX_Q4) {
-            const double* p = reinterpret_cast<const double*>(s_red) + (size_t)(wv - 1) * NA * 16 * 64;
-#pragma unroll
-            for (int a = 0; a < NA; ++a)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) dacc[a][r] += p[(a * 16 + r) * 64 + lane];
-        } else {
-            const int* p = reinterpret_cast<const int*>(s_red) + (size_t)(wv - 1) * NA * 32 * 64;
-            const int* pw = reinterpret_cast<const int*>(s_red) + (size_t)(kWaves - 1) * NA * 32 * 64 + (wv - 1) * NA * 64;
-#pragma unroll
-            for (int a = 0; a < NA; ++a) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    ch[a][r] += p[(a * 32 + r) * 64 + lane];
-                    cl[a][r] += p[(a * 32 + 16 + r) * 64 + lane];
-                }
-                wsum[a] += pw[a * 64 + lane];
-            }
-        }
-    }
 
     // epilogue: this lane holds column n for 16 token rows
     int wtot[NA];
@@ -408,26 +533,51 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(const GemmLaunch G) {
 
 using GemmFn = void (*)(const GemmLaunch);
 
-template <int EPI>
-GemmFn pick(int kind) {
+template <int EPI, int NW, bool RMS>
+GemmFn pick_kind(int kind) {
     switch (kind) {
-        case VGX_Q8: return gemm_kernel<VGX_Q8, EPI>;
-        case VGX_Q4: return gemm_kernel<VGX_Q4, EPI>;
-        case VGX_T3: return gemm_kernel<VGX_T3, EPI>;
+        case VGX_Q8: return gemm_kernel<VGX_Q8, EPI, NW, RMS>;
+        case VGX_Q4: return gemm_kernel<VGX_Q4, EPI, NW, RMS>;
+        case VGX_T3: return gemm_kernel<VGX_T3, EPI, NW, RMS>;
     }
     return nullptr;
+}
+
+template <int EPI, bool RMS>
+GemmFn pick_nw(int kind, int nw) {
+    switch (nw) {
+        case 4: return pick_kind<EPI, 4, RMS>(kind);
+        case 8: return pick_kind<EPI, 8, RMS>(kind);
+    }
+    return nullptr;
+}
+
+GemmFn pick(int epi, int kind, int nw, bool rms) {
+    if (epi == BEPI_STORE) return rms ? pick_nw<BEPI_STORE, true>(kind, nw) : pick_nw<BEPI_STORE, false>(kind, nw);
+    if (epi == BEPI_GATE) return rms ? pick_nw<BEPI_GATE, true>(kind, nw) : pick_nw<BEPI_GATE, false>(kind, nw);
+    return rms ? nullptr : pick_nw<BEPI_SPLIT, false>(kind, nw);
+}
+
+// Waves per workgroup: 4 when the launch has at least two tiles per CU;
+// otherwise (a few row tiles of a decode batch) 8 when the row has more than
+// 16 k-steps, so the tiles' k-steps are spread over more waves.  (16 waves
+// would cap a lane at 128 registers and spill the operands in flight; 8 waves
+// with four steps in flight keep as many bytes in flight per CU.)
+int waves_for(int tiles, int nsteps, int num_cu) {
+    return tiles < 2 * num_cu && nsteps > 16 ? 8 : 4;
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 int launch(vgx_ctx* ctx, const vgx_mat* W, const vgx_mat* W3, int ntok, const int16_t* x, const int16_t* res,
-           int16_t* y, int epi, int hs, int split, const char* who) {
+           int16_t* y, int epi, int hs, int split, const char* who, const int16_t* rw = nullptr, float eps = 0.0f) {
     if (!ctx || !W || !x || !y) return vgx_fail(VGX_EINVAL, std::string(who) + ": NULL argument");
     if (ntok <= 0 || ntok > 65535 * kTile) return vgx_fail(VGX_EINVAL, std::string(who) + ": ntok outside 1..2097120");
     if (!aligned16(x)) return vgx_fail(VGX_EINVAL, std::string(who) + ": x must be 16-byte aligned");
+    if (rw && !aligned16(rw)) return vgx_fail(VGX_EINVAL, std::string(who) + ": the RMSNorm weight must be 16-byte aligned");
+    if (rw && !(eps > 0.0f)) return vgx_fail(VGX_EINVAL, std::string(who) + ": the RMSNorm epsilon must be positive");
     const MatDev& M = W->d;
-    if (M.kind == VGX_Q8 && M.cols % 16)
-        return vgx_fail(VGX_EINVAL, std::string(who) + ": q8 cols must be a multiple of 16");
+    if (M.cols % 16) return vgx_fail(VGX_EINVAL, std::string(who) + ": cols must be a multiple of 16");
     VGX_HIP(hipSetDevice(ctx->device));
     GemmLaunch L{};
     L.M = M;
@@ -441,11 +591,23 @@ int launch(vgx_ctx* ctx, const vgx_mat* W, const vgx_mat* W3, int ntok, const in
     L.ldy = M.rows;
     L.hs = hs;
     L.split = split;
-    GemmFn fn = epi == BEPI_STORE ? pick<BEPI_STORE>(M.kind)
-              : epi == BEPI_GATE ? pick<BEPI_GATE>(M.kind) : pick<BEPI_SPLIT>(M.kind);
-    if (!fn) return vgx_fail(VGX_EINVAL, std::string(who) + ": unknown weight kind");
+    L.rw = rw;
+    L.eps = eps;
     const dim3 grid((M.rows + kTile - 1) / kTile, (ntok + kTile - 1) / kTile);
-    hipLaunchKernelGGL(fn, grid, dim3(kThreads), 0, ctx->stream, L);
+    const int nw = waves_for((int)(grid.x * grid.y), (M.cols + kTile - 1) / kTile, ctx->num_cu);
+    GemmFn fn = pick(epi, M.kind, nw, rw != nullptr);
+    if (!fn) return vgx_fail(VGX_EINVAL, std::string(who) + ": unknown weight kind");
+    // each wave's activation block: 32 tokens x 4 k-steps of 32 int16
+    const int lds = nw * kTile * 4 * kTile * 2;
+    if (lds > 48 * 1024) {
+        static bool lds_set[64];
+        const int slot = ((epi * 2 + (rw ? 1 : 0)) * 4 + M.kind) * 2 + (nw == 8 ? 1 : 0);
+        if (!lds_set[slot]) {
+            VGX_HIP(hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds));
+            lds_set[slot] = true;
+        }
+    }
+    hipLaunchKernelGGL(fn, grid, dim3(64 * nw), lds, ctx->stream, L);
     VGX_LAUNCH_CHECK("gemm launch");
     return VGX_OK;
 }
@@ -466,6 +628,21 @@ int vgx_gemm_add_split(vgx_ctx* ctx, const vgx_mat* W, int split, int ntok, cons
         return vgx_fail(VGX_EINVAL, "vgx_gemm_add_split: split must be inside cols and a multiple of " +
                                         std::to_string(unit));
     return launch(ctx, W, nullptr, ntok, x, res, y, BEPI_SPLIT, 0, split, "vgx_gemm_add_split");
+}
+
+int vgx_gemm_rms(vgx_ctx* ctx, const vgx_mat* W, int ntok, const int16_t* x, const int16_t* rms_w, float eps,
+                 const int16_t* res, int16_t* y) {
+    if (!rms_w) return vgx_fail(VGX_EINVAL, "vgx_gemm_rms: NULL RMSNorm weight");
+    return launch(ctx, W, nullptr, ntok, x, res, y, BEPI_STORE, 0, 0, "vgx_gemm_rms", rms_w, eps);
+}
+
+int vgx_ffn_gate_batch_rms(vgx_ctx* ctx, const vgx_mat* W1, const vgx_mat* W3, int ntok, const int16_t* x,
+                           const int16_t* rms_w, float eps, int hs, int16_t* h) {
+    if (!W1 || !W3 || !rms_w) return vgx_fail(VGX_EINVAL, "vgx_ffn_gate_batch_rms: NULL argument");
+    if (W1->d.kind != W3->d.kind || W1->d.rows != W3->d.rows || W1->d.cols != W3->d.cols)
+        return vgx_fail(VGX_EINVAL, "vgx_ffn_gate_batch_rms: W1 and W3 differ in kind or shape");
+    if (hs < 0 || hs > 5) return vgx_fail(VGX_EINVAL, "vgx_ffn_gate_batch_rms: hs outside 0..5");
+    return launch(ctx, W1, W3, ntok, x, nullptr, h, BEPI_GATE, hs, 0, "vgx_ffn_gate_batch_rms", rms_w, eps);
 }
 
 int vgx_ffn_gate_batch(vgx_ctx* ctx, const vgx_mat* W1, const vgx_mat* W3, int ntok, const int16_t* x, int hs,

@@ -362,6 +362,21 @@ class GPU:
         _l.check(_l.load().vgx_ffn_gate_batch(self.ctx, w1.h, w3.h, n, _ptr(x), hs, _ptr(out)))
         return out
 
+    def gemm_rms(self, mat, x, rms_w, eps=1e-5, res=None, out=None):
+        """rmsnorm_batch(x, rms_w, eps) then gemm, one launch."""
+        n = x.shape[0]
+        out = out if out is not None else torch.empty((n, mat.rows), dtype=torch.int16, device=x.device)
+        _l.check(_l.load().vgx_gemm_rms(self.ctx, mat.h, n, _ptr(x), _ptr(rms_w), float(eps), _ptr(res), _ptr(out)))
+        return out
+
+    def ffn_gate_batch_rms(self, w1, w3, x, rms_w, eps=1e-5, hs=0, out=None):
+        """rmsnorm_batch(x, rms_w, eps) then ffn_gate_batch, one launch."""
+        n = x.shape[0]
+        out = out if out is not None else torch.empty((n, w1.rows), dtype=torch.int16, device=x.device)
+        _l.check(_l.load().vgx_ffn_gate_batch_rms(self.ctx, w1.h, w3.h, n, _ptr(x), _ptr(rms_w), float(eps), hs,
+                                                  _ptr(out)))
+        return out
+
     def rmsnorm_batch(self, x, w, eps=1e-5, out=None):
         out = out if out is not None else torch.empty_like(x)
         _l.check(_l.load().vgx_rmsnorm_batch(self.ctx, x.shape[0], x.shape[1], _ptr(x), _ptr(w), float(eps),
