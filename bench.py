@@ -296,6 +296,7 @@ def prefill_bench(runs):
     blob = synth.container(spec, "q4", seed=0)
     prompt = synth.prompt(256, spec.vocab, seed=0)
     eng = Engine(blob, kv_bits=8)
+    eng.set_graphs(GRAPHS)
     eng.prefill(prompt, logits=False)
     batched = []
     for _ in range(runs):

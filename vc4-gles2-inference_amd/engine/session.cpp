@@ -62,7 +62,7 @@ struct vgx_engine {
     // batched prefill: row buffers for up to pcap positions; prompts run in
     // batches of pbatch (serial steps when pbatch < 2)
     int pcap = 0, pbatch = 0;
-    int16_t *bh = nullptr, *bx1 = nullptr, *bqkv = nullptr, *batt = nullptr, *bhid = nullptr;
+    int16_t *bh = nullptr, *bx1 = nullptr, *bxn = nullptr, *bqkv = nullptr, *batt = nullptr, *bhid = nullptr;
     // batched decode of nseq sequences in lockstep: their KV caches, the LM
     // head as one matrix, nseq rows of logits, the token history
     vgx_attn* attn_b = nullptr;
@@ -323,7 +323,7 @@ struct vgx_engine {
         pcap = seq < 512 ? seq : 512;
         pbatch = pcap;
         const size_t P = (size_t)pcap;
-        if ((st = dalloc(&bh, P * D)) || (st = dalloc(&bx1, P * D)) ||
+        if ((st = dalloc(&bh, P * D)) || (st = dalloc(&bx1, P * D)) || (st = dalloc(&bxn, P * D)) ||
             (st = dalloc(&batt, P * D)) || (st = dalloc(&bqkv, P * qkv_rows)) || (st = dalloc(&bhid, P * m.hidden)))
             return st;
         hipError_t he = hipDeviceSynchronize();
@@ -389,18 +389,29 @@ struct vgx_engine {
         if ((st = vgx_embed_q8_batch(ctx, emb, emb_scale, m.vocab, D, n, toks_dev, bh))) return st;
         for (int l = 0; l < m.layers; ++l) {
             Layer& ly = L[l];
+            // RMSNorm in the consuming GEMM up to 32 positions (one token tile:
+            // the normalisation runs once per row tile); above, on its own
+            const bool fuse = n <= 32;
+            if (!fuse && (st = vgx_rmsnorm_batch(ctx, n, D, bh, ly.rms_att, eps, bxn))) return st;
+            const vgx_mat* in_mat = is_conv(l) ? ly.conv_in : ly.qkv;
+            st = fuse ? vgx_gemm_rms(ctx, in_mat, n, bh, ly.rms_att, eps, nullptr, bqkv)
+                      : vgx_gemm(ctx, in_mat, n, bxn, nullptr, bqkv);
+            if (st) return st;
             if (is_conv(l)) {
                 // the conv over the batch walks its positions in order
-                if ((st = vgx_gemm_rms(ctx, ly.conv_in, n, bh, ly.rms_att, eps, nullptr, bqkv))) return st;
                 if ((st = vgx_conv_step(conv, l, n, bqkv, batt))) return st;
                 if ((st = vgx_gemm(ctx, ly.conv_out, n, batt, bh, bx1))) return st;
             } else {
-                if ((st = vgx_gemm_rms(ctx, ly.qkv, n, bh, ly.rms_att, eps, nullptr, bqkv))) return st;
                 if ((st = vgx_kv_append_batch(A, l, pos0, n, bqkv))) return st;
                 if ((st = vgx_attn_decode_batch(A, l, pos0, n, bqkv, batt))) return st;
                 if ((st = vgx_gemm(ctx, ly.wo, n, batt, bh, bx1))) return st;
             }
-            if ((st = vgx_ffn_gate_batch_rms(ctx, ly.w1, ly.w3, n, bx1, ly.rms_ffn, eps, ly.hs, bhid))) return st;
+            if (fuse) {
+                if ((st = vgx_ffn_gate_batch_rms(ctx, ly.w1, ly.w3, n, bx1, ly.rms_ffn, eps, ly.hs, bhid))) return st;
+            } else {
+                if ((st = vgx_rmsnorm_batch(ctx, n, D, bx1, ly.rms_ffn, eps, bxn))) return st;
+                if ((st = vgx_ffn_gate_batch(ctx, ly.w1, ly.w3, n, bxn, ly.hs, bhid))) return st;
+            }
             if (ffn_chunk) st = vgx_gemm_add_split(ctx, ly.w2, ffn_chunk, n, bhid, bx1, bh);
             else st = vgx_gemm(ctx, ly.w2, n, bhid, bx1, bh);
             if (st) return st;
