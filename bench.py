@@ -15,6 +15,7 @@ same shapes on this host's cores.
 """
 import argparse
 import json
+import re
 import os
 import sys
 import time
@@ -82,8 +83,9 @@ def pmc_summary(fetch_csv, write_csv, bench_log):
     per = {}
     for kind, kid in (("q8", 1), ("q4", 2)):
         def cold(rows):
-            return [r for r in rows if r["Kernel_Name"].startswith("void (anonymous namespace)::gemv_kernel<%d," % kid)
-                    and ", 4, 1, 1>" in r["Kernel_Name"]]
+            # the f32-epilogue launches with 4 rows per lane: gemv_kernel<kind, lpr, 4, 1, 1[, single]>
+            pat = re.compile(r"gemv_kernel<%d, \d+, 4, 1, 1(, (true|false))?>" % kid)
+            return [r for r in rows if pat.search(r["Kernel_Name"])]
         cfk, cwk = cold(fe), cold(wr)
         per[kind] = {}
         for i, s in enumerate(names):

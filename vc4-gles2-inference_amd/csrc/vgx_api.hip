@@ -184,7 +184,11 @@ int vgx_mat_upload(vgx_ctx* ctx, const vgx_weight_desc* w, vgx_mat** out) {
     m->d.rows = rows;
     m->d.cols = cols;
     m->body_bytes = need;
-    hipError_t e = hipMalloc(&m->body_alloc, need);
+    // q4 rows of 128 bytes or more start at 128-byte multiples (q4_rstride):
+    // a row that ended mid cache line was fetched partly twice
+    const size_t rstride = w->kind == VGX_Q4 ? (size_t)q4_rstride(cols) : 0;
+    m->body_alloc_bytes = w->kind == VGX_Q4 ? (size_t)rows * rstride : need;
+    hipError_t e = hipMalloc(&m->body_alloc, m->body_alloc_bytes);
     if (e != hipSuccess) { delete m; return vgx_hip_fail(e, "hipMalloc(body)"); }
     m->d.body = static_cast<const uint8_t*>(m->body_alloc);
 
@@ -195,6 +199,11 @@ int vgx_mat_upload(vgx_ctx* ctx, const vgx_weight_desc* w, vgx_mat** out) {
         const uint8_t* src = static_cast<const uint8_t*>(w->body);
         for (size_t i = 0; i < need; ++i) tmp[i] = src[i] ^ 0x80u;
         e = hipMemcpy(m->body_alloc, tmp.data(), need, hipMemcpyHostToDevice);
+    } else if (w->kind == VGX_Q4 && rstride != (size_t)cols / 2) {
+        e = hipMemset(m->body_alloc, 0, m->body_alloc_bytes);
+        if (e == hipSuccess)
+            e = hipMemcpy2D(m->body_alloc, rstride, w->body, (size_t)cols / 2, (size_t)cols / 2, (size_t)rows,
+                            hipMemcpyHostToDevice);
     } else {
         e = hipMemcpy(m->body_alloc, w->body, need, hipMemcpyHostToDevice);
     }
@@ -235,9 +244,11 @@ int vgx_mat_clone(vgx_ctx* ctx, const vgx_mat* src, vgx_mat** out) {
     vgx_mat* m = new vgx_mat();
     m->d = src->d;
     m->body_bytes = src->body_bytes;
+    m->body_alloc_bytes = src->body_alloc_bytes;
     m->plane_bytes = src->plane_bytes;
-    hipError_t e = hipMalloc(&m->body_alloc, m->body_bytes);
-    if (e == hipSuccess) e = hipMemcpyAsync(m->body_alloc, src->body_alloc, m->body_bytes, hipMemcpyDeviceToDevice, ctx->stream);
+    hipError_t e = hipMalloc(&m->body_alloc, m->body_alloc_bytes);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(m->body_alloc, src->body_alloc, m->body_alloc_bytes, hipMemcpyDeviceToDevice, ctx->stream);
     if (e == hipSuccess) e = hipMalloc(&m->plane_alloc, m->plane_bytes);
     if (e == hipSuccess) e = hipMemcpyAsync(m->plane_alloc, src->plane_alloc, m->plane_bytes, hipMemcpyDeviceToDevice, ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
@@ -275,6 +286,7 @@ int vgx_mat_concat(vgx_ctx* ctx, int n, vgx_mat* const* mats, vgx_mat** out) {
     m->d.rows = (int)rows;
     m->d.out_off = m->d.blk_off = 0;
     m->body_bytes = body;
+    m->body_alloc_bytes = body;
     m->plane_bytes = plane;
     hipError_t e = hipMalloc(&m->body_alloc, body);
     if (e == hipSuccess) e = hipMalloc(&m->plane_alloc, plane);

@@ -15,10 +15,14 @@
 // each summed in position order, then the chunk sums in chunk order -- and the
 // oracle sums in the same order, so the output is reproducible bit for bit.
 //
-// HBM layout of a layer's cache: seq rows of [K: kv_dim | V: kv_dim], int16
-// little-endian (kv_bits 16, grid 1/2048) or int8 (kv_bits 8, grid 1/16).
-// The reference's texel rows hold the same values in the same order
-// (big-endian for q16); vgx_kv_read_rows / write_rows convert.
+// HBM layout of a layer's cache: head-major planes, K of KV head 0, 1, ...
+// then V of KV head 0, 1, ..., each seq positions x head_dim values, int16
+// little-endian (kv_bits 16, grid 1/2048) or int8 (kv_bits 8, grid 1/16).  A
+// head's prefix 0..pos is one contiguous run (the reference's interleaved
+// [K kv_dim | V kv_dim] texel rows put each head's 96- to 512-byte slice in a
+// different part of a row, so a head's reads straddled cache lines).
+// vgx_kv_read_rows / write_rows gather the planes into the reference's texel
+// rows (big-endian for q16) and back.
 #include <cmath>
 #include <cstring>
 #include <string>
@@ -40,7 +44,8 @@ constexpr int kKPre = KVB == 16 ? 8 : 4;
 
 struct AttnDev {
     int dim, heads, kv_heads, hd, seq, kv_bits, rope_half, qk_norm, group;
-    int row_bytes;
+    int row_bytes;  // one position of every head, K and V: the texel row MMKV1 persists
+    int pstride;    // bytes of one position in a head's plane (head_dim values)
     int lpp;     // lanes per scored position (a power of two)
     // the weighted-V lane plan with one element per lane (vG1 waves per chunk,
     // vC1 chunks per round) and with two (vG2, vC2; taken above head_dim 64
@@ -182,14 +187,14 @@ __device__ __forceinline__ void v_chunk_load(const AttnDev& A, __amdgpu_buffer_r
     if (vE == 2) {
 #pragma unroll
         for (int u = 0; u < kChunk; ++u) {
-            const int off = min(c * kChunk + u, A.seq) * A.row_bytes + vi * (KVB / 8);
+            const int off = min(c * kChunk + u, A.seq) * A.pstride + vi * (KVB / 8);
             if (KVB == 16) vch[u] = (int)__builtin_amdgcn_raw_buffer_load_b32(vrs, off, 0, 0);
             else vch[u] = (int)__builtin_amdgcn_raw_buffer_load_b16(vrs, off, 0, 0);
         }
     } else {
 #pragma unroll
         for (int u = 0; u < kChunk; ++u) {
-            const int off = min(c * kChunk + u, A.seq) * A.row_bytes + vi * (KVB / 8);
+            const int off = min(c * kChunk + u, A.seq) * A.pstride + vi * (KVB / 8);
             if (KVB == 16) vch[u] = (int)__builtin_amdgcn_raw_buffer_load_b16(vrs, off, 0, 0);
             else vch[u] = (int)__builtin_amdgcn_raw_buffer_load_b8(vrs, off, 0, 0);
         }
@@ -250,7 +255,7 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     asm volatile("" ::"s"(kv), "s"(rtab), "s"(qn), "s"(kn), "s"(qkv), "s"(out), "s"(pos0), "s"(do_write),
                  "s"(do_attend), "s"(seq_stride), "s"(pos_step), "s"(pos_ptr));
     asm volatile("" ::"s"(A.dim), "s"(A.kv_heads), "s"(A.hd), "s"(A.seq), "s"(A.rope_half), "s"(A.qk_norm),
-                 "s"(A.group), "s"(A.row_bytes), "s"(A.lpp), "s"(A.vG1), "s"(A.vC1), "s"(A.vG2), "s"(A.vC2),
+                 "s"(A.group), "s"(A.pstride), "s"(A.lpp), "s"(A.vG1), "s"(A.vC1), "s"(A.vG2), "s"(A.vC2),
                  "s"(A.nchmax), "s"(A.o_wmax),
                  "s"(A.o_vpk), "s"(A.o_kpk), "s"(A.o_qhw), "s"(A.o_qlw), "s"(A.o_sc), "s"(A.o_ep), "s"(A.o_csum),
                  "s"(A.o_vpart), "s"(A.o_acc));
@@ -292,8 +297,11 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     double* vpart = reinterpret_cast<double*>(smem + A.o_vpart);  // vC*hd
     double* acc = reinterpret_cast<double*>(smem + A.o_acc);    // hd
 
-    const uint8_t* khead = kv + (size_t)kvh * hd * (KVB / 8);
-    const uint8_t* vhead = kv + (size_t)(kv_dim + kvh * hd) * (KVB / 8);
+    // this KV head's planes: position t of K at khead + t * pstride
+    uint8_t* const khead_w = kv + (size_t)kvh * A.seq * A.pstride;
+    uint8_t* const vhead_w = kv + (size_t)(A.kv_heads + kvh) * A.seq * A.pstride;
+    const uint8_t* khead = khead_w;
+    const uint8_t* vhead = vhead_w;
     const int16_t* kq = qkv + A.dim + kvh * hd;           // this group's K (q16)
     const int16_t* vq = qkv + A.dim + kv_dim + kvh * hd;  // and V
     const int16_t* qh = qkv + h * hd;                     // this head's q
@@ -339,15 +347,15 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     uint4 kreg[KP];
     int vch[kChunk];  // V of elements vi.. at the chunk's positions, as stored
     // rows 0..npos-1 of this head's K and V slices
-    const __amdgpu_buffer_rsrc_t krs = rows_rsrc(khead, npos * A.row_bytes);
-    const __amdgpu_buffer_rsrc_t vrs = rows_rsrc(vhead, npos * A.row_bytes);
+    const __amdgpu_buffer_rsrc_t krs = rows_rsrc(khead, npos * A.pstride);
+    const __amdgpu_buffer_rsrc_t vrs = rows_rsrc(vhead, npos * A.pstride);
     {
         // only the lanes of a scored position read its K row
         const int t = min(tid / lpp, npos);
 #pragma unroll
         for (int k = 0; k < KP; ++k)
             kreg[k] = __builtin_bit_cast(
-                uint4, __builtin_amdgcn_raw_buffer_load_b128(krs, t * A.row_bytes + 16 * min(sj + k * lpp, nv - 1), 0, 0));
+                uint4, __builtin_amdgcn_raw_buffer_load_b128(krs, t * A.pstride + 16 * min(sj + k * lpp, nv - 1), 0, 0));
     }
     // the K loads first: the scores wait for them, not for the V loads after
     asm volatile("" ::: "memory");
@@ -389,9 +397,8 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
         const int q = kv_enc<KVB>(o);
         const int qv = kv_enc<KVB>((float)vqi / 256.0f);
         if (writer) {
-            uint8_t* row = kv + (size_t)pos * A.row_bytes;
-            kv_put<KVB>(row, kvh * hd + tid, q);
-            kv_put<KVB>(row, kv_dim + kvh * hd + tid, qv);
+            kv_put<KVB>(khead_w + (size_t)pos * A.pstride, tid, q);
+            kv_put<KVB>(vhead_w + (size_t)pos * A.pstride, tid, qv);
         }
         kv_put<KVB>(kpk, tid, q);
         kv_put<KVB>(vpk, tid, qv);
@@ -453,7 +460,7 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
 #pragma unroll
             for (int k = 0; k < KP; ++k) w[k] = kreg[k];
         } else {
-            const uint4* src = reinterpret_cast<const uint4*>(khead + (size_t)t * A.row_bytes);
+            const uint4* src = reinterpret_cast<const uint4*>(khead + (size_t)t * A.pstride);
 #pragma unroll
             for (int k = 0; k < KP; ++k) w[k] = src[min(sj + k * lpp, nv - 1)];
         }
@@ -695,6 +702,7 @@ int vgx_attn_create_seqs(vgx_ctx* ctx, const vgx_attn_desc* d, int nseq, vgx_att
     A.kv_bits = d->kv_bits; A.rope_half = d->rope_half ? 1 : 0; A.qk_norm = d->qk_norm ? 1 : 0;
     A.group = d->heads / d->kv_heads;
     A.row_bytes = 2 * d->kv_heads * d->head_dim * (d->kv_bits / 8);
+    A.pstride = d->head_dim * (d->kv_bits / 8);
     at->lds = attn_layout(A);
     if (at->lds > 160 * 1024) {
         delete at;
@@ -800,18 +808,30 @@ int vgx_attn_decode_batch(vgx_attn* a, int layer, int pos0, int ntok, const int1
 
 int vgx_kv_row_bytes(const vgx_attn* a) { return a ? a->a.row_bytes : 0; }
 
+// The planes' rows row0 .. row0+nrows-1 as texel rows: per position, K of
+// every head in head order, then V of every head (q16 big-endian).
 int vgx_kv_read_rows(vgx_attn* at, int layer, int row0, int nrows, void* host) {
     if (!at || !host) return vgx_fail(VGX_EINVAL, "vgx_kv_read_rows: NULL argument");
     if (layer < 0 || layer >= at->layers || !at->kv[layer]) return vgx_fail(VGX_ERANGE, "vgx_kv_read_rows: bad layer");
     if (row0 < 0 || nrows < 0 || row0 + nrows > at->a.seq) return vgx_fail(VGX_ERANGE, "vgx_kv_read_rows: rows outside the cache");
+    if (nrows == 0) return VGX_OK;
     VGX_HIP(hipSetDevice(at->ctx->device));
-    const size_t n = (size_t)nrows * at->a.row_bytes;
+    const AttnDev& A = at->a;
+    const size_t ps = (size_t)A.pstride, np = 2 * (size_t)A.kv_heads;
+    std::vector<uint8_t> planes(np * nrows * ps);  // [plane][row][ps]
     VGX_HIP(hipStreamSynchronize(at->ctx->stream));
-    VGX_HIP(hipMemcpy(host, at->kv[layer] + (size_t)row0 * at->a.row_bytes, n, hipMemcpyDeviceToHost));
-    if (at->a.kv_bits == 16) {
-        uint8_t* b = static_cast<uint8_t*>(host);
-        for (size_t i = 0; i + 1 < n; i += 2) { uint8_t t = b[i]; b[i] = b[i + 1]; b[i + 1] = t; }
-    }
+    VGX_HIP(hipMemcpy2D(planes.data(), nrows * ps, at->kv[layer] + (size_t)row0 * ps, (size_t)A.seq * ps, nrows * ps, np,
+                        hipMemcpyDeviceToHost));
+    uint8_t* out = static_cast<uint8_t*>(host);
+    for (int r = 0; r < nrows; ++r)
+        for (size_t p = 0; p < np; ++p) {
+            const uint8_t* src = planes.data() + (p * nrows + r) * ps;
+            uint8_t* dst = out + (size_t)r * A.row_bytes + p * ps;
+            if (A.kv_bits == 16)
+                for (size_t i = 0; i < ps; i += 2) { dst[i] = src[i + 1]; dst[i + 1] = src[i]; }
+            else
+                memcpy(dst, src, ps);
+        }
     return VGX_OK;
 }
 
@@ -819,13 +839,24 @@ int vgx_kv_write_rows(vgx_attn* at, int layer, int row0, int nrows, const void* 
     if (!at || !host) return vgx_fail(VGX_EINVAL, "vgx_kv_write_rows: NULL argument");
     if (layer < 0 || layer >= at->layers || !at->kv[layer]) return vgx_fail(VGX_ERANGE, "vgx_kv_write_rows: bad layer");
     if (row0 < 0 || nrows < 0 || row0 + nrows > at->a.seq) return vgx_fail(VGX_ERANGE, "vgx_kv_write_rows: rows outside the cache");
+    if (nrows == 0) return VGX_OK;
     VGX_HIP(hipSetDevice(at->ctx->device));
-    const size_t n = (size_t)nrows * at->a.row_bytes;
-    std::vector<uint8_t> tmp(static_cast<const uint8_t*>(host), static_cast<const uint8_t*>(host) + n);
-    if (at->a.kv_bits == 16)
-        for (size_t i = 0; i + 1 < n; i += 2) { uint8_t t = tmp[i]; tmp[i] = tmp[i + 1]; tmp[i + 1] = t; }
+    const AttnDev& A = at->a;
+    const size_t ps = (size_t)A.pstride, np = 2 * (size_t)A.kv_heads;
+    std::vector<uint8_t> planes(np * nrows * ps);
+    const uint8_t* in = static_cast<const uint8_t*>(host);
+    for (int r = 0; r < nrows; ++r)
+        for (size_t p = 0; p < np; ++p) {
+            const uint8_t* src = in + (size_t)r * A.row_bytes + p * ps;
+            uint8_t* dst = planes.data() + (p * nrows + r) * ps;
+            if (A.kv_bits == 16)
+                for (size_t i = 0; i < ps; i += 2) { dst[i] = src[i + 1]; dst[i + 1] = src[i]; }
+            else
+                memcpy(dst, src, ps);
+        }
     VGX_HIP(hipStreamSynchronize(at->ctx->stream));
-    VGX_HIP(hipMemcpy(at->kv[layer] + (size_t)row0 * at->a.row_bytes, tmp.data(), n, hipMemcpyHostToDevice));
+    VGX_HIP(hipMemcpy2D(at->kv[layer] + (size_t)row0 * ps, (size_t)A.seq * ps, planes.data(), nrows * ps, nrows * ps, np,
+                        hipMemcpyHostToDevice));
     return VGX_OK;
 }
 

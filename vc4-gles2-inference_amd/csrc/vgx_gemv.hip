@@ -417,7 +417,7 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
 
     // --- weight chunk geometry
     const int nch = KIND == VGX_Q8 ? (K >> 4) : (K >> 5);
-    const size_t ustride = KIND == VGX_Q8 ? (size_t)K : KIND == VGX_Q4 ? (size_t)(K >> 1)
+    const size_t ustride = KIND == VGX_Q8 ? (size_t)K : KIND == VGX_Q4 ? (size_t)q4_rstride(K)
                                                                      : (size_t)(K >> 3) * 4;
     const uint8_t* body3 = (EPI == EPI_GATE) ? M3.body : nullptr;
     const int niter = (nch + LPR - 1) / LPR;
@@ -940,7 +940,7 @@ __global__ void dequant_kernel(const MatDev M, float* out) {
         if (M.kind == VGX_Q8) {
             v = (float)((int)M.body[i] - 128) * M.wsr[r];
         } else if (M.kind == VGX_Q4) {
-            const uint8_t b = M.body[(size_t)r * (M.cols / 2) + c / 2];
+            const uint8_t b = M.body[(size_t)r * q4_rstride(M.cols) + c / 2];
             const int nb = (c & 1) ? (b >> 4) : (b & 15);
             const uint32_t sm = M.sm[(size_t)r * (M.cols / 32) + c / 32];
             const float sa = (float)(int16_t)(sm & 0xFFFFu) * M.ps;

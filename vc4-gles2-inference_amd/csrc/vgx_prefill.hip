@@ -133,7 +133,7 @@ __device__ __forceinline__ uint4 w_raw(const MatDev& M, int n, int k0, int K) {
     if (KIND == VGX_Q8) return *reinterpret_cast<const uint4*>(M.body + (size_t)n * K + k0);
     uint2 v;
     if (KIND == VGX_Q4) {
-        v = *reinterpret_cast<const uint2*>(M.body + (size_t)n * (K >> 1) + (k0 >> 1));
+        v = *reinterpret_cast<const uint2*>(M.body + (size_t)n * q4_rstride(K) + (k0 >> 1));
     } else {
         const size_t ustride = (size_t)(K >> 3) * 4;
         v = *reinterpret_cast<const uint2*>(M.body + (size_t)(n >> 1) * ustride + (size_t)(k0 >> 3) * 4);
