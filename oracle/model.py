@@ -219,6 +219,83 @@ class QModel(_Base):
         return np.concatenate([o.store(t.rowval(xf)) for t in self.tiles])
 
 
+def rowval_q4_view4(nib, s16, m16, ps, rows, cols, x):
+    """Row values of a q4 matrix as the reference's 4-bit texture view
+    evaluates them, step by step in IEEE fp32 with round-to-nearest and no
+    fused multiply-add: matvec_i4_add_4x4 (engine/src/shaders.cpp:1754-1782);
+    the gate's i4_gate_flat8b (shaders.cpp:1539-1590) and the qkv's
+    matvec_i4_4x4 accumulate the same way.
+
+    The view differs from the packed form only in rounding:
+    - a weight nibble n is sampled from GL_RGBA4 as UNORM, fp32(n/15);
+    - the group scale is unsigned, sampled as two UNORM8 bytes
+      (engine/src/gpu_upload.cpp:170-180: r = s16 >> 8, g = s16 & 255) and
+      rebuilt as r*(65280*15*ps) + g*(255*15*ps);
+    - the group minimum goes through x_i16raw (r*65280 + g*255, minus 65536
+      at or above 32767.5) times ps;
+    - per 8 columns, d += w0.x*xa.x + ... + w1.w*xb.w left to right;
+    - per group, s += sc*d + mn*xsum.
+    What the driver does with the UNORM conversions and whether its compiler
+    fuses multiply-adds is not in the reference's sources, so this is a model
+    of one conforming evaluation, not of a measured device."""
+    f = np.float32
+    ps = f(ps)
+    G = cols // 32
+    b = np.asarray(nib, np.uint8).reshape(rows, cols // 2)
+    n = np.empty((rows, cols), np.uint8)
+    n[:, 0::2], n[:, 1::2] = b & 15, b >> 4
+    w = n.astype(f) / f(15)
+    xf = np.asarray(x, np.int16).astype(f)
+    u, v = f(f(979200) * ps), f(f(3825) * ps)
+    su = np.asarray(s16, np.int16).reshape(rows, G).view(np.uint16)
+    sc = (su >> 8).astype(f) / f(255) * u + (su & 255).astype(f) / f(255) * v
+    mu = np.asarray(m16, np.int16).reshape(rows, G).view(np.uint16)
+    raw = (mu >> 8).astype(f) / f(255) * f(65280) + (mu & 255).astype(f) / f(255) * f(255)
+    mn = np.where(raw >= f(32767.5), raw - f(65536), raw).astype(f) * ps
+    p = (w * xf).reshape(rows, G, 4, 8)
+    e = p[..., 0]
+    for j in range(1, 8):
+        e = e + p[..., j]
+    d = e[..., 0]
+    for t in range(1, 4):
+        d = d + e[..., t]
+    # xsum is a sum of at most 32 integers of 16 bits: exact in fp32
+    xsum = xf.reshape(G, 32).astype(np.int64).sum(axis=1).astype(f)
+    term = sc * d + mn * xsum
+    s = term[:, 0]
+    for g in range(1, G):
+        s = s + term[:, g]
+    return s.astype(f)
+
+
+class _Mat4(_Mat):
+    """A q4 matrix read through the 4-bit texture view."""
+
+    def rowval(self, x):
+        ps = float(np.float32(self.scale) * np.float32(self.mul))
+        return rowval_q4_view4(self.body, self.s16, self.m16, ps, self.rows, self.cols, x)
+
+    @staticmethod
+    def of(m):
+        if m.kind != "q4":
+            return m
+        return _Mat4(m.kind, m.rows, m.cols, m.body, m.scale, m.prebiased, m.plane, m.s16, m.m16, m.mul)
+
+
+class QModelView4(QModel):
+    """QModel with the reference's default q4 path: Model::apply_q4_fmt
+    (engine/src/model.cpp:337-400) marks every q4 qkv, wo, gate, w2 chunk and
+    conv projection of a chunked-FFN model (hidden > 2048) for the 4-bit view
+    unless Q4_FMT=0; an unchunked model keeps the packed view, as QModel."""
+
+    def __init__(self, blob, seq=None, kv_bits=16):
+        super().__init__(blob, seq, kv_bits)
+        if not self.chunk:
+            return
+        self.mats = [{k: _Mat4.of(m) for k, m in L.items()} for L in self.mats]
+        self.w2ab = [(_Mat4.of(a), _Mat4.of(b)) for a, b in self.w2ab]
+
+
 class FModel(_Base):
     """The float CPU path on the dequantised container weights.
 

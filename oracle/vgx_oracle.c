@@ -396,16 +396,19 @@ void vgxo_rowval_q8_ref32(const uint8_t* body, int prebiased, int rows, int cols
     }
 }
 
-/* q4: per 32-group D = sum n*x and X = sum x are exact integers (the shader's
- * fp32 sums of these stay below 2^24); the group term
- * fl(fl(sa*D) + fl(ma*X)) is the shader's own fp32 expression; the build sums
- * the group terms in double (the shader: fp32, sequentially). */
+/* q4: the weight is n*(s16*ps) + m16*ps per 32-group (the packed view,
+ * engine/src/shaders.cpp:1784-1811), so a row value is
+ *   sum_g ps*(s16_g*D_g + m16_g*X_g),  D = sum n*x, X = sum x.
+ * The build takes the integer I = sum_g s16_g*D_g + m16_g*X_g exactly
+ * (|D| < 2^24, |X| <= 2^20, |I| < 2^47) and rounds once, (float)I * ps: the
+ * rule of q8's (float)S * wsr, and independent of the order groups are added
+ * in.  The shader's own fp32 order is vgxo_rowval_q4_ref32. */
 void vgxo_rowval_q4(const uint8_t* nib, const int16_t* s16, const int16_t* m16, float ps,
                     int rows, int cols, const int16_t* x, float* v) {
     const int groups = cols / 32;
 #pragma omp parallel for schedule(static)
     for (int r = 0; r < rows; ++r) {
-        double S = 0.0;
+        int64_t I = 0;
         for (int g = 0; g < groups; ++g) {
             int32_t D = 0, X = 0;
             const uint8_t* b = nib + (size_t)r * (cols / 2) + (size_t)g * 16;
@@ -414,13 +417,9 @@ void vgxo_rowval_q4(const uint8_t* nib, const int16_t* s16, const int16_t* m16, 
                 D += (int32_t)(b[k] & 15) * xg[2 * k] + (int32_t)(b[k] >> 4) * xg[2 * k + 1];
                 X += xg[2 * k] + xg[2 * k + 1];
             }
-            float sa = (float)s16[(size_t)r * groups + g] * ps;
-            float ma = (float)m16[(size_t)r * groups + g] * ps;
-            float t1 = sa * (float)D, t2 = ma * (float)X;
-            float t = t1 + t2;
-            S += (double)t;
+            I += (int64_t)s16[(size_t)r * groups + g] * D + (int64_t)m16[(size_t)r * groups + g] * X;
         }
-        v[r] = (float)S;
+        v[r] = (float)I * ps;
     }
 }
 

@@ -418,3 +418,43 @@ def test_gemv_bandwidth_plans(gpu, kind, rows, cols, copies, plan):
     assert np.array_equal(host(gpu.matvec(W1, dev(x), dev(res))), o.store(v, res))
     v = oracle_rowval(one, o.quantize_act(xf))
     assert np.array_equal(host(gpu.matvec_f32(W1, dev(xf))), o.store_f32(v))
+
+
+def q4_adversarial_matrix(rng, rows, cols):
+    from test_oracle_pins import q4_adversarial
+    body, s16, m16, ps, _ = q4_adversarial(rng, rows, cols)
+    return mmcf.Matrix("q4", rows, cols, body, ps, s16=s16, m16=m16)
+
+
+# q4 rows whose group terms span ~2^39 (scales of 1-3 beside scales near 2^15,
+# minima at the rails, rail and near-empty activation groups): every plan's
+# lane order, the gate, the split and the f32 entry point stay bit-exact
+@pytest.mark.parametrize("rows,cols,copies,plan", [(768, 768, 1, None), (33, 96, 1, None),
+                                                   (768, 768, 48, (8, 4)), (768, 2432, 11, (16, 4))])
+def test_q4_adversarial_groups(gpu, rows, cols, copies, plan):
+    from test_oracle_pins import q4_adversarial_x
+    rng = np.random.default_rng(rows + copies)
+    mats = [q4_adversarial_matrix(rng, rows, cols) for _ in range(copies)]
+    Ws = [gpu.upload(m) for m in mats]
+    x = q4_adversarial_x(rng, cols)
+    xf = x.astype(np.float32) / np.float32(256)  # quantize_act gives x back
+    assert np.array_equal(o.quantize_act(xf), x)
+    v = np.concatenate([oracle_rowval(m, x) for m in mats])
+    if copies > 1:
+        G = gpu.group(Ws)
+        assert G.plan() == plan
+        assert np.array_equal(host(G.gemv(dev(x))), o.store(v))
+        assert np.array_equal(host(G.gemv_f32(dev(xf))).view(np.uint32), o.store_f32(v).view(np.uint32))
+        G.free()
+        return
+    res = rand_x(rng, rows, True)
+    assert np.array_equal(host(gpu.matvec(Ws[0], dev(x), dev(res))), o.store(v, res))
+    assert np.array_equal(host(gpu.matvec_f32(Ws[0], dev(xf))).view(np.uint32), o.store_f32(v).view(np.uint32))
+    m3 = q4_adversarial_matrix(rng, rows, cols)
+    h = host(gpu.ffn_gate(Ws[0], gpu.upload(m3), dev(x), 0))
+    assert np.array_equal(h, o.gate(v, oracle_rowval(m3, x), 0))
+    split = cols // 2 // 32 * 32
+    a, b = mats[0].slice_cols(0, split), mats[0].slice_cols(split, cols)
+    y1 = o.store(oracle_rowval(a, x[:split]), res)
+    assert np.array_equal(host(gpu.matvec_add_split(Ws[0], split, dev(x), dev(res))),
+                          o.store(oracle_rowval(b, x[split:]), y1))

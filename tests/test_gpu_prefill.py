@@ -170,3 +170,27 @@ def test_batch_refusals(gpu):
     with pytest.raises(VgxError):
         A.block_batch(0, 5, dev(np.zeros((4, 256), np.int16)))  # positions 5..8 past the cache
     A.free()
+
+
+def test_gemm_q4_adversarial_groups(gpu):
+    # the q4 group terms of test_q4_adversarial_groups through the batched
+    # GEMM: plain, split and gate epilogues, bit-exact per token
+    from test_gpu_kernels import q4_adversarial_matrix
+    from test_oracle_pins import q4_adversarial_x
+    rng = np.random.default_rng(77)
+    rows, cols, ntok = 256, 768, 37
+    m, m3 = q4_adversarial_matrix(rng, rows, cols), q4_adversarial_matrix(rng, rows, cols)
+    W, W3 = gpu.upload(m), gpu.upload(m3)
+    x = np.stack([q4_adversarial_x(rng, cols) for _ in range(ntok)])
+    res = x_rows(rng, ntok, rows, full=True)
+    got = host(gpu.gemm(W, dev(x), res=dev(res)))
+    gate = host(gpu.ffn_gate_batch(W, W3, dev(x), 0))
+    split = 384
+    got_s = host(gpu.gemm_add_split(W, split, dev(x), dev(res)))
+    a, b = m.slice_cols(0, split), m.slice_cols(split, cols)
+    for t in range(ntok):
+        v = oracle_rowval(m, x[t])
+        assert np.array_equal(got[t], o.store(v, res[t])), t
+        assert np.array_equal(gate[t], o.gate(v, oracle_rowval(m3, x[t]), 0)), t
+        y1 = o.store(oracle_rowval(a, x[t, :split]), res[t])
+        assert np.array_equal(got_s[t], o.store(oracle_rowval(b, x[t, split:]), y1)), t

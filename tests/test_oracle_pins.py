@@ -165,6 +165,75 @@ def test_q4_rowval_against_dequant():
     assert np.max(np.abs(o.store(v).astype(int) - o.store(v32).astype(int))) <= 1
 
 
+def q4_adversarial(rng, rows, cols):
+    """q4 rows whose groups mix scales of 1-3 with scales near 2^15, minima at
+    the int16 rails, all-0 / all-15 nibble groups, and a full-mantissa ps:
+    per-group float terms then span ~2^39, beyond what a double sum of fp32
+    terms holds exactly."""
+    G = cols // 32
+    nib = rng.integers(0, 16, (rows, cols))
+    pat = rng.random((rows, G))
+    nib = np.where(np.repeat(pat < 0.2, 32, axis=1), 15, np.where(np.repeat(pat > 0.85, 32, axis=1), 0, nib))
+    body = (nib[:, 0::2] | (nib[:, 1::2] << 4)).astype(np.uint8).ravel()
+    s16 = np.where(rng.random((rows, G)) < 0.5, rng.integers(1, 4, (rows, G)),
+                   rng.integers(32000, 32768, (rows, G))).astype(np.int16)
+    m16 = rng.choice(np.array([-32768, -1, 0, 1, 32767]), (rows, G)).astype(np.int16)
+    ps = float(np.float32(2.0 ** -32 / 3))
+    return body, s16.ravel(), m16.ravel(), ps, q4_adversarial_x(rng, cols)
+
+
+def q4_adversarial_x(rng, cols):
+    """Full-range activations with rail groups and near-empty groups."""
+    x = rng.integers(-32768, 32768, cols).astype(np.int16)
+    xg = x.reshape(cols // 32, 32)
+    for g in range(cols // 32):
+        r = rng.random()
+        if r < 0.25:
+            xg[g] = 32767 if rng.random() < 0.5 else -32767
+        elif r < 0.4:
+            xg[g] = 0
+            xg[g, rng.integers(32)] = rng.integers(1, 4)
+    return x
+
+
+def _q4_exact_int(body, s16, m16, rows, cols, x):
+    """sum_g s16*D + m16*X per row with Python integers."""
+    G = cols // 32
+    out = []
+    for r in range(rows):
+        I = 0
+        for g in range(G):
+            D = X = 0
+            for k in range(16):
+                b = int(body[r * cols // 2 + g * 16 + k])
+                x0, x1 = int(x[g * 32 + 2 * k]), int(x[g * 32 + 2 * k + 1])
+                D += (b & 15) * x0 + (b >> 4) * x1
+                X += x0 + x1
+            I += int(s16[r * G + g]) * D + int(m16[r * G + g]) * X
+        out.append(I)
+    return out
+
+
+def test_q4_rowval_exact_and_order_free():
+    # the row value is (float)I * ps of the exact integer I: Python integers
+    # pin it, and any permutation of the groups gives the same bits
+    rng = np.random.default_rng(17)
+    rows, cols = 24, 384
+    G = cols // 32
+    body, s16, m16, ps, x = q4_adversarial(rng, rows, cols)
+    got = o.rowval_q4(body, s16, m16, ps, rows, cols, x)
+    ints = _q4_exact_int(body, s16, m16, rows, cols, x)
+    assert max(abs(I) for I in ints) < 2 ** 47
+    # |I| < 2^53: float(I) is exact, and its fp32 conversion rounds once, as (float)I
+    want = np.array([np.float32(float(I)) * np.float32(ps) for I in ints], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    perm = rng.permutation(G)
+    bp = body.reshape(rows, G, 16)[:, perm].ravel()
+    sp, mp = s16.reshape(rows, G)[:, perm].ravel(), m16.reshape(rows, G)[:, perm].ravel()
+    xp = x.reshape(G, 32)[perm].ravel()
+    assert np.array_equal(o.rowval_q4(bp, sp, mp, ps, rows, cols, xp).view(np.uint32), got.view(np.uint32))
+
+
 def test_t3_rowval_exact():
     rng = np.random.default_rng(7)
     rows, cols = 9, 64

@@ -12,7 +12,10 @@
 //   t3 : sum lv*x      = 256*sdot4(lv+1, xh) + udot4(lv+1, xl) - sum(x)
 //   q4 : sum n*x       = 256*sdot4(n, xh)    + udot4(n, xl)         (per group)
 // (lv+1 in {0,1,2} comes from a 256-entry byte -> 4 levels table in LDS.)
-// Every sum is an exact integer; the epilogue applies the reference's fp32
+// q4 folds each group's scale and minimum in as integers too,
+//   I = sum_g s16_g * D_g + m16_g * X_g   (int64, |I| < 2^47),
+// so every row value is an exact integer times one fp32 scale, whatever the
+// order the lanes add in.  The epilogue applies the reference's fp32
 // scale/round/clamp with no contraction (this file is built with
 // -ffp-contract=off).  Rows of a wave are reduced across their LPR lanes by a
 // butterfly that halves the row set per step, so RI rows cost RI-1+log2(LPR)
@@ -632,38 +635,29 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
     for (int tile = blockIdx.x;;) {
     // --- main loop
     if (KIND == VGX_Q4) {
-        double acc[RI][NV];
+        long long acc[RI][NV];
 #pragma unroll
         for (int it = 0; it < RI; ++it)
 #pragma unroll
-            for (int k = 0; k < NV; ++k) acc[it][k] = 0.0;
+            for (int k = 0; k < NV; ++k) acc[it][k] = 0;
         const float ps = M.ps;
         const float ps3 = (EPI == EPI_GATE) ? M3.ps : 0.0f;
         // one chunk c of row slot it: weights wv, scale/min word sm (and the
-        // gate's second matrix)
+        // gate's second matrix); |D| < 2^24, |X| <= 2^20
         auto q4_step = [&](int it, int c, const uint4 wv, uint32_t sm, const uint4 wv3, uint32_t sm3) {
             const uint4 xhe = lds[4 * c], xle = lds[4 * c + 1], xho = lds[4 * c + 2], xlo = lds[4 * c + 3];
-            const float Xg = (float)xg[c];
+            const int Xg = xg[c];
             const int kk = (EPI == EPI_SPLIT && c >= L.split_chunk) ? 1 : 0;
             const int D = q4_chunk(wv, xhe, xle, xho, xlo);
-            const float sa = (float)(int16_t)(sm & 0xFFFFu) * ps;
-            const float ma = (float)(int16_t)(sm >> 16) * ps;
-            const float t1 = sa * (float)D;
-            const float t2 = ma * Xg;
-            const float t = t1 + t2;
+            const long long t = (long long)(int16_t)(sm & 0xFFFFu) * D + (long long)(int16_t)(sm >> 16) * Xg;
             if (EPI == EPI_SPLIT) {
-                if (kk) acc[it][NV - 1] += (double)t; else acc[it][0] += (double)t;
+                if (kk) acc[it][NV - 1] += t; else acc[it][0] += t;
             } else {
-                acc[it][0] += (double)t;
+                acc[it][0] += t;
             }
             if (EPI == EPI_GATE) {
                 const int D3 = q4_chunk(wv3, xhe, xle, xho, xlo);
-                const float sb = (float)(int16_t)(sm3 & 0xFFFFu) * ps3;
-                const float mb = (float)(int16_t)(sm3 >> 16) * ps3;
-                const float u1 = sb * (float)D3;
-                const float u2 = mb * Xg;
-                const float u = u1 + u2;
-                acc[it][NV - 1] += (double)u;
+                acc[it][NV - 1] += (long long)(int16_t)(sm3 & 0xFFFFu) * D3 + (long long)(int16_t)(sm3 >> 16) * Xg;
             }
         };
         if (PF) {
@@ -711,11 +705,11 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
                 }
             }
         }
-        const int row_it = seg_reduce<LPR, RI, NV, double>(acc, cl);
+        const int row_it = seg_reduce<LPR, RI, NV, long long>(acc, cl);
         if ((cl % (LPR / RI > 0 ? LPR / RI : 1)) == 0) {
             const int u = unit0 + row_it * RPI + rs;
             if (u < units) {
-                const float v = (float)acc[0][0];
+                const float v = (float)acc[0][0] * ps;
                 const float rv = PF ? (float)pick(pres, row_it, 0)
                                     : (L.res ? (float)gld(L.res + M.out_off + u) : 0.0f);
                 if (EPI == EPI_STORE || EPI == EPI_STORE_ARGMAX) {
@@ -729,12 +723,12 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
                 } else if (EPI == EPI_STORE_F32) {
                     gst(static_cast<float*>(L.y) + M.out_off + u, v * (1.0f / 256.0f));
                 } else if (EPI == EPI_SPLIT) {
-                    const float vb = (float)acc[0][NV - 1];
+                    const float vb = (float)acc[0][NV - 1] * ps;
                     const float t = v + rv;
                     const float y1 = (float)q16_round(t);
                     gst(static_cast<int16_t*>(L.y) + u, (int16_t)q16_round(vb + y1));
                 } else {  // gate
-                    const float vb = (float)acc[0][NV - 1];
+                    const float vb = (float)acc[0][NV - 1] * ps3;
                     const float g = (float)q16_round(v), uu = (float)q16_round(vb);
                     const float a = g / 256.0f;
                     const float e = (float)exp(-(double)a);

@@ -27,11 +27,11 @@
 // operands straight into the matrix-core layout made every load instruction
 // touch 32 token rows 2 bytes x cols apart; on MI355X that cost up to 3.4 us
 // per 32-token launch.  Wave 0 adds the other waves' partial sums (exact
-// integers; for q4 doubles, in wave order) before the epilogue.  Epilogues
-// restate the batch-1 GEMV's fp32 expressions: q16 store (+ residual, one
-// rounding), the SwiGLU gate over W1 and W3, and the two-half residual add of
-// the split w2.  q4 applies its per-group fp32 terms after each 32-column
-// group (one MFMA k-step = one group) and sums them in double.  The RMS
+// integers) before the epilogue.  Epilogues restate the batch-1 GEMV's fp32
+// expressions: q16 store (+ residual, one rounding), the SwiGLU gate over W1
+// and W3, and the two-half residual add of the split w2.  q4 folds each
+// 32-column group's scale and minimum in after its k-step (one MFMA k-step =
+// one group) as the int64 s16*D + m16*X, and scales the total once.  The RMS
 // variants normalise the activation rows on the way into LDS, with the
 // statistics formed in the workgroup (GPU::rmsnorm's rounding).
 #include <cmath>
@@ -272,7 +272,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmLaunch G) {
     unsigned char* s_xw = s_dyn + (size_t)wave * XB;
 
     i32x16 ch[NA], cl[NA];
-    double dacc[NA][16];
+    long long dacc[NA][16];
     int wsum[NA];
 #pragma unroll
     for (int a = 0; a < NA; ++a) {
@@ -280,7 +280,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmLaunch G) {
         cl[a] = (i32x16){};
         wsum[a] = 0;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) dacc[a][r] = 0.0;
+        for (int r = 0; r < 16; ++r) dacc[a][r] = 0;
     }
     const float ps = M.ps, ps3 = G.M3.ps;
 
@@ -396,8 +396,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmLaunch G) {
                 }
             } else {
                 // one step = one 32-column group g = s: D = sum n*x exactly (|D| <
-                // 2^24), then the shader's fp32 term (s16*ps)*D + (m16*ps)*X,
-                // summed in double
+                // 2^24), then the group's exact s16*D + m16*X in int64
                 const i32x16 zero = {};
                 const int xg = xs + __shfl_xor(xs, 32, 64);  // token li's group sum
                 if (half == 0) s_xg[wave][li] = xg;
@@ -411,22 +410,17 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmLaunch G) {
 #pragma unroll
                 for (int mm = 0; mm < nmat; ++mm) {
                     const Op& wo = mm == 0 ? w : w3;
-                    const float pss = mm == 0 ? ps : ps3;
                     const i32x16 dh = mfma(xh, wo, zero);
                     const i32x16 dl = mfma(xl, wo, zero);
                     const int wl = mm == 0 ? ws : ws3;
                     const int wg = wl + __shfl_xor(wl, 32, 64);
                     const uint32_t smm = mm == 0 ? sm : sm3;
-                    const float sa = (float)(int16_t)(smm & 0xFFFFu) * pss;
-                    const float ma = (float)(int16_t)(smm >> 16) * pss;
+                    const long long sa = (int16_t)(smm & 0xFFFFu), ma = (int16_t)(smm >> 16);
                     const int slot = EPI == BEPI_GATE ? mm : side;
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int D = 256 * dh[r] + dl[r] + 128 * wg;
-                        const float t1 = sa * (float)D;
-                        const float t2 = ma * (float)X[r];
-                        const float tt = t1 + t2;
-                        dacc[slot][r] += (double)tt;
+                        dacc[slot][r] += sa * D + ma * X[r];
                     }
                 }
             }
@@ -440,12 +434,12 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmLaunch G) {
     unsigned char* s_red = s_dyn;
 
     // the waves' partial sums meet in wave 0, RC accumulator registers a
-    // round, added in wave order (exact integers; for q4 the doubles)
+    // round, added in wave order (exact integers)
 #pragma unroll
     for (int r0 = 0; r0 < 16; r0 += RC) {
         if (wave > 0) {
             if (KIND == VGX_Q4) {
-                double* p = reinterpret_cast<double*>(s_red) + (size_t)(wave - 1) * NA * RC * 64;
+                long long* p = reinterpret_cast<long long*>(s_red) + (size_t)(wave - 1) * NA * RC * 64;
 #pragma unroll
                 for (int a = 0; a < NA; ++a)
 #pragma unroll
@@ -465,7 +459,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmLaunch G) {
         if (wave == 0) {
             for (int wv = 1; wv < NW; ++wv) {
                 if (KIND == VGX_Q4) {
-                    const double* p = reinterpret_cast<const double*>(s_red) + (size_t)(wv - 1) * NA * RC * 64;
+                    const long long* p = reinterpret_cast<const long long*>(s_red) + (size_t)(wv - 1) * NA * RC * 64;
 #pragma unroll
                     for (int a = 0; a < NA; ++a)
 #pragma unroll
@@ -511,7 +505,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmLaunch G) {
 #pragma unroll
         for (int a = 0; a < NA; ++a) {
             if (KIND == VGX_Q4) {
-                v[a] = (float)dacc[a][r];
+                v[a] = (float)dacc[a][r] * ((EPI == BEPI_GATE && a == 1) ? ps3 : ps);
             } else {
                 const long long S = 256LL * ch[a][r] + (long long)cl[a][r] + 128LL * wtot[a];
                 const float sc = (EPI == BEPI_GATE && a == 1) ? wsr3 : wsr;
