@@ -204,3 +204,75 @@ def test_attention_sequences_in_lockstep(gpu, bits):
     with pytest.raises(vl.VgxError):
         A.view(nseq)
     A.free()
+
+
+def _attn_setup(gpu, rng, bits, heads, kvh, hd, seq, nseq=1, qk_norm=1):
+    dim = heads * hd
+    rc, rs = o.rope_cos_sin(10000.0, hd, seq)
+    qn = rng.uniform(0.5, 1.5, (1, hd)).astype(np.float32)
+    kn = rng.uniform(0.5, 1.5, (1, hd)).astype(np.float32)
+    A = gpu.attention(dim=dim, heads=heads, kv_heads=kvh, head_dim=hd, seq=seq, layers=1, kv_bits=bits,
+                      rope_half=1, qk_norm=qk_norm, rope_cos=rc, rope_sin=rs, q_norm=qn, k_norm=kn, nseq=nseq)
+    c = o.attn_cfg(dim, heads, kvh, hd, seq, bits, 1, qk_norm)
+    ref = (c, o.quantize_act(qn[0]) if qk_norm else None, o.quantize_act(kn[0]) if qk_norm else None,
+           o.rope_table(rc, rs))
+    return A, ref, dim + 2 * kvh * hd
+
+
+# Batches of positions through the query-block kernel (a workgroup per KV head
+# and block of 16/G positions): query heads per KV head 1, 2, 4, 8 and 32,
+# head_dim 32..256, both KV widths, blocks cut short at the batch's end, and
+# contexts of up to 24 chunks
+QBLOCK = [  # bits, heads, kv_heads, head_dim, seq, batch sizes in order from position 0
+    (8, 8, 4, 96, 768, (256, 37, 300)),
+    (16, 8, 4, 96, 320, (5, 131, 64)),
+    (16, 16, 2, 64, 512, (128, 3, 200)),
+    (8, 16, 16, 64, 96, (17, 40)),
+    (16, 4, 1, 256, 160, (33, 100)),
+    (16, 32, 1, 32, 80, (30, 20)),
+]
+
+
+@pytest.mark.parametrize("bits,heads,kvh,hd,seq,batches", QBLOCK)
+def test_query_block_batches(gpu, bits, heads, kvh, hd, seq, batches):
+    rng = np.random.default_rng(heads * 31 + hd + bits)
+    A, (c, qnq, knq, rtab), width = _attn_setup(gpu, rng, bits, heads, kvh, hd, seq)
+    kv = np.zeros(seq * o.kv_row_bytes(c), np.uint8)
+    pos = 0
+    for n in batches:
+        print("query block bits=%d heads=%d kvh=%d hd=%d rows %d..%d" % (bits, heads, kvh, hd, pos, pos + n - 1),
+              flush=True)
+        q = np.clip(rng.standard_normal((n, width)) * 700, -32768, 32767).astype(np.int16)
+        got = A.block_batch(0, pos, dev(q)).cpu().numpy()
+        for r in range(n):
+            want = o.attn_block(c, q[r], qnq, knq, rtab, pos + r, kv)
+            assert np.array_equal(got[r], want), pos + r
+        pos += n
+    assert np.array_equal(A.read_rows(0, 0, pos), kv[:pos * o.kv_row_bytes(c)])
+    A.free()
+
+
+@pytest.mark.parametrize("bits,heads,kvh,hd,seq", [(16, 16, 2, 64, 512), (8, 8, 4, 96, 768), (16, 8, 1, 128, 96)])
+def test_query_block_sequences(gpu, bits, heads, kvh, hd, seq):
+    # sequences in lockstep (each workgroup packs its KV head's row of the
+    # position, then its G query heads attend), against the oracle per sequence
+    nseq = 5
+    rng = np.random.default_rng(heads + hd + bits)
+    A, (c, qnq, knq, rtab), width = _attn_setup(gpu, rng, bits, heads, kvh, hd, seq, nseq=nseq)
+    rb = o.kv_row_bytes(c)
+    kv = [np.zeros(seq * rb, np.uint8) for _ in range(nseq)]
+    pre = min(seq - 40, 300)
+    for s in range(nseq):
+        q = np.clip(rng.standard_normal((pre, width)) * 700, -32768, 32767).astype(np.int16)
+        A.view(s).block_batch(0, 0, dev(q))
+        for r in range(pre):
+            o.attn_block(c, q[r], qnq, knq, rtab, r, kv[s])
+    for pos in list(range(pre, pre + 3)) + [seq - 2, seq - 1]:
+        print("query block sequences bits=%d hd=%d pos=%d" % (bits, hd, pos), flush=True)
+        q = np.clip(rng.standard_normal((nseq, width)) * 700, -32768, 32767).astype(np.int16)
+        out = A.block_seqs(0, pos, dev(q)).cpu().numpy()
+        for s in range(nseq):
+            assert np.array_equal(out[s], o.attn_block(c, q[s], qnq, knq, rtab, pos, kv[s])), (s, pos)
+    for s in range(nseq):
+        assert np.array_equal(A.view(s).read_rows(0, 0, seq), kv[s]), s
+    A.free()

@@ -23,6 +23,7 @@
 // different part of a row, so a head's reads straddled cache lines).
 // vgx_kv_read_rows / write_rows gather the planes into the reference's texel
 // rows (big-endian for q16) and back.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <string>
@@ -601,6 +602,415 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     }
 }
 
+// ---------------------------------------------------------------------------
+// Query-block attention: one workgroup per (KV head, slice of its query heads)
+// and block of query vectors -- the slice's heads at tq consecutive positions
+// of one sequence (batched prefill), or at one position of sequence blockIdx.z
+// (sequences in lockstep).  Each position's K row is read once per block and
+// dotted with every query vector of the block; the V rows pass through LDS in
+// rounds of whole chunks, converted to double once for all query vectors (the
+// first round's loads, and the first K rows, issue at kernel start).  The
+// statistics and the weighted V sum of each query vector follow the per-head
+// kernel step for step (the same score grid, max, exponentials, chunk sums in
+// position order, the total in chunk order, weights, per-chunk fma chains
+// added in chunk order), so every output equals the per-head kernel's bit for
+// bit.
+struct GroupArgs {
+    uint8_t* kv;
+    const int32_t* rtab;
+    const int16_t* qn;
+    const int16_t* kn;
+    const int16_t* qkv;
+    int16_t* out;
+    size_t seq_stride;  // sequences mode: bytes from one sequence's cache to the next
+    int pos0;           // batch: position of row 0; sequences: the position
+    int ntok;           // batch: rows of the batch
+    int tq;             // batch: rows (positions) per block; sequences: 1
+    int hs;             // query heads per workgroup (a divisor of the group)
+    int seqs;           // 1: blockIdx.z is the sequence, every row at pos0
+    int write;          // sequences: pack row pos0 of this KV head first
+    int fstride;        // floats per query vector's score row (nchmax chunks of 33)
+    int rc;             // chunks per V round
+    int qws;            // int words per query vector's plane (zero-padded to the lane plan)
+    int o_qh, o_ql, o_kpk, o_vpk, o_f, o_cs, o_st, o_raw, o_vt, o_part;  // LDS byte offsets
+};
+
+constexpr int kGroupPre = 4;  // 16-byte V vectors a thread stages per round (vp0..vp3)
+
+// A query vector's score row: position t at t + t/32 (one pad float per chunk,
+// so a lane per chunk reads distinct banks).
+__device__ __forceinline__ int fidx(int t) { return t + (t >> 5); }
+
+template <int KVB>
+__global__ void __launch_bounds__(kThreads) attn_group_kernel(const AttnDev A, const GroupArgs g) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int KP = kKPre<KVB>;
+    constexpr int VPV = 128 / KVB;  // V values per 16-byte vector
+    const int hd = A.hd, G = A.group, kv_dim = A.kv_heads * hd;
+    const int nsl = G / g.hs;  // head slices per KV head
+    const int kvh = blockIdx.x / nsl, h0 = kvh * G + (blockIdx.x - kvh * nsl) * g.hs;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int rbase = g.seqs ? (int)blockIdx.z : (int)blockIdx.y * g.tq;
+    const int nrow = g.seqs ? 1 : min(g.tq, g.ntok - rbase);
+    const int hs = g.hs, nq = hs * nrow;
+    uint8_t* kv = g.kv + (g.seqs ? (size_t)blockIdx.z * g.seq_stride : 0);
+    const int qrow = A.dim + 2 * kv_dim;
+    const int pfirst = g.seqs ? g.pos0 : g.pos0 + rbase;  // position of the block's row 0
+    const int npmax = pfirst + nrow;
+    uint8_t* const khead_w = kv + (size_t)kvh * A.seq * A.pstride;
+    uint8_t* const vhead_w = kv + (size_t)(A.kv_heads + kvh) * A.seq * A.pstride;
+    const uint8_t* khead = khead_w;
+    int* qhw = reinterpret_cast<int*>(smem + g.o_qh);  // [nq][qws]
+    int* qlw = reinterpret_cast<int*>(smem + g.o_ql);
+    uint8_t* kpk = smem + g.o_kpk;  // the own row's packed K / V (sequences mode)
+    uint8_t* vpk = smem + g.o_vpk;
+    float* F = reinterpret_cast<float*>(smem + g.o_f);         // [nq][fstride]
+    double* cs = reinterpret_cast<double*>(smem + g.o_cs);     // [nq][nchmax] chunk sums
+    float* st = reinterpret_cast<float*>(smem + g.o_st);       // [nq][2]: max, 1/sum
+    double* vt = reinterpret_cast<double*>(smem + g.o_vt);     // V round as doubles [rows][hd]
+    double* part = reinterpret_cast<double*>(smem + g.o_part);  // [item][rc][64*vE]
+    const bool own = g.write != 0;
+    // query vector v = j*hs + i: row j of the block, head h0 + i, position pfirst + j
+
+    // --- every global read that waits for nothing is issued first: the first
+    // V round's rows and the K rows of this thread's first scored position
+    const int nvec_row = A.pstride / 16;
+    // (four named registers: an array here is kept in scratch memory)
+    uint4 vp0, vp1, vp2, vp3;
+#define VGX_V_ROUND_LOAD(r)                                                                           \
+    do {                                                                                              \
+        const int row0_ = (r) * g.rc * kChunk, n_ = min(npmax - row0_, g.rc * kChunk) * nvec_row;     \
+        const uint4* src_ = reinterpret_cast<const uint4*>(vhead_w + (size_t)row0_ * A.pstride);      \
+        vp0 = src_[min(tid, n_ - 1)];                                                                 \
+        vp1 = src_[min(tid + kThreads, n_ - 1)];                                                      \
+        vp2 = src_[min(tid + 2 * kThreads, n_ - 1)];                                                  \
+        vp3 = src_[min(tid + 3 * kThreads, n_ - 1)];                                                  \
+    } while (0)
+    VGX_V_ROUND_LOAD(0);
+    const int nv = hd * KVB / 128;
+    const int lpp = A.lpp, sj = tid & (lpp - 1), P = kThreads / lpp;
+    uint4 kreg[KP];
+    {
+        const int t = min(tid / lpp, npmax - 1);
+        const uint4* src = reinterpret_cast<const uint4*>(khead + (size_t)t * A.pstride);
+#pragma unroll
+        for (int k = 0; k < KP; ++k) kreg[k] = src[min(sj + k * lpp, nv - 1)];
+    }
+
+    // --- the own row's KV pack (att_kv_rope), by wave 0: lane l takes elements
+    // l, l+64, ... of the KV head; the first slice's workgroup stores the row
+    if (own && wave == 0) {
+        const int16_t* kq = g.qkv + (size_t)rbase * qrow + A.dim + kvh * hd;
+        const int16_t* vq = kq + kv_dim;
+        const int32_t* rt = g.rtab + (size_t)g.pos0 * (hd / 2) * 2;
+        const int16_t* knp = A.qk_norm ? g.kn : kq;
+        const bool store = h0 == kvh * G;
+        double ssk = 0.0;
+        for (int c = 0; c < 4; ++c) {
+            const int i = lane + 64 * c;
+            const int k = i < hd ? kq[i] : 0;
+            ssk += (double)(k * k);
+        }
+        ssk = wave_sum_exact(ssk);
+        float rk = 1.0f;
+        if (A.qk_norm) {
+            const float ss = (float)ssk * (1.0f / 65536.0f);
+            rk = rsqrt_d(ss / (float)hd + 1e-6f);
+        }
+        for (int i = lane; i < hd; i += 64) {
+            int j, ti;
+            bool first;
+            rope_pair(A.rope_half, hd, i, j, ti, first);
+            const float co = (float)rt[2 * ti] / 4096.0f, sn = (float)rt[2 * ti + 1] / 4096.0f;
+            float vv = (float)kq[i] / 256.0f, bb = (float)kq[j] / 256.0f;
+            if (A.qk_norm) {
+                vv = (vv * rk) * ((float)knp[i] / 256.0f);
+                bb = (bb * rk) * ((float)knp[j] / 256.0f);
+            }
+            const float o = first ? (vv * co) - (bb * sn) : (bb * sn) + (vv * co);
+            const int q = kv_enc<KVB>(o);
+            const int qv = kv_enc<KVB>((float)vq[i] / 256.0f);
+            if (store) {
+                kv_put<KVB>(khead_w + (size_t)g.pos0 * A.pstride, i, q);
+                kv_put<KVB>(vhead_w + (size_t)g.pos0 * A.pstride, i, qv);
+            }
+            kv_put<KVB>(kpk, i, q);
+            kv_put<KVB>(vpk, i, qv);
+        }
+    }
+
+    // --- q prep (att_qnorm_scale + att_qrot), a wave per query vector; the
+    // plane words past the row stay zero, so the scores need no mask
+    for (int i = tid; i < nq * g.qws; i += kThreads) qhw[i] = qlw[i] = 0;
+    __syncthreads();
+    for (int v = wave; v < nq; v += kThreads / 64) {
+        const int j = v / hs, h = h0 + (v - j * hs), p = pfirst + j;
+        const int16_t* qh = g.qkv + (size_t)(rbase + j) * qrow + h * hd;
+        const int16_t* qnp = A.qk_norm ? g.qn : qh;
+        const int32_t* rt = g.rtab + (size_t)p * (hd / 2) * 2;
+        double ssq = 0.0;
+        for (int c = 0; c < 4; ++c) {
+            const int i = lane + 64 * c;
+            const int q = i < hd ? qh[i] : 0;
+            ssq += (double)(q * q);
+        }
+        ssq = wave_sum_exact(ssq);
+        float rq = 1.0f;
+        if (A.qk_norm) {
+            const float ss = (float)ssq * (1.0f / 65536.0f);
+            float r = rsqrt_d(ss / (float)hd + 1e-6f);
+            r = fminf(r, 127.0f);
+            rq = floorf(r * 65536.0f + 0.5f) / 65536.0f;
+        }
+        for (int i = lane; i < hd; i += 64) {
+            int jj, ti;
+            bool first;
+            rope_pair(A.rope_half, hd, i, jj, ti, first);
+            const float co = (float)rt[2 * ti] / 4096.0f, sn = (float)rt[2 * ti + 1] / 4096.0f;
+            float qv = (float)qh[i] / 256.0f, b = (float)qh[jj] / 256.0f;
+            if (A.qk_norm) {
+                qv = (qv * rq) * ((float)qnp[i] / 256.0f);
+                b = (b * rq) * ((float)qnp[jj] / 256.0f);
+            }
+            const float o = first ? (qv * co) - (b * sn) : (b * sn) + (qv * co);
+            q_split<KVB>(q16_round(o * 256.0f), i, qhw + v * g.qws, qlw + v * g.qws);
+        }
+    }
+    __syncthreads();
+
+    // --- scores (att_score): lpp lanes per position, the position's K row in
+    // registers, dotted with every query vector of the block whose position
+    // reaches it
+    {
+        const float invsqrt = 1.0f / sqrtf((float)hd);
+        const float unit = KVB == 16 ? 1.0f / 524288.0f : 1.0f / 4096.0f;
+        for (int t = tid / lpp, it = 0; t < npmax; t += P, ++it) {
+            uint4 w[KP];
+            if (it == 0) {
+#pragma unroll
+                for (int k = 0; k < KP; ++k) w[k] = kreg[k];
+            } else {
+                const uint4* src = reinterpret_cast<const uint4*>(khead + (size_t)t * A.pstride);
+#pragma unroll
+                for (int k = 0; k < KP; ++k) w[k] = src[min(sj + k * lpp, nv - 1)];
+            }
+            if (own && t == g.pos0) {
+                const uint4* o4 = reinterpret_cast<const uint4*>(kpk);
+#pragma unroll
+                for (int k = 0; k < KP; ++k) w[k] = o4[min(sj + k * lpp, nv - 1)];
+            }
+            int sk = 0;
+            if (KVB == 8) {
+#pragma unroll
+                for (int k = 0; k < KP; ++k) {
+                    const int ones = sj + k * lpp < nv ? 0x01010101 : 0;
+                    const unsigned ws[4] = {w[k].x, w[k].y, w[k].z, w[k].w};
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) sk = __builtin_amdgcn_sdot4(ones, (int)ws[u], sk, false);
+                }
+            }
+            const int j0 = max(t - pfirst, 0);  // rows j >= j0 reach position t
+            for (int v = j0 * hs; v < nq; ++v) {
+                const int4* qa4 = reinterpret_cast<const int4*>(qhw + v * g.qws) + sj;
+                const int4* qb4 = reinterpret_cast<const int4*>(qlw + v * g.qws) + sj;
+                int sh = 0, sl = 0;
+#pragma unroll
+                for (int k = 0; k < KP; ++k) {
+                    const int4 qa = qa4[k * lpp], qb = qb4[k * lpp];
+                    const unsigned ws[4] = {w[k].x, w[k].y, w[k].z, w[k].w};
+                    const int as[4] = {qa.x, qa.y, qa.z, qa.w}, bs[4] = {qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        if (KVB == 16) {
+                            sh = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, as[u]),
+                                                        __builtin_bit_cast(short2_t, ws[u]), sh, false);
+                            sl = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, bs[u]),
+                                                        __builtin_bit_cast(short2_t, ws[u]), sl, false);
+                        } else {
+                            sh = __builtin_amdgcn_sdot4(as[u], (int)ws[u], sh, false);
+                            sl = __builtin_amdgcn_sdot4(bs[u], (int)ws[u], sl, false);
+                        }
+                    }
+                }
+                long long d = 256ll * sh + sl;
+                if (KVB == 8) d += 128ll * sk;
+                for (int o = 1; o < lpp; o <<= 1) d += __shfl_xor(d, o, 64);
+                if (sj == 0) {
+                    const float s = (float)d * unit;
+                    float f = floorf((s * invsqrt) * 1024.0f + 0.5f);
+                    f = fminf(fmaxf(f, -32768.0f), 32767.0f);
+                    F[v * g.fstride + fidx(t)] = f;
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // --- stats (att_stats): the max per query vector (a wave each), the
+    // exponentials (+0.0 to the end of the last chunk), chunk sums in position
+    // order, their total in chunk order, 1/sum on its grid
+    for (int v = wave; v < nq; v += kThreads / 64) {
+        const float* Fv = F + v * g.fstride;
+        const int npos = pfirst + v / hs + 1;
+        int m = -32768;
+        for (int t = lane; t < npos; t += 64) m = max(m, (int)Fv[fidx(t)]);
+        m = wave_max(m);
+        if (lane == 0) st[2 * v] = (float)m / 1024.0f;
+    }
+    __syncthreads();
+    const int nchb = (npmax + kChunk - 1) / kChunk;
+    for (int v = 0; v < nq; ++v) {
+        float* Fv = F + v * g.fstride;
+        const int npos = pfirst + v / hs + 1, nch = (npos + kChunk - 1) / kChunk;
+        const float mx = st[2 * v];
+        for (int t = tid; t < nch * kChunk; t += kThreads)
+            Fv[fidx(t)] = t < npos ? exp_d(Fv[fidx(t)] / 1024.0f - mx) : 0.0f;
+    }
+    __syncthreads();
+    for (int i = tid; i < nq * nchb; i += kThreads) {
+        const int v = i / nchb, c = i - v * nchb;
+        if (c * kChunk > pfirst + v / hs) continue;
+        const float* Fc = F + v * g.fstride + fidx(c * kChunk);
+        double s = 0.0;
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) s += (double)Fc[k];
+        cs[v * A.nchmax + c] = s;
+    }
+    __syncthreads();
+    if (tid < nq) {
+        const int v = tid, nch = (pfirst + v / hs + 1 + kChunk - 1) / kChunk;
+        double sum = 0.0;
+        for (int c = 0; c < nch; ++c) sum += cs[v * A.nchmax + c];
+        const float fs = (float)sum;
+        float qs = floorf(fs * 32.0f + 0.5f);
+        qs = fminf(fmaxf(qs, -32768.0f), 32767.0f);
+        const float sd = qs / 32.0f;
+        st[2 * v + 1] = sd > 0.0f ? 1.0f / sd : 0.0f;
+    }
+
+    // --- weighted V (att_v): rounds of rc chunks, the V rows as doubles in
+    // LDS.  Work unit (item, chunk): item = (query vector, 64*vE elements),
+    // lane = element; the unit's fma chain runs in position order into the
+    // round's partials, then the item's owner wave adds them to its sums in
+    // chunk order.  Weight of position t: (double)(e*iv) times the V grid unit.
+    const double vunit_d = KVB == 16 ? 1.0 / 2048.0 : 1.0 / 16.0;
+    const int vE = hd > 64 ? 2 : 1;
+    const int nblk = (hd + 64 * vE - 1) / (64 * vE);
+    const int nitem = nq * nblk;
+    constexpr int kItems = 4;  // items per wave (nq * nblk <= 32)
+    double acc_a[kItems], acc_b[kItems];
+#pragma unroll
+    for (int k = 0; k < kItems; ++k) acc_a[k] = acc_b[k] = 0.0;
+    for (int r = 0; r * g.rc < nchb; ++r) {
+        const int c0 = r * g.rc, ncr = min(g.rc, nchb - c0);
+        const int row0 = c0 * kChunk, rows = min(npmax - row0, g.rc * kChunk);
+        __syncthreads();  // the stats are done / the previous round's reads are done
+        {
+            // this thread's vectors of the round into the raw tile (lanes on
+            // consecutive 16 bytes)
+            const int n = rows * nvec_row;
+            uint4* raw = reinterpret_cast<uint4*>(smem + g.o_raw);
+            if (tid < n) raw[tid] = vp0;
+            if (tid + kThreads < n) raw[tid + kThreads] = vp1;
+            if (tid + 2 * kThreads < n) raw[tid + 2 * kThreads] = vp2;
+            if (tid + 3 * kThreads < n) raw[tid + 3 * kThreads] = vp3;
+            // the own row from the LDS copy (its cache row is being written)
+            const int orow = own ? g.pos0 - row0 : -1;
+            if (orow >= 0 && orow < rows) {
+                __syncthreads();
+                if (tid < nvec_row) raw[orow * nvec_row + tid] = reinterpret_cast<const uint4*>(vpk)[tid];
+            }
+        }
+        __syncthreads();
+        {
+            // the raw tile as doubles, two elements a lane (16 consecutive
+            // bytes); rows past the block's last position to the end of the
+            // round's last chunk are zero (their weights are zero, and 0 * x
+            // must not meet a stale NaN)
+            const uint8_t* raw = smem + g.o_raw;
+            const int hh = hd / 2;
+            for (int i = tid; i < ncr * kChunk * hh; i += kThreads) {
+                const int rw = i / hh, e2 = 2 * (i - rw * hh);
+                double2 d = make_double2(0.0, 0.0);
+                if (rw < rows) {
+                    const uint8_t* src = raw + (size_t)rw * A.pstride + e2 * (KVB / 8);
+                    if (KVB == 16) {
+                        const uint32_t x = *reinterpret_cast<const uint32_t*>(src);
+                        d = make_double2((double)(int)(int16_t)(x & 0xffff), (double)((int)x >> 16));
+                    } else {
+                        const uint32_t x = *reinterpret_cast<const uint16_t*>(src);
+                        d = make_double2((double)(int)(int8_t)(x & 0xff), (double)(int)(int8_t)(x >> 8));
+                    }
+                }
+                *reinterpret_cast<double2*>(vt + (size_t)rw * hd + e2) = d;
+            }
+        }
+        __syncthreads();
+        if (c0 + g.rc < nchb) VGX_V_ROUND_LOAD(r + 1);
+        for (int unit = wave; unit < nitem * ncr; unit += kThreads / 64) {
+            const int item = unit / ncr, c = c0 + unit - item * ncr;
+            const int v = item / nblk, eb = item - v * nblk;
+            if (c * kChunk > pfirst + v / hs) continue;  // past this query's last chunk
+            const float* Fv = F + v * g.fstride;
+            const float iv = st[2 * v + 1];
+            const int ve = (eb * 64 + lane) * vE, vi = min(ve, hd - vE);
+            const double* rowp = vt + (size_t)(c - c0) * kChunk * hd + vi;
+            const double wl = (double)(Fv[fidx(c * kChunk + (lane & (kChunk - 1)))] * iv) * vunit_d;
+            double a = 0.0, b = 0.0;
+            if (vE == 2) {
+#pragma unroll
+                for (int u0 = 0; u0 < kChunk; u0 += 8) {
+                    double2 pv[8];
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) pv[k] = *reinterpret_cast<const double2*>(rowp + (u0 + k) * hd);
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        const double wu = readlane_d(wl, u0 + k);
+                        a = fma(wu, pv[k].x, a);
+                        b = fma(wu, pv[k].y, b);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int u0 = 0; u0 < kChunk; u0 += 8) {
+                    double pv[8];
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) pv[k] = rowp[(u0 + k) * hd];
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) a = fma(readlane_d(wl, u0 + k), pv[k], a);
+                }
+            }
+            double* pp = part + ((size_t)item * g.rc + (c - c0)) * 64 * vE + lane * vE;
+            pp[0] = a;
+            if (vE == 2) pp[1] = b;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < kItems; ++k) {
+            const int item = wave + k * (kThreads / 64);
+            const int nch = item < nitem ? (pfirst + (item / nblk) / hs + 1 + kChunk - 1) / kChunk : 0;
+            const double* pp = part + (size_t)item * g.rc * 64 * vE + lane * vE;
+            for (int c = c0; c < min(nch, c0 + ncr); ++c) {
+                acc_a[k] += pp[(c - c0) * 64 * vE];
+                if (vE == 2) acc_b[k] += pp[(c - c0) * 64 * vE + 1];
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kItems; ++k) {
+        const int item = wave + k * (kThreads / 64);
+        const int v = item / nblk, eb = item - v * nblk;
+        const int j = v / hs;
+        const int ve = (eb * 64 + lane) * vE;
+        if (item < nitem && ve < hd) {
+            int16_t* o = g.out + (size_t)(rbase + j) * A.dim + (h0 + v - j * hs) * hd;
+            o[ve] = (int16_t)q16_round((float)acc_a[k] * 256.0f);
+            if (vE == 2) o[ve + 1] = (int16_t)q16_round((float)acc_b[k] * 256.0f);
+        }
+    }
+#undef VGX_V_ROUND_LOAD
+}
+
 // LDS carve-up of one workgroup and the lane plan; returns the bytes used.
 size_t attn_layout(AttnDev& A) {
     const int hd = A.hd;
@@ -633,6 +1043,11 @@ size_t attn_layout(AttnDev& A) {
     return off;
 }
 
+int launch_group(vgx_attn* at, int layer, int pos, int ntok, const int16_t* qkv, int16_t* out, bool seqs);
+// Sequences in lockstep take the query-block kernel from this many query
+// heads per KV head (every head of a group then reads the K/V rows once).
+constexpr int kGroupSeqsG = 2;
+
 // Positions pos .. pos + ntok - 1 (their qkv and output rows consecutive).
 // With ntok > 1 the KV write and the attention must be separate launches: a
 // position reads the rows the others write.
@@ -659,6 +1074,12 @@ int launch(vgx_attn* at, int layer, int pos, int ntok, const int16_t* qkv, int16
     const AttnDev& A = at->a;
     const int16_t* qn = at->qn ? at->qn + (size_t)layer * A.hd : nullptr;
     const int16_t* kn = at->kn ? at->kn + (size_t)layer * A.hd : nullptr;
+    // a batch of positions, and sequences in lockstep, take the query-block
+    // kernel when a block of query vectors fits a workgroup's LDS
+    if (att && !pos_ptr && ((!seqs && !w && ntok > 1) || (seqs && w && A.group >= kGroupSeqsG))) {
+        const int st = launch_group(at, layer, pos, ntok, qkv, out, seqs);
+        if (st != VGX_ESTATE) return st;
+    }
     const dim3 grid(att ? A.heads : A.kv_heads, ntok);
     const size_t stride = seqs ? at->seq_bytes : 0;
     const int step = seqs ? 0 : 1;
@@ -669,6 +1090,100 @@ int launch(vgx_attn* at, int layer, int pos, int ntok, const int16_t* qkv, int16
         hipLaunchKernelGGL(attn_kernel<8>, grid, dim3(kThreads), at->lds, at->ctx->stream, A,
                            at->kv[layer], at->rtab, qn, kn, qkv, out, pos, w, att, stride, step, pos_ptr);
     VGX_LAUNCH_CHECK("attention launch");
+    return VGX_OK;
+}
+
+// LDS of a query-block launch of nq query vectors and rc chunks per V round;
+// fills g's offsets.
+size_t group_layout(const AttnDev& A, int nq, int rc, GroupArgs& g) {
+    const int kp = A.kv_bits == 16 ? kKPre<16> : kKPre<8>;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off = (off + bytes + 15) & ~(size_t)15;
+        return (int)o;
+    };
+    g.fstride = A.nchmax * (kChunk + 1);
+    g.rc = rc;
+    g.qws = 4 * kp * A.lpp;  // every vector slot of the lane plan, zero past the row
+    g.o_qh = take(4 * (size_t)nq * g.qws);
+    g.o_ql = take(4 * (size_t)nq * g.qws);
+    g.o_kpk = take((size_t)A.hd * A.kv_bits / 8);
+    g.o_vpk = take((size_t)A.hd * A.kv_bits / 8);
+    g.o_f = take(4 * (size_t)nq * g.fstride);
+    g.o_cs = take(8 * (size_t)nq * A.nchmax);
+    g.o_st = take(8 * (size_t)nq);
+    g.o_raw = take((size_t)rc * kChunk * A.pstride);
+    g.o_vt = take((size_t)rc * kChunk * A.hd * 8);
+    const int vE = A.hd > 64 ? 2 : 1, nblk = (A.hd + 64 * vE - 1) / (64 * vE);
+    g.o_part = take((size_t)nq * nblk * rc * 64 * vE * 8);
+    return off;
+}
+
+constexpr size_t kLdsMax = 160 * 1024;
+
+// The block plan of a query-block launch over nrow rows (batch) or nseq
+// sequences: hs query heads per workgroup, tq rows per block, rc chunks per V
+// round -- enough workgroups to cover the CUs, at most 16 query vectors a
+// block (32 work items of the V pass), a V round of at most kGroupPre vectors
+// per thread.  Returns the LDS bytes, or 0 when no plan fits.
+size_t group_plan(const AttnDev& A, bool seqs, int n, int num_cu, GroupArgs& g) {
+    const int G = A.group;
+    const int vE = A.hd > 64 ? 2 : 1, nblk = (A.hd + 64 * vE - 1) / (64 * vE);
+    const int qmax = std::min(16, 32 / nblk);
+    int hs = G;
+    while (hs > qmax && hs % 2 == 0) hs /= 2;
+    if (hs > qmax) return 0;
+    int tq = 1;
+    if (seqs) {
+        while (hs % 2 == 0 && (long)A.kv_heads * (G / hs) * n < num_cu) hs /= 2;
+    } else {
+        const int want = (int)(((long)n * A.kv_heads * (G / hs) + num_cu - 1) / num_cu);
+        tq = std::max(1, std::min({n, qmax / hs, want}));
+    }
+    // a V round: at most kGroupPre vectors per thread, at most 48 KB of doubles
+    // (one chunk at least), partials of at most 32 KB
+    const size_t per_chunk_part = (size_t)hs * tq * nblk * 64 * vE * 8;
+    int rc = (int)std::min<size_t>({(size_t)kGroupPre * kThreads * 16 / ((size_t)kChunk * A.pstride),
+                                    std::max<size_t>(1, 49152 / ((size_t)kChunk * A.hd * 8)),
+                                    std::max<size_t>(1, 32768 / per_chunk_part), (size_t)A.nchmax});
+    if (rc < 1) return 0;
+    size_t lds = group_layout(A, hs * tq, rc, g);
+    while (lds > kLdsMax && tq > 1) lds = group_layout(A, hs * --tq, rc, g);
+    while (lds > kLdsMax / 2 && rc > 1) lds = group_layout(A, hs * tq, --rc, g);
+    if (lds > kLdsMax) return 0;
+    g.hs = hs;
+    g.tq = tq;
+    return lds;
+}
+
+// The query-block kernel over rows 0..ntok-1 (positions pos .. pos+ntok-1 of
+// one sequence), or over position pos of ntok sequences (seqs: packing the
+// row first).  Returns VGX_ESTATE when no block plan fits (the caller then
+// takes the per-head kernel).
+int launch_group(vgx_attn* at, int layer, int pos, int ntok, const int16_t* qkv, int16_t* out, bool seqs) {
+    const AttnDev& A = at->a;
+    GroupArgs g{};
+    const size_t lds = group_plan(A, seqs, ntok, at->ctx->num_cu, g);
+    if (!lds) return VGX_ESTATE;
+    g.kv = at->kv[layer];
+    g.rtab = at->rtab;
+    g.qn = at->qn ? at->qn + (size_t)layer * A.hd : nullptr;
+    g.kn = at->kn ? at->kn + (size_t)layer * A.hd : nullptr;
+    g.qkv = qkv;
+    g.out = out;
+    g.seq_stride = seqs ? at->seq_bytes : 0;
+    g.pos0 = pos;
+    g.ntok = ntok;
+    g.seqs = seqs ? 1 : 0;
+    g.write = seqs ? 1 : 0;
+    const int nsl = A.group / g.hs;
+    const dim3 grid(A.kv_heads * nsl, seqs ? 1 : (ntok + g.tq - 1) / g.tq, seqs ? ntok : 1);
+    if (A.kv_bits == 16)
+        hipLaunchKernelGGL(attn_group_kernel<16>, grid, dim3(kThreads), lds, at->ctx->stream, A, g);
+    else
+        hipLaunchKernelGGL(attn_group_kernel<8>, grid, dim3(kThreads), lds, at->ctx->stream, A, g);
+    VGX_LAUNCH_CHECK("query-block attention launch");
     return VGX_OK;
 }
 
@@ -745,6 +1260,10 @@ int vgx_attn_create_seqs(vgx_ctx* ctx, const vgx_attn_desc* d, int nseq, vgx_att
         hipError_t a2 = hipFuncSetAttribute((const void*)attn_kernel<8>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)at->lds);
         if (a1 != hipSuccess) return fail(a1, "hipFuncSetAttribute");
         if (a2 != hipSuccess) return fail(a2, "hipFuncSetAttribute");
+    }
+    for (const void* k : {(const void*)attn_group_kernel<16>, (const void*)attn_group_kernel<8>}) {
+        const hipError_t a = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax);
+        if (a != hipSuccess) return fail(a, "hipFuncSetAttribute");
     }
     *out = at;
     return VGX_OK;
