@@ -194,3 +194,35 @@ def test_gemm_q4_adversarial_groups(gpu):
         assert np.array_equal(gate[t], o.gate(v, oracle_rowval(m3, x[t]), 0)), t
         y1 = o.store(oracle_rowval(a, x[t, :split]), res[t])
         assert np.array_equal(got_s[t], o.store(oracle_rowval(b, x[t, split:]), y1)), t
+
+
+# Launches of one token tile whose row tiles leave most CUs idle (the decode
+# batch) split K across workgroups: each stores its exact integer sums and an
+# epilogue kernel adds them and applies the fp32 epilogue -- every row still
+# equals the oracle's batch-1 result
+@pytest.mark.parametrize("kind,rows,cols", [("q8", 768, 2432), ("q4", 768, 2432), ("t3", 1024, 4096),
+                                            ("t3", 1280, 1024), ("q4", 1536, 768)])
+@pytest.mark.parametrize("ntok", [1, 7, 32])
+def test_split_k_decode_batch(gpu, kind, rows, cols, ntok):
+    rng = np.random.default_rng(rows + cols + ntok)
+    m = MK[kind](rng, rows, cols)
+    W = gpu.upload(m)
+    x = x_rows(rng, ntok, cols, full=True)
+    res = x_rows(rng, ntok, rows)
+    got = host(gpu.gemm(W, dev(x), res=dev(res)))
+    split = cols // 2 // 32 * 32
+    got_s = host(gpu.gemm_add_split(W, split, dev(x), dev(res)))
+    a, b = m.slice_cols(0, split), m.slice_cols(split, cols)
+    m3 = MK[kind](rng, rows, cols)
+    gate = host(gpu.ffn_gate_batch(W, gpu.upload(m3), dev(x), 2))
+    rw = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    rwq = o.quantize_act(rw)
+    got_r = host(gpu.gemm_rms(W, dev(x), dev(rwq), 1e-5))
+    for t in range(ntok):
+        v = oracle_rowval(m, x[t])
+        assert np.array_equal(got[t], o.store(v, res[t])), t
+        y1 = o.store(oracle_rowval(a, x[t, :split]), res[t])
+        assert np.array_equal(got_s[t], o.store(oracle_rowval(b, x[t, split:]), y1)), t
+        assert np.array_equal(gate[t], o.gate(v, oracle_rowval(m3, x[t]), 2)), t
+        xn = o.rmsnorm(x[t], rwq, 1e-5)
+        assert np.array_equal(got_r[t], o.store(oracle_rowval(m, xn))), t

@@ -95,6 +95,10 @@ int vgx_ctx_create(int device, vgx_ctx** out) {
 
 int vgx_ctx_destroy(vgx_ctx* ctx) {
     if (!ctx) return VGX_OK;
+    if (ctx->ws) {
+        (void)hipStreamSynchronize(ctx->stream);
+        (void)hipFree(ctx->ws);
+    }
     if (ctx->own) {
         (void)hipStreamSynchronize(ctx->own);
         (void)hipStreamDestroy(ctx->own);

@@ -5,6 +5,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -65,6 +66,11 @@ struct vgx_ctx {
     // this device's address of the library's static key-slot array (the
     // no-allocation argmax entry point), resolved once per device at create
     unsigned long long* scratch_keys = nullptr;
+    // split-K GEMM partial sums, allocated at the first launch that splits
+    // and grown on demand (freed at destroy)
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    std::mutex ws_mu;
 };
 
 struct vgx_mat {

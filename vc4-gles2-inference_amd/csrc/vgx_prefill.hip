@@ -34,7 +34,9 @@
 // one group) as the int64 s16*D + m16*X, and scales the total once.  The RMS
 // variants normalise the activation rows on the way into LDS, with the
 // statistics formed in the workgroup (GPU::rmsnorm's rounding).
+#include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <string>
 
 #include "vgx_internal.h"
@@ -62,6 +64,7 @@ struct GemmLaunch {
     int split;              // split: first column of the second half
     const int16_t* rw;      // RMS prologue: the q16 norm weight (cols values)
     float eps;              // RMS prologue: epsilon
+    long long* part;        // split K: [split][set][ntok][rows] exact partial sums
 };
 
 union Op {
@@ -238,7 +241,7 @@ __device__ __forceinline__ void rms_stats(const GemmLaunch& G, int t0, unsigned 
 // tiles; 8 when it has few (the decode batch of up to 32 sequences), so that
 // each wave walks fewer steps.  RMS: the input rows go through RMSNorm first,
 // the statistics formed in the workgroup.
-template <int KIND, int EPI, int NW, bool RMS>
+template <int KIND, int EPI, int NW, bool RMS, bool PART>
 __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmLaunch G) {
     constexpr int NT = 64 * NW;
     constexpr int NA = EPI == BEPI_STORE ? 1 : 2;  // accumulator sets: W1/W3 or the two halves
@@ -267,8 +270,12 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmLaunch G) {
     const int t = t0 + li;  // this lane's token row (A operand)
     const bool nok = n < M.rows;
     const bool tok = t < G.ntok;
+    // split K (PART): workgroup z of the launch's gridDim.z takes k-steps
+    // [zs0, zs1) and stores its exact integer sums for the epilogue kernel
     const int nsteps = (K + kTile - 1) / kTile;
-    const int s_beg = (nsteps * wave) / NW, s_end = (nsteps * (wave + 1)) / NW;
+    const int zs0 = PART ? (int)(((long)nsteps * blockIdx.z) / gridDim.z) : 0;
+    const int zs1 = PART ? (int)(((long)nsteps * (blockIdx.z + 1)) / gridDim.z) : nsteps;
+    const int s_beg = zs0 + ((zs1 - zs0) * wave) / NW, s_end = zs0 + ((zs1 - zs0) * (wave + 1)) / NW;
     unsigned char* s_xw = s_dyn + (size_t)wave * XB;
 
     i32x16 ch[NA], cl[NA];
@@ -349,6 +356,26 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmLaunch G) {
         x_load(s_beg, xn, wn);
 #pragma unroll
         for (int j = 0; j < NPF; ++j) raw_load(min(s_beg + j, s_end - 1), rb[j]);
+    }
+    // wave 0's epilogue operands (row scales, residuals), loaded before
+    // anything waits: issued at the epilogue they cost a memory round trip
+    // there
+    float wsr_e = 0.0f, wsr3_e = 0.0f;
+    int res_e[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) res_e[r] = 0;
+    if (!PART && wave == 0) {
+        if (KIND != VGX_Q4) {
+            wsr_e = M.wsr[nn];
+            if (EPI == BEPI_GATE) wsr3_e = G.M3.wsr[nn];
+        }
+        if (EPI != BEPI_GATE && G.res) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int tt = min(t0 + 8 * (r >> 2) + 4 * half + (r & 3), G.ntok - 1);
+                res_e[r] = G.res[(size_t)tt * G.ldy + nn];
+            }
+        }
     }
     if (RMS) rms_stats<NT>(G, t0, s_tot, s_inv);
     auto do_round = [&](int s0, uint4 (&xv)[8], uint4& wv, Raw* rr) {
@@ -488,16 +515,38 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmLaunch G) {
 #pragma unroll
                 for (int a = 0; a < NA; ++a) wsum[a] += s_ws[wv - 1][a][lane];
     }
-    if (wave != 0) return;
+    // the gate's epilogue spreads its exponentials over every wave (below);
+    // the others run in wave 0
+    constexpr bool GSPREAD = EPI == BEPI_GATE && !PART;
+    if (wave != 0 && !GSPREAD) return;
 
     // epilogue: this lane holds column n for 16 token rows
     int wtot[NA];
 #pragma unroll
     for (int a = 0; a < NA; ++a) wtot[a] = wsum[a] + __shfl_xor(wsum[a], 32, 64);
-    const float wsr = (KIND != VGX_Q4 && nok) ? M.wsr[n] : 0.0f;
-    const float wsr3 = (KIND != VGX_Q4 && EPI == BEPI_GATE && nok) ? G.M3.wsr[n] : 0.0f;
+    if (PART) {
+        // this split's exact sums: the q4 group sums, or 256*hi + lo + 128*sum(w)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int tt = t0 + 8 * (r >> 2) + 4 * half + (r & 3);
+            if (!nok || tt >= G.ntok) continue;
+#pragma unroll
+            for (int a = 0; a < NA; ++a) {
+                const long long S = KIND == VGX_Q4 ? dacc[a][r]
+                                                   : 256LL * ch[a][r] + (long long)cl[a][r] + 128LL * wtot[a];
+                G.part[(((size_t)blockIdx.z * NA + a) * G.ntok + tt) * M.rows + n] = S;
+            }
+        }
+        return;
+    }
+    const float wsr = nok ? wsr_e : 0.0f;
+    const float wsr3 = nok ? wsr3_e : 0.0f;
+    // gate: wave 0 leaves the tile's (W1, W3) row values in LDS, then every
+    // thread takes outputs of the tile
+    float2* gv = reinterpret_cast<float2*>(s_dyn);  // [32 tokens][32 rows]
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
+        if (GSPREAD && wave != 0) break;
         const int m = 8 * (r >> 2) + 4 * half + (r & 3);
         const int tt = t0 + m;
         if (!nok || tt >= G.ntok) continue;
@@ -514,42 +563,117 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmLaunch G) {
         }
         int16_t* yo = G.y + (size_t)tt * G.ldy + n;
         if (EPI == BEPI_STORE) {
-            const float o = G.res ? v[0] + (float)G.res[(size_t)tt * G.ldy + n] : v[0];
+            const float o = G.res ? v[0] + (float)res_e[r] : v[0];
             *yo = (int16_t)q16_round(o);
         } else if (EPI == BEPI_SPLIT) {
-            const float y1 = (float)q16_round(v[0] + (float)G.res[(size_t)tt * G.ldy + n]);
+            const float y1 = (float)q16_round(v[0] + (float)res_e[r]);
             *yo = (int16_t)q16_round(v[NA - 1] + y1);
         } else {
-            *yo = (int16_t)q16_round(gate_value(v[0], v[NA - 1], G.hs));
+            gv[m * kTile + li] = make_float2(v[0], v[NA - 1]);
         }
+    }
+    if (GSPREAD) {
+        __syncthreads();
+        for (int i = threadIdx.x; i < kTile * kTile; i += NT) {
+            const int m = i / kTile, c = i - m * kTile;
+            const int tt = t0 + m, nr = n0 + c;
+            if (tt < G.ntok && nr < M.rows)
+                G.y[(size_t)tt * G.ldy + nr] = (int16_t)q16_round(gate_value(gv[i].x, gv[i].y, G.hs));
+        }
+    }
+}
+
+// The epilogue of a split-K launch: the splits' exact sums added (in split
+// order; integers, so any order gives the same total), then the same fp32
+// epilogue as gemm_kernel's.  A thread per output row n of token blockIdx.y.
+constexpr int kMaxSplit = 8;
+
+template <int EPI>
+__global__ void __launch_bounds__(256) gemm_epi_kernel(const GemmLaunch G, int nz) {
+    constexpr int NA = EPI == BEPI_STORE ? 1 : 2;
+    const MatDev& M = G.M;
+    const int n = blockIdx.x * 256 + threadIdx.x, tt = blockIdx.y;
+    if (n >= M.rows) return;
+    float v[NA];
+#pragma unroll
+    for (int a = 0; a < NA; ++a) {
+        // every split's sum loads at once (clamped, unconditional), then adds
+        long long p[kMaxSplit];
+#pragma unroll
+        for (int z = 0; z < kMaxSplit; ++z)
+            p[z] = G.part[(((size_t)min(z, nz - 1) * NA + a) * G.ntok + tt) * M.rows + n];
+        long long S = 0;
+#pragma unroll
+        for (int z = 0; z < kMaxSplit; ++z) S += z < nz ? p[z] : 0;
+        const MatDev& Ma = (EPI == BEPI_GATE && a == 1) ? G.M3 : M;
+        v[a] = M.kind == VGX_Q4 ? (float)S * Ma.ps : (float)S * Ma.wsr[n];
+    }
+    int16_t* yo = G.y + (size_t)tt * G.ldy + n;
+    if (EPI == BEPI_STORE) {
+        const float o = G.res ? v[0] + (float)G.res[(size_t)tt * G.ldy + n] : v[0];
+        *yo = (int16_t)q16_round(o);
+    } else if (EPI == BEPI_SPLIT) {
+        const float y1 = (float)q16_round(v[0] + (float)G.res[(size_t)tt * G.ldy + n]);
+        *yo = (int16_t)q16_round(v[NA - 1] + y1);
+    } else {
+        *yo = (int16_t)q16_round(gate_value(v[0], v[NA - 1], G.hs));
     }
 }
 
 using GemmFn = void (*)(const GemmLaunch);
 
-template <int EPI, int NW, bool RMS>
+template <int EPI, int NW, bool RMS, bool PART>
 GemmFn pick_kind(int kind) {
     switch (kind) {
-        case VGX_Q8: return gemm_kernel<VGX_Q8, EPI, NW, RMS>;
-        case VGX_Q4: return gemm_kernel<VGX_Q4, EPI, NW, RMS>;
-        case VGX_T3: return gemm_kernel<VGX_T3, EPI, NW, RMS>;
+        case VGX_Q8: return gemm_kernel<VGX_Q8, EPI, NW, RMS, PART>;
+        case VGX_Q4: return gemm_kernel<VGX_Q4, EPI, NW, RMS, PART>;
+        case VGX_T3: return gemm_kernel<VGX_T3, EPI, NW, RMS, PART>;
     }
     return nullptr;
 }
 
 template <int EPI, bool RMS>
-GemmFn pick_nw(int kind, int nw) {
+GemmFn pick_nw(int kind, int nw, bool part) {
+    if (part) return nw == 4 ? pick_kind<EPI, 4, RMS, true>(kind) : nullptr;
     switch (nw) {
-        case 4: return pick_kind<EPI, 4, RMS>(kind);
-        case 8: return pick_kind<EPI, 8, RMS>(kind);
+        case 4: return pick_kind<EPI, 4, RMS, false>(kind);
+        case 8: return pick_kind<EPI, 8, RMS, false>(kind);
     }
     return nullptr;
 }
 
-GemmFn pick(int epi, int kind, int nw, bool rms) {
-    if (epi == BEPI_STORE) return rms ? pick_nw<BEPI_STORE, true>(kind, nw) : pick_nw<BEPI_STORE, false>(kind, nw);
-    if (epi == BEPI_GATE) return rms ? pick_nw<BEPI_GATE, true>(kind, nw) : pick_nw<BEPI_GATE, false>(kind, nw);
-    return rms ? nullptr : pick_nw<BEPI_SPLIT, false>(kind, nw);
+GemmFn pick(int epi, int kind, int nw, bool rms, bool part) {
+    if (epi == BEPI_STORE)
+        return rms ? pick_nw<BEPI_STORE, true>(kind, nw, part) : pick_nw<BEPI_STORE, false>(kind, nw, part);
+    if (epi == BEPI_GATE)
+        return rms ? pick_nw<BEPI_GATE, true>(kind, nw, part) : pick_nw<BEPI_GATE, false>(kind, nw, part);
+    return rms ? nullptr : pick_nw<BEPI_SPLIT, false>(kind, nw, part);
+}
+
+// Splits of K for a launch of one token tile whose row tiles leave most CUs
+// idle (the decode batch): enough workgroups to cover the CUs, at least four
+// k-steps (one per wave) a split; 1 = no split.
+int k_splits(int tiles_x, int tiles_y, int nsteps, int num_cu) {
+    if (tiles_y != 1 || tiles_x >= num_cu / 2) return 1;
+    return std::max(1, std::min({num_cu / tiles_x, nsteps / 4, kMaxSplit}));
+}
+
+// The context's split-K workspace, grown to at least `bytes`.
+int workspace(vgx_ctx* ctx, size_t bytes, long long** out) {
+    std::lock_guard<std::mutex> lock(ctx->ws_mu);
+    if (ctx->ws_bytes < bytes) {
+        if (ctx->ws) {
+            VGX_HIP(hipStreamSynchronize(ctx->stream));
+            VGX_HIP(hipFree(ctx->ws));
+            ctx->ws = nullptr;
+            ctx->ws_bytes = 0;
+        }
+        const size_t want = std::max(bytes, (size_t)8 << 20);
+        VGX_HIP(hipMalloc(&ctx->ws, want));
+        ctx->ws_bytes = want;
+    }
+    *out = static_cast<long long*>(ctx->ws);
+    return VGX_OK;
 }
 
 // Waves per workgroup: 4 when the launch has at least two tiles per CU;
@@ -587,9 +711,18 @@ int launch(vgx_ctx* ctx, const vgx_mat* W, const vgx_mat* W3, int ntok, const in
     L.split = split;
     L.rw = rw;
     L.eps = eps;
-    const dim3 grid((M.rows + kTile - 1) / kTile, (ntok + kTile - 1) / kTile);
-    const int nw = waves_for((int)(grid.x * grid.y), (M.cols + kTile - 1) / kTile, ctx->num_cu);
-    GemmFn fn = pick(epi, M.kind, nw, rw != nullptr);
+    dim3 grid((M.rows + kTile - 1) / kTile, (ntok + kTile - 1) / kTile);
+    const int nsteps = (M.cols + kTile - 1) / kTile;
+    // (the RMS variants stay whole: every split would recompute the row statistics)
+    int nz = rw ? 1 : k_splits((int)grid.x, (int)grid.y, nsteps, ctx->num_cu);
+    if (nz > 1) {
+        const int na = epi == BEPI_STORE ? 1 : 2;
+        const size_t bytes = (size_t)nz * na * ntok * M.rows * sizeof(long long);
+        if (workspace(ctx, bytes, &L.part) != VGX_OK) nz = 1;  // no workspace: one pass
+        grid.z = nz;
+    }
+    const int nw = nz > 1 ? 4 : waves_for((int)(grid.x * grid.y), nsteps, ctx->num_cu);
+    GemmFn fn = pick(epi, M.kind, nw, rw != nullptr, nz > 1);
     if (!fn) return vgx_fail(VGX_EINVAL, std::string(who) + ": unknown weight kind");
     // each wave's activation block: 32 tokens x 4 k-steps of 32 int16
     const int lds = nw * kTile * 4 * kTile * 2;
@@ -603,6 +736,13 @@ int launch(vgx_ctx* ctx, const vgx_mat* W, const vgx_mat* W3, int ntok, const in
     }
     hipLaunchKernelGGL(fn, grid, dim3(64 * nw), lds, ctx->stream, L);
     VGX_LAUNCH_CHECK("gemm launch");
+    if (nz > 1) {
+        const dim3 eg((M.rows + 255) / 256, ntok);
+        if (epi == BEPI_STORE) hipLaunchKernelGGL(gemm_epi_kernel<BEPI_STORE>, eg, dim3(256), 0, ctx->stream, L, nz);
+        else if (epi == BEPI_GATE) hipLaunchKernelGGL(gemm_epi_kernel<BEPI_GATE>, eg, dim3(256), 0, ctx->stream, L, nz);
+        else hipLaunchKernelGGL(gemm_epi_kernel<BEPI_SPLIT>, eg, dim3(256), 0, ctx->stream, L, nz);
+        VGX_LAUNCH_CHECK("gemm epilogue launch");
+    }
     return VGX_OK;
 }
 
