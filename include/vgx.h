@@ -218,7 +218,13 @@ int vgx_logits_argmax_rms_noalloc(vgx_ctx* ctx, const vgx_group* g, const int16_
  *   vgx_kv_append_batch / vgx_attn_decode_batch: positions pos0 .. pos0+ntok-1,
  *     qkv and out rows consecutive; the KV rows are written first, then every
  *     position attends to its prefix (att_stage, att_scores_batch,
- *     att_stats_row, att_v_row: engine/src/gpu_attn.cpp:433-532). */
+ *     att_stats_row, att_v_row: engine/src/gpu_attn.cpp:433-532).
+ * A vgx_gemm, vgx_gemm_add_split or vgx_ffn_gate_batch launch of at most 32
+ * tokens whose row tiles leave most CUs idle splits K over up to 8 workgroups
+ * and adds their exact integer sums in a second launch; the sums live in a
+ * workspace of the context (hipMalloc at the first such call, at least 8 MiB,
+ * grown on demand, freed by vgx_ctx_destroy).  Results are identical either
+ * way; a workspace that cannot be allocated leaves the launch whole. */
 int vgx_gemm(vgx_ctx* ctx, const vgx_mat* W, int ntok, const int16_t* x, const int16_t* res, int16_t* y);
 int vgx_gemm_add_split(vgx_ctx* ctx, const vgx_mat* W, int split, int ntok, const int16_t* x, const int16_t* res,
                        int16_t* y);

@@ -607,10 +607,10 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
 // and block of query vectors -- the slice's heads at tq consecutive positions
 // of one sequence (batched prefill), or at one position of sequence blockIdx.z
 // (sequences in lockstep).  Each position's K row is read once per block and
-// dotted with every query vector of the block; the V rows pass through LDS in
-// rounds of whole chunks, converted to double once for all query vectors (the
-// first round's loads, and the first K rows, issue at kernel start).  The
-// statistics and the weighted V sum of each query vector follow the per-head
+// dotted with every query vector of the block (the first K rows issue at kernel
+// start); the weighted V sum runs a wave per (query vector, chunk) with the V
+// values in registers.  The statistics and the weighted V sum of each query
+// vector follow the per-head
 // kernel step for step (the same score grid, max, exponentials, chunk sums in
 // position order, the total in chunk order, weights, per-chunk fma chains
 // added in chunk order), so every output equals the per-head kernel's bit for
@@ -632,10 +632,18 @@ struct GroupArgs {
     int fstride;        // floats per query vector's score row (nchmax chunks of 33)
     int rc;             // chunks per V round
     int qws;            // int words per query vector's plane (zero-padded to the lane plan)
-    int o_qh, o_ql, o_kpk, o_vpk, o_f, o_cs, o_st, o_raw, o_vt, o_part;  // LDS byte offsets
+    int o_qh, o_ql, o_kpk, o_vpk, o_f, o_cs, o_st, o_part;  // LDS byte offsets
 };
 
-constexpr int kGroupPre = 4;  // 16-byte V vectors a thread stages per round (vp0..vp3)
+// The own row's V field of elements i (and i+1 when vE is 2) from its LDS copy,
+// as v_chunk_load stores it.
+template <int KVB>
+__device__ __forceinline__ int vpk_word(const uint8_t* vpk, int vE, int i) {
+    if (vE == 2)
+        return KVB == 16 ? (int)*reinterpret_cast<const uint32_t*>(vpk + i * 2)
+                         : (int)*reinterpret_cast<const uint16_t*>(vpk + i);
+    return KVB == 16 ? (int)*reinterpret_cast<const uint16_t*>(vpk + i * 2) : (int)vpk[i];
+}
 
 // A query vector's score row: position t at t + t/32 (one pad float per chunk,
 // so a lane per chunk reads distinct banks).
@@ -667,26 +675,12 @@ __global__ void __launch_bounds__(kThreads) attn_group_kernel(const AttnDev A, c
     float* F = reinterpret_cast<float*>(smem + g.o_f);         // [nq][fstride]
     double* cs = reinterpret_cast<double*>(smem + g.o_cs);     // [nq][nchmax] chunk sums
     float* st = reinterpret_cast<float*>(smem + g.o_st);       // [nq][2]: max, 1/sum
-    double* vt = reinterpret_cast<double*>(smem + g.o_vt);     // V round as doubles [rows][hd]
     double* part = reinterpret_cast<double*>(smem + g.o_part);  // [item][rc][64*vE]
     const bool own = g.write != 0;
     // query vector v = j*hs + i: row j of the block, head h0 + i, position pfirst + j
 
-    // --- every global read that waits for nothing is issued first: the first
-    // V round's rows and the K rows of this thread's first scored position
-    const int nvec_row = A.pstride / 16;
-    // (four named registers: an array here is kept in scratch memory)
-    uint4 vp0, vp1, vp2, vp3;
-#define VGX_V_ROUND_LOAD(r)                                                                           \
-    do {                                                                                              \
-        const int row0_ = (r) * g.rc * kChunk, n_ = min(npmax - row0_, g.rc * kChunk) * nvec_row;     \
-        const uint4* src_ = reinterpret_cast<const uint4*>(vhead_w + (size_t)row0_ * A.pstride);      \
-        vp0 = src_[min(tid, n_ - 1)];                                                                 \
-        vp1 = src_[min(tid + kThreads, n_ - 1)];                                                      \
-        vp2 = src_[min(tid + 2 * kThreads, n_ - 1)];                                                  \
-        vp3 = src_[min(tid + 3 * kThreads, n_ - 1)];                                                  \
-    } while (0)
-    VGX_V_ROUND_LOAD(0);
+    // --- every global read that waits for nothing is issued first: the K rows
+    // of this thread's first scored position
     const int nv = hd * KVB / 128;
     const int lpp = A.lpp, sj = tid & (lpp - 1), P = kThreads / lpp;
     uint4 kreg[KP];
@@ -696,10 +690,21 @@ __global__ void __launch_bounds__(kThreads) attn_group_kernel(const AttnDev A, c
 #pragma unroll
         for (int k = 0; k < KP; ++k) kreg[k] = src[min(sj + k * lpp, nv - 1)];
     }
+    const int nchb = (npmax + kChunk - 1) / kChunk;
+    const int vE = hd > 64 ? 2 : 1;
+    const int nblk = (hd + 64 * vE - 1) / (64 * vE);
+    const int nitem = nq * nblk;
+    // rows 0 .. npmax-1 of the head's V plane; a row past them reads zero
+    const __amdgpu_buffer_rsrc_t vrs = rows_rsrc(vhead_w, npmax * A.pstride);
 
-    // --- the own row's KV pack (att_kv_rope), by wave 0: lane l takes elements
-    // l, l+64, ... of the KV head; the first slice's workgroup stores the row
-    if (own && wave == 0) {
+    // the query planes' words past the row stay zero, so the scores need no mask
+    for (int i = tid; i < nq * g.qws; i += kThreads) qhw[i] = qlw[i] = 0;
+    __syncthreads();
+
+    // --- the own row's KV pack (att_kv_rope), by the last wave while the first
+    // waves prepare the queries: lane l takes elements l, l+64, ... of the KV
+    // head; the first slice's workgroup stores the row
+    if (own && wave == kThreads / 64 - 1) {
         const int16_t* kq = g.qkv + (size_t)rbase * qrow + A.dim + kvh * hd;
         const int16_t* vq = kq + kv_dim;
         const int32_t* rt = g.rtab + (size_t)g.pos0 * (hd / 2) * 2;
@@ -739,10 +744,7 @@ __global__ void __launch_bounds__(kThreads) attn_group_kernel(const AttnDev A, c
         }
     }
 
-    // --- q prep (att_qnorm_scale + att_qrot), a wave per query vector; the
-    // plane words past the row stay zero, so the scores need no mask
-    for (int i = tid; i < nq * g.qws; i += kThreads) qhw[i] = qlw[i] = 0;
-    __syncthreads();
+    // --- q prep (att_qnorm_scale + att_qrot), a wave per query vector
     for (int v = wave; v < nq; v += kThreads / 64) {
         const int j = v / hs, h = h0 + (v - j * hs), p = pfirst + j;
         const int16_t* qh = g.qkv + (size_t)(rbase + j) * qrow + h * hd;
@@ -858,7 +860,6 @@ __global__ void __launch_bounds__(kThreads) attn_group_kernel(const AttnDev A, c
         if (lane == 0) st[2 * v] = (float)m / 1024.0f;
     }
     __syncthreads();
-    const int nchb = (npmax + kChunk - 1) / kChunk;
     for (int v = 0; v < nq; ++v) {
         float* Fv = F + v * g.fstride;
         const int npos = pfirst + v / hs + 1, nch = (npos + kChunk - 1) / kChunk;
@@ -888,111 +889,83 @@ __global__ void __launch_bounds__(kThreads) attn_group_kernel(const AttnDev A, c
         st[2 * v + 1] = sd > 0.0f ? 1.0f / sd : 0.0f;
     }
 
-    // --- weighted V (att_v): rounds of rc chunks, the V rows as doubles in
-    // LDS.  Work unit (item, chunk): item = (query vector, 64*vE elements),
-    // lane = element; the unit's fma chain runs in position order into the
-    // round's partials, then the item's owner wave adds them to its sums in
-    // chunk order.  Weight of position t: (double)(e*iv) times the V grid unit.
+    // --- weighted V (att_v) in rounds of rc chunks.  Work unit (item, chunk):
+    // item = (query vector, 64*vE elements), lane = element; the unit's V
+    // values come straight from the cache into registers (the next unit's
+    // loads issue before this unit's chain), its fma chain runs in position
+    // order into the round's partials, then the item's owner wave adds them
+    // to its sums in chunk order.  Weight of position t: (double)(e*iv) times
+    // the V grid unit.
     const double vunit_d = KVB == 16 ? 1.0 / 2048.0 : 1.0 / 16.0;
-    const int vE = hd > 64 ? 2 : 1;
-    const int nblk = (hd + 64 * vE - 1) / (64 * vE);
-    const int nitem = nq * nblk;
     constexpr int kItems = 4;  // items per wave (nq * nblk <= 32)
     double acc_a[kItems], acc_b[kItems];
 #pragma unroll
     for (int k = 0; k < kItems; ++k) acc_a[k] = acc_b[k] = 0.0;
+    const int vo = own ? vpk_word<KVB>(vpk, vE, min(lane * vE, hd - vE)) : 0;
     for (int r = 0; r * g.rc < nchb; ++r) {
-        const int c0 = r * g.rc, ncr = min(g.rc, nchb - c0);
-        const int row0 = c0 * kChunk, rows = min(npmax - row0, g.rc * kChunk);
-        __syncthreads();  // the stats are done / the previous round's reads are done
-        {
-            // this thread's vectors of the round into the raw tile (lanes on
-            // consecutive 16 bytes)
-            const int n = rows * nvec_row;
-            uint4* raw = reinterpret_cast<uint4*>(smem + g.o_raw);
-            if (tid < n) raw[tid] = vp0;
-            if (tid + kThreads < n) raw[tid + kThreads] = vp1;
-            if (tid + 2 * kThreads < n) raw[tid + 2 * kThreads] = vp2;
-            if (tid + 3 * kThreads < n) raw[tid + 3 * kThreads] = vp3;
-            // the own row from the LDS copy (its cache row is being written)
-            const int orow = own ? g.pos0 - row0 : -1;
-            if (orow >= 0 && orow < rows) {
-                __syncthreads();
-                if (tid < nvec_row) raw[orow * nvec_row + tid] = reinterpret_cast<const uint4*>(vpk)[tid];
+        const int c0 = r * g.rc, ncr = min(g.rc, nchb - c0), nunit = nitem * ncr;
+        __syncthreads();  // the stats are done / the previous round's partials are read
+        int vch[kChunk], vnx[kChunk];
+        auto unit_of = [&](int unit, int& item, int& c) {
+            item = unit / ncr;
+            c = c0 + unit - item * ncr;
+        };
+        int item, c;
+        unit_of(wave, item, c);
+        if (wave < nunit)
+            v_chunk_load<KVB>(A, vrs, vE, c, min(((item % nblk) * 64 + lane) * vE, hd - vE), vch);
+        for (int unit = wave; unit < nunit; unit += kThreads / 64) {
+            unit_of(unit, item, c);
+            const int nxt = unit + kThreads / 64;
+            if (nxt < nunit) {
+                int it2, c2;
+                unit_of(nxt, it2, c2);
+                v_chunk_load<KVB>(A, vrs, vE, c2, min(((it2 % nblk) * 64 + lane) * vE, hd - vE), vnx);
             }
-        }
-        __syncthreads();
-        {
-            // the raw tile as doubles, two elements a lane (16 consecutive
-            // bytes); rows past the block's last position to the end of the
-            // round's last chunk are zero (their weights are zero, and 0 * x
-            // must not meet a stale NaN)
-            const uint8_t* raw = smem + g.o_raw;
-            const int hh = hd / 2;
-            for (int i = tid; i < ncr * kChunk * hh; i += kThreads) {
-                const int rw = i / hh, e2 = 2 * (i - rw * hh);
-                double2 d = make_double2(0.0, 0.0);
-                if (rw < rows) {
-                    const uint8_t* src = raw + (size_t)rw * A.pstride + e2 * (KVB / 8);
-                    if (KVB == 16) {
-                        const uint32_t x = *reinterpret_cast<const uint32_t*>(src);
-                        d = make_double2((double)(int)(int16_t)(x & 0xffff), (double)((int)x >> 16));
-                    } else {
-                        const uint32_t x = *reinterpret_cast<const uint16_t*>(src);
-                        d = make_double2((double)(int)(int8_t)(x & 0xff), (double)(int)(int8_t)(x >> 8));
-                    }
-                }
-                *reinterpret_cast<double2*>(vt + (size_t)rw * hd + e2) = d;
-            }
-        }
-        __syncthreads();
-        if (c0 + g.rc < nchb) VGX_V_ROUND_LOAD(r + 1);
-        for (int unit = wave; unit < nitem * ncr; unit += kThreads / 64) {
-            const int item = unit / ncr, c = c0 + unit - item * ncr;
             const int v = item / nblk, eb = item - v * nblk;
-            if (c * kChunk > pfirst + v / hs) continue;  // past this query's last chunk
-            const float* Fv = F + v * g.fstride;
-            const float iv = st[2 * v + 1];
-            const int ve = (eb * 64 + lane) * vE, vi = min(ve, hd - vE);
-            const double* rowp = vt + (size_t)(c - c0) * kChunk * hd + vi;
-            const double wl = (double)(Fv[fidx(c * kChunk + (lane & (kChunk - 1)))] * iv) * vunit_d;
-            double a = 0.0, b = 0.0;
-            if (vE == 2) {
+            if (c * kChunk <= pfirst + v / hs) {  // a chunk this query reaches
+                const int ve = (eb * 64 + lane) * vE;
+                // the own row (the last position of a sequences-mode block)
+                // from the LDS copy: its cache row is being written
+                if (own && c == nchb - 1) {
+                    const int uo = npmax - 1 - c * kChunk;
+                    const int ow = eb == 0 ? vo : vpk_word<KVB>(vpk, vE, min(ve, hd - vE));
 #pragma unroll
-                for (int u0 = 0; u0 < kChunk; u0 += 8) {
-                    double2 pv[8];
+                    for (int u = 0; u < kChunk; ++u) vch[u] = u == uo ? ow : vch[u];
+                }
+                const float* Fv = F + v * g.fstride;
+                const float iv = st[2 * v + 1];
+                const double wl = (double)(Fv[fidx(c * kChunk + (lane & (kChunk - 1)))] * iv) * vunit_d;
+                double a = 0.0, b = 0.0;
+                if (vE == 2) {
 #pragma unroll
-                    for (int k = 0; k < 8; ++k) pv[k] = *reinterpret_cast<const double2*>(rowp + (u0 + k) * hd);
-#pragma unroll
-                    for (int k = 0; k < 8; ++k) {
-                        const double wu = readlane_d(wl, u0 + k);
-                        a = fma(wu, pv[k].x, a);
-                        b = fma(wu, pv[k].y, b);
+                    for (int u = 0; u < kChunk; ++u) {
+                        const double wu = readlane_d(wl, u);
+                        a = fma(wu, (double)v_lo<KVB>(vch[u]), a);
+                        b = fma(wu, (double)v_hi<KVB>(vch[u]), b);
                     }
+                } else {
+#pragma unroll
+                    for (int u = 0; u < kChunk; ++u) a = fma(readlane_d(wl, u), (double)v_lo<KVB>(vch[u]), a);
                 }
-            } else {
-#pragma unroll
-                for (int u0 = 0; u0 < kChunk; u0 += 8) {
-                    double pv[8];
-#pragma unroll
-                    for (int k = 0; k < 8; ++k) pv[k] = rowp[(u0 + k) * hd];
-#pragma unroll
-                    for (int k = 0; k < 8; ++k) a = fma(readlane_d(wl, u0 + k), pv[k], a);
-                }
+                double* pp = part + ((size_t)item * g.rc + (c - c0)) * 64 * vE + lane * vE;
+                pp[0] = a;
+                if (vE == 2) pp[1] = b;
             }
-            double* pp = part + ((size_t)item * g.rc + (c - c0)) * 64 * vE + lane * vE;
-            pp[0] = a;
-            if (vE == 2) pp[1] = b;
+            if (nxt < nunit) {
+#pragma unroll
+                for (int u = 0; u < kChunk; ++u) vch[u] = vnx[u];
+            }
         }
         __syncthreads();
 #pragma unroll
         for (int k = 0; k < kItems; ++k) {
-            const int item = wave + k * (kThreads / 64);
-            const int nch = item < nitem ? (pfirst + (item / nblk) / hs + 1 + kChunk - 1) / kChunk : 0;
-            const double* pp = part + (size_t)item * g.rc * 64 * vE + lane * vE;
-            for (int c = c0; c < min(nch, c0 + ncr); ++c) {
-                acc_a[k] += pp[(c - c0) * 64 * vE];
-                if (vE == 2) acc_b[k] += pp[(c - c0) * 64 * vE + 1];
+            const int it = wave + k * (kThreads / 64);
+            const int nch = it < nitem ? (pfirst + (it / nblk) / hs + 1 + kChunk - 1) / kChunk : 0;
+            const double* pp = part + (size_t)it * g.rc * 64 * vE + lane * vE;
+            for (int cc = c0; cc < min(nch, c0 + ncr); ++cc) {
+                acc_a[k] += pp[(cc - c0) * 64 * vE];
+                if (vE == 2) acc_b[k] += pp[(cc - c0) * 64 * vE + 1];
             }
         }
     }
@@ -1008,7 +981,6 @@ __global__ void __launch_bounds__(kThreads) attn_group_kernel(const AttnDev A, c
             if (vE == 2) o[ve + 1] = (int16_t)q16_round((float)acc_b[k] * 256.0f);
         }
     }
-#undef VGX_V_ROUND_LOAD
 }
 
 // LDS carve-up of one workgroup and the lane plan; returns the bytes used.
@@ -1113,8 +1085,6 @@ size_t group_layout(const AttnDev& A, int nq, int rc, GroupArgs& g) {
     g.o_f = take(4 * (size_t)nq * g.fstride);
     g.o_cs = take(8 * (size_t)nq * A.nchmax);
     g.o_st = take(8 * (size_t)nq);
-    g.o_raw = take((size_t)rc * kChunk * A.pstride);
-    g.o_vt = take((size_t)rc * kChunk * A.hd * 8);
     const int vE = A.hd > 64 ? 2 : 1, nblk = (A.hd + 64 * vE - 1) / (64 * vE);
     g.o_part = take((size_t)nq * nblk * rc * 64 * vE * 8);
     return off;
@@ -1141,13 +1111,9 @@ size_t group_plan(const AttnDev& A, bool seqs, int n, int num_cu, GroupArgs& g) 
         const int want = (int)(((long)n * A.kv_heads * (G / hs) + num_cu - 1) / num_cu);
         tq = std::max(1, std::min({n, qmax / hs, want}));
     }
-    // a V round: at most kGroupPre vectors per thread, at most 48 KB of doubles
-    // (one chunk at least), partials of at most 32 KB
+    // a V round: partials of at most 32 KB (one chunk at least)
     const size_t per_chunk_part = (size_t)hs * tq * nblk * 64 * vE * 8;
-    int rc = (int)std::min<size_t>({(size_t)kGroupPre * kThreads * 16 / ((size_t)kChunk * A.pstride),
-                                    std::max<size_t>(1, 49152 / ((size_t)kChunk * A.hd * 8)),
-                                    std::max<size_t>(1, 32768 / per_chunk_part), (size_t)A.nchmax});
-    if (rc < 1) return 0;
+    int rc = (int)std::min<size_t>(std::max<size_t>(1, 32768 / per_chunk_part), (size_t)A.nchmax);
     size_t lds = group_layout(A, hs * tq, rc, g);
     while (lds > kLdsMax && tq > 1) lds = group_layout(A, hs * --tq, rc, g);
     while (lds > kLdsMax / 2 && rc > 1) lds = group_layout(A, hs * tq, --rc, g);
