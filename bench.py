@@ -345,23 +345,33 @@ def prefill_bench(runs):
             "gemm_int8_peak_TOPS": INT8_PEAK_TOPS, "gemms": gemms}
 
 
-def decode_cpu_baseline(blob, prompt, steps):
-    """The float CPU path for `steps` positions: the reference's float forward
-    on the dequantised container weights (oracle/model.py FModel semantics),
-    run by the C/OpenMP float path (oracle/vgx_float.c), on every host core
-    this process may use and on one."""
+def decode_cpu_baseline(blob, prompt, n_gen):
+    """The float CPU path over the GPU leg's own positions: the prompt, then
+    greedy steps on its own argmax, timed over the n_gen - 1 steps after the
+    first generated token, as the GPU leg is -- the
+    reference's float forward on the dequantised container weights
+    (oracle/model.py FModel semantics) run by the C/OpenMP float path
+    (oracle/vgx_float.c), on every host core this process may use and on one."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
     from model import CFModel, float_lib
 
     f = CFModel(blob)
     lib = float_lib()
     cores = lib.vgxf_threads()
+    n_prompt = len(prompt)
 
     def rate():
+        logits = None
+        for pos in range(n_prompt):
+            logits = f.step(int(prompt[pos]), pos)
+        # the first generated token comes from the prompt's last logits; the
+        # GPU leg times the n_gen - 1 steps after it, and so does this
+        tok = int(np.argmax(logits))
         t0 = time.perf_counter()
-        for pos in range(steps):
-            f.step(int(prompt[pos % len(prompt)]), pos)
-        return steps / (time.perf_counter() - t0)
+        for pos in range(n_prompt, n_prompt + n_gen - 1):
+            tok = int(np.argmax(f.step(tok, pos)))
+        return (n_gen - 1) / (time.perf_counter() - t0)
 
     rate()  # first touch of the weights
     all_cores = rate()
@@ -369,8 +379,9 @@ def decode_cpu_baseline(blob, prompt, steps):
     one = rate()
     lib.vgxf_set_threads(cores)
     return {"tokens_per_s": round(all_cores, 2), "cores": cores, "one_core_tokens_per_s": round(one, 2),
-            "sample": "%d positions from 0 of the float path (C, fp32 FMA dot products, OpenMP over rows, "
-                      "dequantised container weights)" % steps}
+            "sample": "the GPU leg's positions: a %d-token prompt, then the %d greedy steps after the first "
+                      "token timed (C, fp32 FMA dot products, OpenMP over rows, dequantised container weights)"
+                      % (n_prompt, n_gen - 1)}
 
 
 def main():
@@ -386,7 +397,6 @@ def main():
     ap.add_argument("--skip-decode", action="store_true")
     ap.add_argument("--copy-mb", type=int, default=0, help="also time a device copy of this many MiB")
     ap.add_argument("--skip-stream-ref", action="store_true", help="skip the library read/copy bandwidth reference")
-    ap.add_argument("--cpu-decode-steps", type=int, default=32)
     ap.add_argument("--only", choices=["gemv", "decode", "prefill", "hybrid", "ternary", "ternary32", "attention"],
                     default=None,
                     help="run one leg (for profiling); the JSON line then carries that leg only")
@@ -572,17 +582,17 @@ def main():
         out["attention_c3"] = attention_bench()
     others = []
     if not args.skip_models:
-        others = [("decode_c4", hybrid_decode_bench(args.decode_runs), 16),
-                  ("decode_c5_batch1", ternary_decode_bench(args.decode_runs), 8)]
-        for key, (_b, _p, _t, res), _n in others:
+        others = [("decode_c4", hybrid_decode_bench(args.decode_runs)),
+                  ("decode_c5_batch1", ternary_decode_bench(args.decode_runs))]
+        for key, (_b, _p, _t, res) in others:
             out[key] = res
         out["decode_c5_batch32"] = ternary_batch_bench(max(1, args.decode_runs // 2))
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
         if not args.skip_decode:
-            out["decode"]["cpu_float_path"] = decode_cpu_baseline(blob, prompt, args.cpu_decode_steps)
-        for key, (b, p, _t, _r), n in others:
-            out[key]["cpu_float_path"] = decode_cpu_baseline(b, p, n)
+            out["decode"]["cpu_float_path"] = decode_cpu_baseline(blob, prompt, out["decode"]["gen"])
+        for key, (b, p, _t, r) in others:
+            out[key]["cpu_float_path"] = decode_cpu_baseline(b, p, r["gen"])
     print(json.dumps(out))
 
 
