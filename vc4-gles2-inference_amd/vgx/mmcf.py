@@ -94,22 +94,35 @@ def q4mat(w):
     return packed, s16, m16, ps, groups
 
 
+def _t3_byte_index(rows, cols):
+    """Byte of weight (r, c) in the texel grid and its bit shift, from the
+    container's texel formula (docs/checkpoint-container.md, "t3"): texel
+    (c8, t) is 4 bytes at t*stride + 4*c8; row 2t's columns 8c8..8c8+3 are
+    byte 0, 8c8+4..8c8+7 byte 1, row 2t+1 the same in bytes 2 and 3; weight k
+    of a byte sits at bits 2k."""
+    stride = (cols // 8) * 4
+    r = np.arange(rows)[:, None]
+    c = np.arange(cols)[None, :]
+    byte = (r // 2) * stride + (c // 8) * 4 + (r % 2) * 2 + (c // 4) % 2
+    return byte, 2 * (c % 4)
+
+
 def t3_codes_pack(code):
     """(rows, cols) 2-bit codes, rows even and cols a multiple of 8 -> the texel
-    grid: texel (c, t) = row 2t cols 8c..8c+3, 8c+4..8c+7, then row 2t+1."""
+    grid bytes, (rows/2, cols/2) per texel row."""
     rows, cols = code.shape
-    q = code.reshape(rows // 2, 2, cols // 8, 2, 4).astype(np.uint8)
-    b = q[..., 0] | (q[..., 1] << 2) | (q[..., 2] << 4) | (q[..., 3] << 6)
-    return b.transpose(0, 2, 1, 3).reshape(rows // 2, -1).astype(np.uint8)
+    byte, shift = _t3_byte_index(rows, cols)
+    out = np.zeros((rows // 2) * (cols // 8) * 4, np.uint8)
+    for k in range(4):  # each byte holds one weight of each column phase k
+        out[byte[:, k::4].ravel()] |= ((code[:, k::4].astype(np.uint8) & 3) << (2 * k)).ravel()
+    return out.reshape(rows // 2, -1)
 
 
 def t3_codes_unpack(block, rows, cols):
     rpad, cpad = rows + (rows % 2), cols + ((-cols) % 8)
-    b = np.frombuffer(bytes(block), np.uint8).reshape(rpad // 2, cpad // 8, 2, 2).transpose(0, 2, 1, 3)
-    out = np.empty((rpad // 2, 2, cpad // 8, 2, 4), np.uint8)
-    for k in range(4):
-        out[..., k] = (b >> (2 * k)) & 3
-    return out.reshape(rpad, cpad)[:rows, :cols]
+    body = np.frombuffer(bytes(block), np.uint8)
+    byte, shift = _t3_byte_index(rpad, cpad)
+    return ((body[byte] >> shift) & 3).astype(np.uint8)[:rows, :cols]
 
 
 def t3_levels(codes):
