@@ -244,6 +244,21 @@ int vgx_ffn_gate_batch_rms(vgx_ctx* ctx, const vgx_mat* W1, const vgx_mat* W3, i
                            const int16_t* rms_w, float eps, int hs, int16_t* h);
 int vgx_embed_q8_batch(vgx_ctx* ctx, const int8_t* emb, const float* emb_scale, int vocab, int dim, int ntok,
                        const int* tokens, int16_t* x);
+/* The other side of the same fusion: a GEMM that writes the residual stream
+ * also normalises the rows it wrote, per token,
+ *   vgx_gemm_norm            vgx_gemm, then vgx_rmsnorm_batch(y, rms_w, eps) -> yn
+ *   vgx_gemm_add_split_norm  vgx_gemm_add_split, then the same
+ * with identical bytes in y and yn.  For the decode of a batch of sequences:
+ * in Session::forward_gpu_hidden, the wo residual and the FFN norm
+ * (engine/src/session.cpp:1508-1516), the w2 residual (:1572) and the next
+ * layer's attention norm (:1483) or the final norm (:1580), so the GEMM that
+ * reads yn needs no norm of its own.  A launch whose K is split adds the RMSNorm to its
+ * epilogue launch (one workgroup per token row); otherwise it is a launch of
+ * its own.  rms_w: W's rows q16 values; yn: ntok rows of W's rows values. */
+int vgx_gemm_norm(vgx_ctx* ctx, const vgx_mat* W, int ntok, const int16_t* x, const int16_t* res, int16_t* y,
+                  const int16_t* rms_w, float eps, int16_t* yn);
+int vgx_gemm_add_split_norm(vgx_ctx* ctx, const vgx_mat* W, int split, int ntok, const int16_t* x,
+                            const int16_t* res, int16_t* y, const int16_t* rms_w, float eps, int16_t* yn);
 
 /* One matrix holding the rows of n q8 or t3 matrices of equal cols, in order
  * (the LM head tiles as a single operand of vgx_gemm, for batched decode);

@@ -226,3 +226,30 @@ def test_split_k_decode_batch(gpu, kind, rows, cols, ntok):
         assert np.array_equal(gate[t], o.gate(v, oracle_rowval(m3, x[t]), 2)), t
         xn = o.rmsnorm(x[t], rwq, 1e-5)
         assert np.array_equal(got_r[t], o.store(oracle_rowval(m, xn))), t
+
+
+@pytest.mark.parametrize("kind,rows,cols", [("t3", 1024, 1024), ("q8", 768, 2432), ("q4", 768, 768)])
+@pytest.mark.parametrize("ntok", [1, 32, 40])
+def test_gemm_norm_equals_gemm_then_rmsnorm(gpu, kind, rows, cols, ntok):
+    # the GEMM that writes the residual stream and the RMSNorm of its rows:
+    # in the split-K epilogue launch (32 rows or fewer) or as a launch of its
+    # own (40), the same bytes as vgx_gemm / vgx_gemm_add_split then
+    # vgx_rmsnorm_batch, and the oracle's rows
+    rng = np.random.default_rng(rows + ntok)
+    m = MK[kind](rng, rows, cols)
+    W = gpu.upload(m)
+    x = x_rows(rng, ntok, cols, full=True)
+    res = x_rows(rng, ntok, rows)
+    nw = o.quantize_act(rng.uniform(0.5, 1.5, rows).astype(np.float32))
+    split = cols // 2 // 32 * 32
+    for sp in (0, split):
+        y, yn = gpu.gemm_norm(W, dev(x), dev(res), dev(nw), 1e-5, split=sp)
+        y, yn = host(y), host(yn)
+        if sp:
+            want_y = host(gpu.gemm_add_split(W, sp, dev(x), dev(res)))
+        else:
+            want_y = host(gpu.gemm(W, dev(x), res=dev(res)))
+        assert np.array_equal(y, want_y), sp
+        assert np.array_equal(yn, host(gpu.rmsnorm_batch(dev(y), dev(nw), 1e-5))), sp
+        for t in range(min(ntok, 4)):
+            assert np.array_equal(yn[t], o.rmsnorm(y[t], nw, 1e-5)), (sp, t)

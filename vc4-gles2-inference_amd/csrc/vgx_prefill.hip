@@ -588,12 +588,13 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmLaunch G) {
 // epilogue as gemm_kernel's.  A thread per output row n of token blockIdx.y.
 constexpr int kMaxSplit = 8;
 
+// Output row n of token tt of a split-K launch: the splits' exact sums added
+// (integers: any order gives the same total), then gemm_kernel's fp32
+// epilogue.
 template <int EPI>
-__global__ void __launch_bounds__(256) gemm_epi_kernel(const GemmLaunch G, int nz) {
+__device__ __forceinline__ int16_t epi_value(const GemmLaunch& G, int nz, int tt, int n) {
     constexpr int NA = EPI == BEPI_STORE ? 1 : 2;
     const MatDev& M = G.M;
-    const int n = blockIdx.x * 256 + threadIdx.x, tt = blockIdx.y;
-    if (n >= M.rows) return;
     float v[NA];
 #pragma unroll
     for (int a = 0; a < NA; ++a) {
@@ -608,16 +609,67 @@ __global__ void __launch_bounds__(256) gemm_epi_kernel(const GemmLaunch G, int n
         const MatDev& Ma = (EPI == BEPI_GATE && a == 1) ? G.M3 : M;
         v[a] = M.kind == VGX_Q4 ? (float)S * Ma.ps : (float)S * Ma.wsr[n];
     }
-    int16_t* yo = G.y + (size_t)tt * G.ldy + n;
     if (EPI == BEPI_STORE) {
         const float o = G.res ? v[0] + (float)G.res[(size_t)tt * G.ldy + n] : v[0];
-        *yo = (int16_t)q16_round(o);
+        return (int16_t)q16_round(o);
     } else if (EPI == BEPI_SPLIT) {
         const float y1 = (float)q16_round(v[0] + (float)G.res[(size_t)tt * G.ldy + n]);
-        *yo = (int16_t)q16_round(v[NA - 1] + y1);
-    } else {
-        *yo = (int16_t)q16_round(gate_value(v[0], v[NA - 1], G.hs));
+        return (int16_t)q16_round(v[NA - 1] + y1);
     }
+    return (int16_t)q16_round(gate_value(v[0], v[NA - 1], G.hs));
+}
+
+// The epilogue of a split-K launch: a thread per output row n of token
+// blockIdx.y.
+template <int EPI>
+__global__ void __launch_bounds__(256) gemm_epi_kernel(const GemmLaunch G, int nz) {
+    const int n = blockIdx.x * 256 + threadIdx.x, tt = blockIdx.y;
+    if (n >= G.M.rows) return;
+    G.y[(size_t)tt * G.ldy + n] = epi_value<EPI>(G, nz, tt, n);
+}
+
+// The same epilogue for a whole token row per workgroup, followed by the
+// RMSNorm of the row it wrote (rmsnorm_kernel's arithmetic: 32 partial sums
+// of x^2 over contiguous slices of ceil(rows/32), each floor(P/16 + 1/2),
+// then (x * inv) * w on the q16 grid) into yn.  The row is kept in LDS.
+constexpr int kNormThreads = 1024;  // a row of up to 1024 values: one value a thread
+
+template <int EPI>
+__global__ void __launch_bounds__(kNormThreads) gemm_epi_norm_kernel(const GemmLaunch G, int nz, const int16_t* nw,
+                                                                     float neps, int16_t* yn) {
+    extern __shared__ __align__(16) unsigned char s_dyn[];
+    int16_t* row = reinterpret_cast<int16_t*>(s_dyn);
+    __shared__ long long part[32];
+    __shared__ float s_inv;
+    const int tt = blockIdx.x, rows = G.M.rows, tid = threadIdx.x;
+    for (int n = tid; n < rows; n += kNormThreads) {
+        const int16_t q = epi_value<EPI>(G, nz, tt, n);
+        G.y[(size_t)tt * G.ldy + n] = q;
+        row[n] = q;
+    }
+    __syncthreads();
+    const int per = (rows + 31) / 32;
+    if (tid < 256) {  // 8 threads a partial slice
+        const int p = tid >> 3, sub = tid & 7;
+        long long P = 0;
+        for (int k = sub; k < per; k += 8) {
+            const int i = p * per + k;
+            if (i < rows) P += (long long)row[i] * row[i];
+        }
+        for (int o = 4; o >= 1; o >>= 1) P += __shfl_xor(P, o, 64);
+        if (sub == 0) part[p] = (P + 8) >> 4;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        long long tot = 0;
+        for (int p = 0; p < 32; ++p) tot += part[p];
+        const float ss = (float)tot / 4096.0f;
+        s_inv = (float)(1.0 / sqrt((double)(ss / (float)rows + neps)));
+    }
+    __syncthreads();
+    const float inv = s_inv;
+    for (int i = tid; i < rows; i += kNormThreads)
+        yn[(size_t)tt * rows + i] = (int16_t)rms_elem((uint16_t)row[i], (uint16_t)nw[i], inv);
 }
 
 using GemmFn = void (*)(const GemmLaunch);
@@ -687,8 +739,11 @@ int waves_for(int tiles, int nsteps, int num_cu) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// nrm_w / neps / yn: also the RMSNorm of the rows written (y's rows, W's rows
+// wide) into yn, in the split-K epilogue launch or as a launch of its own.
 int launch(vgx_ctx* ctx, const vgx_mat* W, const vgx_mat* W3, int ntok, const int16_t* x, const int16_t* res,
-           int16_t* y, int epi, int hs, int split, const char* who, const int16_t* rw = nullptr, float eps = 0.0f) {
+           int16_t* y, int epi, int hs, int split, const char* who, const int16_t* rw = nullptr, float eps = 0.0f,
+           const int16_t* nrm_w = nullptr, float neps = 0.0f, int16_t* yn = nullptr) {
     if (!ctx || !W || !x || !y) return vgx_fail(VGX_EINVAL, std::string(who) + ": NULL argument");
     if (ntok <= 0 || ntok > 65535 * kTile) return vgx_fail(VGX_EINVAL, std::string(who) + ": ntok outside 1..2097120");
     if (!aligned16(x)) return vgx_fail(VGX_EINVAL, std::string(who) + ": x must be 16-byte aligned");
@@ -736,6 +791,18 @@ int launch(vgx_ctx* ctx, const vgx_mat* W, const vgx_mat* W3, int ntok, const in
     }
     hipLaunchKernelGGL(fn, grid, dim3(64 * nw), lds, ctx->stream, L);
     VGX_LAUNCH_CHECK("gemm launch");
+    const bool norm_rows = yn && M.rows * 2 <= 64 * 1024;  // the row fits the epilogue's LDS
+    if (nz > 1 && yn && norm_rows) {
+        const size_t rl = (size_t)M.rows * 2;
+        if (epi == BEPI_STORE)
+            hipLaunchKernelGGL(gemm_epi_norm_kernel<BEPI_STORE>, dim3(ntok), dim3(kNormThreads), rl, ctx->stream, L,
+                               nz, nrm_w, neps, yn);
+        else
+            hipLaunchKernelGGL(gemm_epi_norm_kernel<BEPI_SPLIT>, dim3(ntok), dim3(kNormThreads), rl, ctx->stream, L,
+                               nz, nrm_w, neps, yn);
+        VGX_LAUNCH_CHECK("gemm epilogue launch");
+        return VGX_OK;
+    }
     if (nz > 1) {
         const dim3 eg((M.rows + 255) / 256, ntok);
         if (epi == BEPI_STORE) hipLaunchKernelGGL(gemm_epi_kernel<BEPI_STORE>, eg, dim3(256), 0, ctx->stream, L, nz);
@@ -743,6 +810,7 @@ int launch(vgx_ctx* ctx, const vgx_mat* W, const vgx_mat* W3, int ntok, const in
         else hipLaunchKernelGGL(gemm_epi_kernel<BEPI_SPLIT>, eg, dim3(256), 0, ctx->stream, L, nz);
         VGX_LAUNCH_CHECK("gemm epilogue launch");
     }
+    if (yn) return vgx_rmsnorm_batch(ctx, ntok, M.rows, y, nrm_w, neps, yn);
     return VGX_OK;
 }
 
@@ -762,6 +830,25 @@ int vgx_gemm_add_split(vgx_ctx* ctx, const vgx_mat* W, int split, int ntok, cons
         return vgx_fail(VGX_EINVAL, "vgx_gemm_add_split: split must be inside cols and a multiple of " +
                                         std::to_string(unit));
     return launch(ctx, W, nullptr, ntok, x, res, y, BEPI_SPLIT, 0, split, "vgx_gemm_add_split");
+}
+
+int vgx_gemm_norm(vgx_ctx* ctx, const vgx_mat* W, int ntok, const int16_t* x, const int16_t* res, int16_t* y,
+                  const int16_t* rms_w, float eps, int16_t* yn) {
+    if (!rms_w || !yn) return vgx_fail(VGX_EINVAL, "vgx_gemm_norm: NULL RMSNorm weight or output");
+    if (!(eps > 0.0f)) return vgx_fail(VGX_EINVAL, "vgx_gemm_norm: the RMSNorm epsilon must be positive");
+    return launch(ctx, W, nullptr, ntok, x, res, y, BEPI_STORE, 0, 0, "vgx_gemm_norm", nullptr, 0.0f, rms_w, eps, yn);
+}
+
+int vgx_gemm_add_split_norm(vgx_ctx* ctx, const vgx_mat* W, int split, int ntok, const int16_t* x,
+                            const int16_t* res, int16_t* y, const int16_t* rms_w, float eps, int16_t* yn) {
+    if (!W || !res || !rms_w || !yn) return vgx_fail(VGX_EINVAL, "vgx_gemm_add_split_norm: NULL argument");
+    if (!(eps > 0.0f)) return vgx_fail(VGX_EINVAL, "vgx_gemm_add_split_norm: the RMSNorm epsilon must be positive");
+    const int unit = W->d.kind == VGX_Q8 ? 16 : 32;
+    if (split <= 0 || split >= W->d.cols || split % unit)
+        return vgx_fail(VGX_EINVAL, "vgx_gemm_add_split_norm: split must be inside cols and a multiple of " +
+                                        std::to_string(unit));
+    return launch(ctx, W, nullptr, ntok, x, res, y, BEPI_SPLIT, 0, split, "vgx_gemm_add_split_norm", nullptr, 0.0f,
+                  rms_w, eps, yn);
 }
 
 int vgx_gemm_rms(vgx_ctx* ctx, const vgx_mat* W, int ntok, const int16_t* x, const int16_t* rms_w, float eps,

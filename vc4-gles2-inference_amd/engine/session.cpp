@@ -497,20 +497,25 @@ struct vgx_engine {
         const int D = m.dim;
         const float eps = m.rms_eps;
         if ((st = vgx_embed_q8_batch(ctx, emb, emb_scale, m.vocab, D, nseq, toks_dev, bh))) return st;
+        // the first attention norm; every later norm comes out of the GEMM that
+        // writes the residual stream (wo: the FFN norm; w2: the next layer's
+        // attention norm, or the final norm after the last layer), so qkv, the
+        // gate and the head read normalised rows
+        if ((st = vgx_rmsnorm_batch(ctx, nseq, D, bh, L[0].rms_att, eps, bxn))) return st;
         for (int l = 0; l < m.layers; ++l) {
             Layer& ly = L[l];
-            if ((st = vgx_gemm_rms(ctx, ly.qkv, nseq, bh, ly.rms_att, eps, nullptr, bqkv))) return st;
+            const int16_t* next_norm = l + 1 < m.layers ? L[l + 1].rms_att : rms_final;
+            if ((st = vgx_gemm(ctx, ly.qkv, nseq, bxn, nullptr, bqkv))) return st;
             if ((st = vgx_attn_block_seqs(attn_b, l, pos, nseq, bqkv, batt))) return st;
-            if ((st = vgx_gemm(ctx, ly.wo, nseq, batt, bh, bx1))) return st;
-            if ((st = vgx_ffn_gate_batch_rms(ctx, ly.w1, ly.w3, nseq, bx1, ly.rms_ffn, eps, ly.hs, bhid))) return st;
-            if (ffn_chunk) st = vgx_gemm_add_split(ctx, ly.w2, ffn_chunk, nseq, bhid, bx1, bh);
-            else st = vgx_gemm(ctx, ly.w2, nseq, bhid, bx1, bh);
+            if ((st = vgx_gemm_norm(ctx, ly.wo, nseq, batt, bh, bx1, ly.rms_ffn, eps, bxn))) return st;
+            if ((st = vgx_ffn_gate_batch(ctx, ly.w1, ly.w3, nseq, bxn, ly.hs, bhid))) return st;
+            if (ffn_chunk)
+                st = vgx_gemm_add_split_norm(ctx, ly.w2, ffn_chunk, nseq, bhid, bx1, bh, next_norm, eps, bxn);
+            else
+                st = vgx_gemm_norm(ctx, ly.w2, nseq, bhid, bx1, bh, next_norm, eps, bxn);
             if (st) return st;
         }
-        // the final norm on its own: the head's many row tiles would each
-        // recompute the statistics
-        if ((st = vgx_rmsnorm_batch(ctx, nseq, D, bh, rms_final, eps, batt))) return st;
-        if ((st = vgx_gemm(ctx, head_cat, nseq, batt, nullptr, blog))) return st;
+        if ((st = vgx_gemm(ctx, head_cat, nseq, bxn, nullptr, blog))) return st;
         return vgx_argmax_rows(ctx, nseq, m.vocab, blog, next_dev);
     }
 };

@@ -362,6 +362,21 @@ class GPU:
         _l.check(_l.load().vgx_ffn_gate_batch(self.ctx, w1.h, w3.h, n, _ptr(x), hs, _ptr(out)))
         return out
 
+    def gemm_norm(self, mat, x, res, rms_w, eps=1e-5, split=0):
+        """gemm (or gemm_add_split when split) and the RMSNorm of the rows it
+        wrote: (y, yn)."""
+        n = x.shape[0]
+        y = torch.empty((n, mat.rows), dtype=torch.int16, device=x.device)
+        yn = torch.empty_like(y)
+        L = _l.load()
+        if split:
+            _l.check(L.vgx_gemm_add_split_norm(self.ctx, mat.h, split, n, _ptr(x), _ptr(res), _ptr(y), _ptr(rms_w),
+                                               float(eps), _ptr(yn)))
+        else:
+            _l.check(L.vgx_gemm_norm(self.ctx, mat.h, n, _ptr(x), _ptr(res), _ptr(y), _ptr(rms_w), float(eps),
+                                     _ptr(yn)))
+        return y, yn
+
     def gemm_rms(self, mat, x, rms_w, eps=1e-5, res=None, out=None):
         """rmsnorm_batch(x, rms_w, eps) then gemm, one launch."""
         n = x.shape[0]
