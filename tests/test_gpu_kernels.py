@@ -458,3 +458,22 @@ def test_q4_adversarial_groups(gpu, rows, cols, copies, plan):
     y1 = o.store(oracle_rowval(a, x[:split]), res)
     assert np.array_equal(host(gpu.matvec_add_split(Ws[0], split, dev(x), dev(res))),
                           o.store(oracle_rowval(b, x[split:]), y1))
+
+
+@pytest.mark.parametrize("n", [73448, 6403, 64402, 8])
+def test_argmax_rows_first_maximum(gpu, n):
+    # 16-byte vectors where a row starts on a 16-byte boundary, the scalar
+    # loop for the tail and for unaligned rows (odd n): the first maximum of
+    # each row, with ties inside one vector, across lanes and at the ends
+    rng = np.random.default_rng(n)
+    V = rng.integers(-30000, 30000, (9, n)).astype(np.int16)
+    V[0, [n - 1, 0]] = 32767                      # first and last
+    V[1, [n // 2, n // 2 + 1]] = 32767            # adjacent (one vector)
+    if n > 9000:
+        V[2, [8 * 1024 + 3, 3]] = 32767           # another lane's vector first
+    if n > 66000:
+        V[3, [n - 5, 8 * 1024 * 8 + 1]] = 32767   # a later round
+    V[4] = -32768                                 # all equal: index 0
+    V[5, -1] = 32767                              # only the tail
+    got = host(gpu.argmax_rows(dev(V)))
+    assert np.array_equal(got, [o.argmax_i16(v) for v in V])

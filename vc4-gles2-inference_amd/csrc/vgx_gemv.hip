@@ -906,9 +906,33 @@ __global__ void __launch_bounds__(1024) argmax_kernel(const int16_t* v, int n, i
     v += (size_t)blockIdx.x * n;
     out += blockIdx.x;
     int best = -65536, bi = 0x7fffffff;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    // A row on a 16-byte boundary is read as 8-value vectors, eight of them a
+    // thread in flight before any comparison; a lane's vectors (and the values
+    // inside one) come in increasing index order, so its first maximum is kept.
+    int head = 0;
+    if (((uintptr_t)v & 15u) == 0) {
+        const int nvec = n / 8;
+        const uint4* v4 = reinterpret_cast<const uint4*>(v);
+        for (int b0 = threadIdx.x; b0 < nvec; b0 += 8 * (int)blockDim.x) {
+            uint4 q[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) q[k] = v4[min(b0 + k * (int)blockDim.x, nvec - 1)];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int b = b0 + k * (int)blockDim.x;
+                const uint32_t w[4] = {q[k].x, q[k].y, q[k].z, q[k].w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int x = (int)(int16_t)(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xFFFFu);
+                    if (b < nvec && x > best) { best = x; bi = 8 * b + e; }
+                }
+            }
+        }
+        head = nvec * 8;
+    }
+    for (int i = head + threadIdx.x; i < n; i += blockDim.x) {
         int x = v[i];
-        if (x > best) { best = x; bi = i; }  // i increases: the first max of this lane is kept
+        if (x > best || (x == best && i < bi)) { best = x; bi = i; }
     }
     for (int o = 32; o >= 1; o >>= 1) {
         int ob = __shfl_xor(best, o, 64), oi = __shfl_xor(bi, o, 64);
