@@ -37,6 +37,7 @@ namespace {
 
 constexpr int kThreads = 512;
 constexpr int kChunk = 32;  // positions per chunk of the summation order
+constexpr int kVStage = 8;  // 16-byte V pieces a thread stages per round (64 KB a workgroup)
 // 16-byte K vectors a lane holds for one scored position (int16 / int8 cache)
 template <int KVB>
 constexpr int kKPre = KVB == 16 ? 8 : 4;
@@ -180,22 +181,25 @@ __device__ __forceinline__ void dot_vec(const int4 a, const int4 b, int ones, co
 // The V values of one chunk for one lane's elements vi (and vi+1 when vE is
 // 2), as stored (16- or 8-bit fields, the first element low): position
 // c*kChunk + u in vch[u].  vrs covers rows 0..npos-1: a row at or past npos
-// reads nothing and gives zero (its weight is zero too).  An idle wave
-// passes a chunk past the cache.
+// reads nothing and gives zero (its weight is zero too); the range check is on
+// the per-lane offset, so rows past the cache need no clamp.  An idle wave
+// passes a chunk past the cache.  c is wave-uniform: one multiply per chunk,
+// then an add per row.
 template <int KVB>
 __device__ __forceinline__ void v_chunk_load(const AttnDev& A, __amdgpu_buffer_rsrc_t vrs, int vE, int c, int vi,
                                              int (&vch)[kChunk]) {
+    const int base = c * kChunk * A.pstride + vi * (KVB / 8);
     if (vE == 2) {
 #pragma unroll
         for (int u = 0; u < kChunk; ++u) {
-            const int off = min(c * kChunk + u, A.seq) * A.pstride + vi * (KVB / 8);
+            const int off = base + u * A.pstride;
             if (KVB == 16) vch[u] = (int)__builtin_amdgcn_raw_buffer_load_b32(vrs, off, 0, 0);
             else vch[u] = (int)__builtin_amdgcn_raw_buffer_load_b16(vrs, off, 0, 0);
         }
     } else {
 #pragma unroll
         for (int u = 0; u < kChunk; ++u) {
-            const int off = min(c * kChunk + u, A.seq) * A.pstride + vi * (KVB / 8);
+            const int off = base + u * A.pstride;
             if (KVB == 16) vch[u] = (int)__builtin_amdgcn_raw_buffer_load_b16(vrs, off, 0, 0);
             else vch[u] = (int)__builtin_amdgcn_raw_buffer_load_b8(vrs, off, 0, 0);
         }
@@ -632,7 +636,7 @@ struct GroupArgs {
     int fstride;        // floats per query vector's score row (nchmax chunks of 33)
     int rc;             // chunks per V round
     int qws;            // int words per query vector's plane (zero-padded to the lane plan)
-    int o_qh, o_ql, o_kpk, o_vpk, o_f, o_cs, o_st, o_part;  // LDS byte offsets
+    int o_qh, o_ql, o_kpk, o_vpk, o_f, o_cs, o_st, o_part, o_vs;  // LDS byte offsets
 };
 
 // The own row's V field of elements i (and i+1 when vE is 2) from its LDS copy,
@@ -649,7 +653,8 @@ __device__ __forceinline__ int vpk_word(const uint8_t* vpk, int vE, int i) {
 // so a lane per chunk reads distinct banks).
 __device__ __forceinline__ int fidx(int t) { return t + (t >> 5); }
 
-template <int KVB>
+// VE: V elements per lane of the weighted-V pass, 2 above head_dim 64.
+template <int KVB, int VE>
 __global__ void __launch_bounds__(kThreads) attn_group_kernel(const AttnDev A, const GroupArgs g) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int KP = kKPre<KVB>;
@@ -691,7 +696,7 @@ __global__ void __launch_bounds__(kThreads) attn_group_kernel(const AttnDev A, c
         for (int k = 0; k < KP; ++k) kreg[k] = src[min(sj + k * lpp, nv - 1)];
     }
     const int nchb = (npmax + kChunk - 1) / kChunk;
-    const int vE = hd > 64 ? 2 : 1;
+    constexpr int vE = VE;
     const int nblk = (hd + 64 * vE - 1) / (64 * vE);
     const int nitem = nq * nblk;
     // rows 0 .. npmax-1 of the head's V plane; a row past them reads zero
@@ -848,6 +853,40 @@ __global__ void __launch_bounds__(kThreads) attn_group_kernel(const AttnDev A, c
     }
     __syncthreads();
 
+    // The V rows of a round, staged in LDS: rows c0*kChunk .. of the head's
+    // plane are contiguous, so the round is one byte range read in 16-byte
+    // pieces, kVStage a thread at most.  Rows at or past npmax read zero; the
+    // own row (sequences mode) comes from its LDS copy, as its cache row is
+    // being written.  The first round's pieces load while the stats run.
+    uint8_t* const vs = smem + g.o_vs;  // [rc * kChunk][pstride]
+    const int per_row = A.pstride / 16;
+    uint4 vst[kVStage];
+    int vs_n = 0;  // pieces of the round in flight
+    auto stage_load = [&](int c0) {
+        const int row0 = c0 * kChunk;
+        vs_n = (min(row0 + g.rc * kChunk, npmax) - row0) * per_row;
+        const int base = row0 * A.pstride;
+#pragma unroll
+        for (int k = 0; k < kVStage; ++k)
+            if (k * kThreads < vs_n)
+                vst[k] = __builtin_bit_cast(
+                    uint4, __builtin_amdgcn_raw_buffer_load_b128(vrs, base + 16 * min(tid + k * kThreads, vs_n - 1), 0, 0));
+    };
+    auto stage_store = [&](int c0) {
+        const int own_piece = own ? (npmax - 1 - c0 * kChunk) * per_row : -1;
+#pragma unroll
+        for (int k = 0; k < kVStage; ++k) {
+            const int i = tid + k * kThreads;
+            if (k * kThreads < vs_n && i < vs_n) {
+                uint4 x = vst[k];
+                if (i >= own_piece && i < own_piece + per_row && own_piece >= 0)
+                    x = reinterpret_cast<const uint4*>(vpk)[i - own_piece];
+                reinterpret_cast<uint4*>(vs)[i] = x;
+            }
+        }
+    };
+    stage_load(0);
+
     // --- stats (att_stats): the max per query vector (a wave each), the
     // exponentials (+0.0 to the end of the last chunk), chunk sums in position
     // order, their total in chunk order, 1/sum on its grid
@@ -891,76 +930,54 @@ __global__ void __launch_bounds__(kThreads) attn_group_kernel(const AttnDev A, c
 
     // --- weighted V (att_v) in rounds of rc chunks.  Work unit (item, chunk):
     // item = (query vector, 64*vE elements), lane = element; the unit's V
-    // values come straight from the cache into registers (the next unit's
-    // loads issue before this unit's chain), its fma chain runs in position
-    // order into the round's partials, then the item's owner wave adds them
-    // to its sums in chunk order.  Weight of position t: (double)(e*iv) times
-    // the V grid unit.
+    // values come from the round's rows in LDS, its fma chain runs in position
+    // order into the round's partials, then the item's owner wave adds them to
+    // its sums in chunk order.  Weight of position t: (double)(e*iv); the sums
+    // take the V grid unit at the end (a power of two, so every rounding on
+    // the way is the one the weights times the unit would give).
     const double vunit_d = KVB == 16 ? 1.0 / 2048.0 : 1.0 / 16.0;
     constexpr int kItems = 4;  // items per wave (nq * nblk <= 32)
     double acc_a[kItems], acc_b[kItems];
 #pragma unroll
     for (int k = 0; k < kItems; ++k) acc_a[k] = acc_b[k] = 0.0;
-    const int vo = own ? vpk_word<KVB>(vpk, vE, min(lane * vE, hd - vE)) : 0;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);  // unit indexing in scalar registers
     for (int r = 0; r * g.rc < nchb; ++r) {
         const int c0 = r * g.rc, ncr = min(g.rc, nchb - c0), nunit = nitem * ncr;
-        __syncthreads();  // the stats are done / the previous round's partials are read
-        int vch[kChunk], vnx[kChunk];
-        auto unit_of = [&](int unit, int& item, int& c) {
-            item = unit / ncr;
-            c = c0 + unit - item * ncr;
-        };
-        int item, c;
-        unit_of(wave, item, c);
-        if (wave < nunit)
-            v_chunk_load<KVB>(A, vrs, vE, c, min(((item % nblk) * 64 + lane) * vE, hd - vE), vch);
-        for (int unit = wave; unit < nunit; unit += kThreads / 64) {
-            unit_of(unit, item, c);
-            const int nxt = unit + kThreads / 64;
-            if (nxt < nunit) {
-                int it2, c2;
-                unit_of(nxt, it2, c2);
-                v_chunk_load<KVB>(A, vrs, vE, c2, min(((it2 % nblk) * 64 + lane) * vE, hd - vE), vnx);
-            }
+        __syncthreads();  // the stats are done / the previous round's rows and partials are read
+        stage_store(c0);
+        if (c0 + g.rc < nchb) stage_load(c0 + g.rc);  // the next round's rows load during this one
+        __syncthreads();
+        for (int unit = wv; unit < nunit; unit += kThreads / 64) {
+            const int item = unit / ncr, c = c0 + unit - item * ncr;
             const int v = item / nblk, eb = item - v * nblk;
-            if (c * kChunk <= pfirst + v / hs) {  // a chunk this query reaches
-                const int ve = (eb * 64 + lane) * vE;
-                // the own row (the last position of a sequences-mode block)
-                // from the LDS copy: its cache row is being written
-                if (own && c == nchb - 1) {
-                    const int uo = npmax - 1 - c * kChunk;
-                    const int ow = eb == 0 ? vo : vpk_word<KVB>(vpk, vE, min(ve, hd - vE));
+            if (c * kChunk > pfirst + v / hs) continue;  // a chunk this query does not reach
+            const int vi = min((eb * 64 + lane) * vE, hd - vE);
+            const uint8_t* rows = vs + (size_t)(c - c0) * kChunk * A.pstride;
+            int vch[kChunk];
 #pragma unroll
-                    for (int u = 0; u < kChunk; ++u) vch[u] = u == uo ? ow : vch[u];
+            for (int u = 0; u < kChunk; ++u) vch[u] = vpk_word<KVB>(rows + u * A.pstride, vE, vi);
+            const float* Fv = F + v * g.fstride;
+            const double wl = (double)(Fv[fidx(c * kChunk + (lane & (kChunk - 1)))] * st[2 * v + 1]);
+            double a = 0.0, b = 0.0;
+            if (vE == 2) {
+#pragma unroll
+                for (int u = 0; u < kChunk; ++u) {
+                    const double wu = readlane_d(wl, u);
+                    a = fma(wu, (double)v_lo<KVB>(vch[u]), a);
+                    b = fma(wu, (double)v_hi<KVB>(vch[u]), b);
                 }
-                const float* Fv = F + v * g.fstride;
-                const float iv = st[2 * v + 1];
-                const double wl = (double)(Fv[fidx(c * kChunk + (lane & (kChunk - 1)))] * iv) * vunit_d;
-                double a = 0.0, b = 0.0;
-                if (vE == 2) {
+            } else {
 #pragma unroll
-                    for (int u = 0; u < kChunk; ++u) {
-                        const double wu = readlane_d(wl, u);
-                        a = fma(wu, (double)v_lo<KVB>(vch[u]), a);
-                        b = fma(wu, (double)v_hi<KVB>(vch[u]), b);
-                    }
-                } else {
-#pragma unroll
-                    for (int u = 0; u < kChunk; ++u) a = fma(readlane_d(wl, u), (double)v_lo<KVB>(vch[u]), a);
-                }
-                double* pp = part + ((size_t)item * g.rc + (c - c0)) * 64 * vE + lane * vE;
-                pp[0] = a;
-                if (vE == 2) pp[1] = b;
+                for (int u = 0; u < kChunk; ++u) a = fma(readlane_d(wl, u), (double)v_lo<KVB>(vch[u]), a);
             }
-            if (nxt < nunit) {
-#pragma unroll
-                for (int u = 0; u < kChunk; ++u) vch[u] = vnx[u];
-            }
+            double* pp = part + ((size_t)item * g.rc + (c - c0)) * 64 * vE + lane * vE;
+            pp[0] = a;
+            if (vE == 2) pp[1] = b;
         }
         __syncthreads();
 #pragma unroll
         for (int k = 0; k < kItems; ++k) {
-            const int it = wave + k * (kThreads / 64);
+            const int it = wv + k * (kThreads / 64);
             const int nch = it < nitem ? (pfirst + (it / nblk) / hs + 1 + kChunk - 1) / kChunk : 0;
             const double* pp = part + (size_t)it * g.rc * 64 * vE + lane * vE;
             for (int cc = c0; cc < min(nch, c0 + ncr); ++cc) {
@@ -977,8 +994,8 @@ __global__ void __launch_bounds__(kThreads) attn_group_kernel(const AttnDev A, c
         const int ve = (eb * 64 + lane) * vE;
         if (item < nitem && ve < hd) {
             int16_t* o = g.out + (size_t)(rbase + j) * A.dim + (h0 + v - j * hs) * hd;
-            o[ve] = (int16_t)q16_round((float)acc_a[k] * 256.0f);
-            if (vE == 2) o[ve + 1] = (int16_t)q16_round((float)acc_b[k] * 256.0f);
+            o[ve] = (int16_t)q16_round((float)(acc_a[k] * vunit_d) * 256.0f);
+            if (vE == 2) o[ve + 1] = (int16_t)q16_round((float)(acc_b[k] * vunit_d) * 256.0f);
         }
     }
 }
@@ -1087,17 +1104,19 @@ size_t group_layout(const AttnDev& A, int nq, int rc, GroupArgs& g) {
     g.o_st = take(8 * (size_t)nq);
     const int vE = A.hd > 64 ? 2 : 1, nblk = (A.hd + 64 * vE - 1) / (64 * vE);
     g.o_part = take((size_t)nq * nblk * rc * 64 * vE * 8);
+    g.o_vs = take((size_t)rc * kChunk * A.pstride);
     return off;
 }
 
 constexpr size_t kLdsMax = 160 * 1024;
 
-// The block plan of a query-block launch over nrow rows (batch) or nseq
-// sequences: hs query heads per workgroup, tq rows per block, rc chunks per V
-// round -- enough workgroups to cover the CUs, at most 16 query vectors a
-// block (32 work items of the V pass), a V round of at most kGroupPre vectors
-// per thread.  Returns the LDS bytes, or 0 when no plan fits.
-size_t group_plan(const AttnDev& A, bool seqs, int n, int num_cu, GroupArgs& g) {
+// The block plan of a query-block launch over n rows (batch) or n sequences
+// at position pos0: hs query heads per workgroup, tq rows per block -- enough
+// workgroups to cover the CUs, at most 16 query vectors a block (32 work items
+// of the V pass) -- and rc chunks per V round: the launch's longest context
+// when its rows fit the staging registers and LDS.  Returns the LDS bytes, or
+// 0 when no plan fits.
+size_t group_plan(const AttnDev& A, bool seqs, int pos0, int n, int num_cu, GroupArgs& g) {
     const int G = A.group;
     const int vE = A.hd > 64 ? 2 : 1, nblk = (A.hd + 64 * vE - 1) / (64 * vE);
     const int qmax = std::min(16, 32 / nblk);
@@ -1111,12 +1130,13 @@ size_t group_plan(const AttnDev& A, bool seqs, int n, int num_cu, GroupArgs& g) 
         const int want = (int)(((long)n * A.kv_heads * (G / hs) + num_cu - 1) / num_cu);
         tq = std::max(1, std::min({n, qmax / hs, want}));
     }
-    // a V round: partials of at most 32 KB (one chunk at least)
-    const size_t per_chunk_part = (size_t)hs * tq * nblk * 64 * vE * 8;
-    int rc = (int)std::min<size_t>(std::max<size_t>(1, 32768 / per_chunk_part), (size_t)A.nchmax);
+    // the score rows do not depend on rc: fit them first
+    while (group_layout(A, hs * tq, 1, g) > kLdsMax && tq > 1) --tq;
+    const int ctx = seqs ? pos0 + 1 : pos0 + n;
+    int rc = std::min({(ctx + kChunk - 1) / kChunk, kVStage * kThreads * 16 / (kChunk * A.pstride), A.nchmax});
+    rc = std::max(rc, 1);
     size_t lds = group_layout(A, hs * tq, rc, g);
-    while (lds > kLdsMax && tq > 1) lds = group_layout(A, hs * --tq, rc, g);
-    while (lds > kLdsMax / 2 && rc > 1) lds = group_layout(A, hs * tq, --rc, g);
+    while (lds > kLdsMax && rc > 1) lds = group_layout(A, hs * tq, --rc, g);
     if (lds > kLdsMax) return 0;
     g.hs = hs;
     g.tq = tq;
@@ -1130,7 +1150,7 @@ size_t group_plan(const AttnDev& A, bool seqs, int n, int num_cu, GroupArgs& g) 
 int launch_group(vgx_attn* at, int layer, int pos, int ntok, const int16_t* qkv, int16_t* out, bool seqs) {
     const AttnDev& A = at->a;
     GroupArgs g{};
-    const size_t lds = group_plan(A, seqs, ntok, at->ctx->num_cu, g);
+    const size_t lds = group_plan(A, seqs, pos, ntok, at->ctx->num_cu, g);
     if (!lds) return VGX_ESTATE;
     g.kv = at->kv[layer];
     g.rtab = at->rtab;
@@ -1145,10 +1165,14 @@ int launch_group(vgx_attn* at, int layer, int pos, int ntok, const int16_t* qkv,
     g.write = seqs ? 1 : 0;
     const int nsl = A.group / g.hs;
     const dim3 grid(A.kv_heads * nsl, seqs ? 1 : (ntok + g.tq - 1) / g.tq, seqs ? ntok : 1);
-    if (A.kv_bits == 16)
-        hipLaunchKernelGGL(attn_group_kernel<16>, grid, dim3(kThreads), lds, at->ctx->stream, A, g);
-    else
-        hipLaunchKernelGGL(attn_group_kernel<8>, grid, dim3(kThreads), lds, at->ctx->stream, A, g);
+    const bool ve2 = A.hd > 64;
+    if (A.kv_bits == 16) {
+        if (ve2) hipLaunchKernelGGL((attn_group_kernel<16, 2>), grid, dim3(kThreads), lds, at->ctx->stream, A, g);
+        else hipLaunchKernelGGL((attn_group_kernel<16, 1>), grid, dim3(kThreads), lds, at->ctx->stream, A, g);
+    } else {
+        if (ve2) hipLaunchKernelGGL((attn_group_kernel<8, 2>), grid, dim3(kThreads), lds, at->ctx->stream, A, g);
+        else hipLaunchKernelGGL((attn_group_kernel<8, 1>), grid, dim3(kThreads), lds, at->ctx->stream, A, g);
+    }
     VGX_LAUNCH_CHECK("query-block attention launch");
     return VGX_OK;
 }
@@ -1227,7 +1251,8 @@ int vgx_attn_create_seqs(vgx_ctx* ctx, const vgx_attn_desc* d, int nseq, vgx_att
         if (a1 != hipSuccess) return fail(a1, "hipFuncSetAttribute");
         if (a2 != hipSuccess) return fail(a2, "hipFuncSetAttribute");
     }
-    for (const void* k : {(const void*)attn_group_kernel<16>, (const void*)attn_group_kernel<8>}) {
+    for (const void* k : {(const void*)attn_group_kernel<16, 1>, (const void*)attn_group_kernel<16, 2>,
+                          (const void*)attn_group_kernel<8, 1>, (const void*)attn_group_kernel<8, 2>}) {
         const hipError_t a = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax);
         if (a != hipSuccess) return fail(a, "hipFuncSetAttribute");
     }
