@@ -27,6 +27,7 @@
 #include <cmath>
 #include <cstring>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "vgx_internal.h"
@@ -114,6 +115,32 @@ __device__ __forceinline__ void rope_pair(int rope_half, int hd, int i, int& j, 
         j = even ? i + 1 : i - 1;
         ti = i / 2;
         first = even;
+    }
+}
+
+// The inputs of one head vector's norm and rotation for lane l's elements
+// i = l + 64c (c < 4): the value, its rotation partner, the norm weights of
+// both (with qk_norm) and the table's cos and sin.  Indexes past the head
+// are clamped to its last element (those lanes' values are not used).
+struct RopeIn {
+    int a[4], b[4], na[4], nb[4], co[4], sn[4];
+};
+__device__ __forceinline__ void rope_load(int rope_half, int qk_norm, int hd, const int16_t* x, const int16_t* nw,
+                                          const int32_t* rt, int lane, RopeIn& r) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        r.a[c] = r.b[c] = r.na[c] = r.nb[c] = r.co[c] = r.sn[c] = 0;
+        if (64 * c >= hd) continue;  // (uniform) no element of this slot in the head
+        const int i = min(lane + 64 * c, hd - 1);
+        int j, ti;
+        bool first;
+        rope_pair(rope_half, hd, i, j, ti, first);
+        r.a[c] = x[i];
+        r.b[c] = x[j];
+        r.na[c] = qk_norm ? nw[i] : 0;
+        r.nb[c] = qk_norm ? nw[j] : 0;
+        r.co[c] = rt[2 * ti];
+        r.sn[c] = rt[2 * ti + 1];
     }
 }
 
@@ -653,8 +680,26 @@ __device__ __forceinline__ int vpk_word(const uint8_t* vpk, int vE, int i) {
 // so a lane per chunk reads distinct banks).
 __device__ __forceinline__ int fidx(int t) { return t + (t >> 5); }
 
-// VE: V elements per lane of the weighted-V pass, 2 above head_dim 64.
-template <int KVB, int VE>
+// Compile-time loop: f(integral_constant<int, U>) for U = B .. E-1.
+template <int B, int E, class Fn>
+__device__ __forceinline__ void static_for(Fn&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+// The weight of position U of a chunk in every lane: lane 16r + n of lo holds
+// the weight of position n (of hi: 16 + n) in each row r of 16 lanes, and the
+// row broadcast (DPP row_newbcast) gives lane n of each row to the whole row.
+template <int U>
+__device__ __forceinline__ double chunk_w(double lo, double hi) {
+    return __builtin_amdgcn_mov_dpp(U < 16 ? lo : hi, 0x150 + (U & 15), 0xf, 0xf, false);
+}
+
+// VE: V elements per lane of the weighted-V pass, 2 above head_dim 64.  QG:
+// query vectors per work unit of that pass (2 for blocks of at most two).
+template <int KVB, int VE, int QG>
 __global__ void __launch_bounds__(kThreads) attn_group_kernel(const AttnDev A, const GroupArgs g) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int KP = kKPre<KVB>;
@@ -702,6 +747,24 @@ __global__ void __launch_bounds__(kThreads) attn_group_kernel(const AttnDev A, c
     // rows 0 .. npmax-1 of the head's V plane; a row past them reads zero
     const __amdgpu_buffer_rsrc_t vrs = rows_rsrc(vhead_w, npmax * A.pstride);
 
+    // the own row's K and V inputs (last wave, sequences mode) and the first
+    // query vector's inputs of each wave: loaded before the first barrier
+    const int last = kThreads / 64 - 1;
+    const int16_t* const kq = g.qkv + (size_t)rbase * qrow + A.dim + kvh * hd;
+    RopeIn kin, qin;
+    int vin[4];
+    if (own && wave == last) {
+        rope_load(A.rope_half, A.qk_norm, hd, kq, g.kn, g.rtab + (size_t)g.pos0 * (hd / 2) * 2, lane, kin);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) vin[c] = 64 * c < hd ? kq[kv_dim + min(lane + 64 * c, hd - 1)] : 0;
+    }
+    auto q_load = [&](int v) {
+        const int j = v / hs, h = h0 + (v - j * hs);
+        rope_load(A.rope_half, A.qk_norm, hd, g.qkv + (size_t)(rbase + j) * qrow + h * hd, g.qn,
+                  g.rtab + (size_t)(pfirst + j) * (hd / 2) * 2, lane, qin);
+    };
+    if (wave < nq) q_load(wave);
+
     // the query planes' words past the row stay zero, so the scores need no mask
     for (int i = tid; i < nq * g.qws; i += kThreads) qhw[i] = qlw[i] = 0;
     __syncthreads();
@@ -709,16 +772,12 @@ __global__ void __launch_bounds__(kThreads) attn_group_kernel(const AttnDev A, c
     // --- the own row's KV pack (att_kv_rope), by the last wave while the first
     // waves prepare the queries: lane l takes elements l, l+64, ... of the KV
     // head; the first slice's workgroup stores the row
-    if (own && wave == kThreads / 64 - 1) {
-        const int16_t* kq = g.qkv + (size_t)rbase * qrow + A.dim + kvh * hd;
-        const int16_t* vq = kq + kv_dim;
-        const int32_t* rt = g.rtab + (size_t)g.pos0 * (hd / 2) * 2;
-        const int16_t* knp = A.qk_norm ? g.kn : kq;
+    if (own && wave == last) {
         const bool store = h0 == kvh * G;
         double ssk = 0.0;
+#pragma unroll
         for (int c = 0; c < 4; ++c) {
-            const int i = lane + 64 * c;
-            const int k = i < hd ? kq[i] : 0;
+            const int k = lane + 64 * c < hd ? kin.a[c] : 0;
             ssk += (double)(k * k);
         }
         ssk = wave_sum_exact(ssk);
@@ -727,19 +786,22 @@ __global__ void __launch_bounds__(kThreads) attn_group_kernel(const AttnDev A, c
             const float ss = (float)ssk * (1.0f / 65536.0f);
             rk = rsqrt_d(ss / (float)hd + 1e-6f);
         }
-        for (int i = lane; i < hd; i += 64) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int i = lane + 64 * c;
+            if (i >= hd) continue;
             int j, ti;
             bool first;
             rope_pair(A.rope_half, hd, i, j, ti, first);
-            const float co = (float)rt[2 * ti] / 4096.0f, sn = (float)rt[2 * ti + 1] / 4096.0f;
-            float vv = (float)kq[i] / 256.0f, bb = (float)kq[j] / 256.0f;
+            const float co = (float)kin.co[c] / 4096.0f, sn = (float)kin.sn[c] / 4096.0f;
+            float vv = (float)kin.a[c] / 256.0f, bb = (float)kin.b[c] / 256.0f;
             if (A.qk_norm) {
-                vv = (vv * rk) * ((float)knp[i] / 256.0f);
-                bb = (bb * rk) * ((float)knp[j] / 256.0f);
+                vv = (vv * rk) * ((float)kin.na[c] / 256.0f);
+                bb = (bb * rk) * ((float)kin.nb[c] / 256.0f);
             }
             const float o = first ? (vv * co) - (bb * sn) : (bb * sn) + (vv * co);
             const int q = kv_enc<KVB>(o);
-            const int qv = kv_enc<KVB>((float)vq[i] / 256.0f);
+            const int qv = kv_enc<KVB>((float)vin[c] / 256.0f);
             if (store) {
                 kv_put<KVB>(khead_w + (size_t)g.pos0 * A.pstride, i, q);
                 kv_put<KVB>(vhead_w + (size_t)g.pos0 * A.pstride, i, qv);
@@ -751,14 +813,11 @@ __global__ void __launch_bounds__(kThreads) attn_group_kernel(const AttnDev A, c
 
     // --- q prep (att_qnorm_scale + att_qrot), a wave per query vector
     for (int v = wave; v < nq; v += kThreads / 64) {
-        const int j = v / hs, h = h0 + (v - j * hs), p = pfirst + j;
-        const int16_t* qh = g.qkv + (size_t)(rbase + j) * qrow + h * hd;
-        const int16_t* qnp = A.qk_norm ? g.qn : qh;
-        const int32_t* rt = g.rtab + (size_t)p * (hd / 2) * 2;
+        if (v != wave) q_load(v);
         double ssq = 0.0;
+#pragma unroll
         for (int c = 0; c < 4; ++c) {
-            const int i = lane + 64 * c;
-            const int q = i < hd ? qh[i] : 0;
+            const int q = lane + 64 * c < hd ? qin.a[c] : 0;
             ssq += (double)(q * q);
         }
         ssq = wave_sum_exact(ssq);
@@ -769,15 +828,18 @@ __global__ void __launch_bounds__(kThreads) attn_group_kernel(const AttnDev A, c
             r = fminf(r, 127.0f);
             rq = floorf(r * 65536.0f + 0.5f) / 65536.0f;
         }
-        for (int i = lane; i < hd; i += 64) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int i = lane + 64 * c;
+            if (i >= hd) continue;
             int jj, ti;
             bool first;
             rope_pair(A.rope_half, hd, i, jj, ti, first);
-            const float co = (float)rt[2 * ti] / 4096.0f, sn = (float)rt[2 * ti + 1] / 4096.0f;
-            float qv = (float)qh[i] / 256.0f, b = (float)qh[jj] / 256.0f;
+            const float co = (float)qin.co[c] / 4096.0f, sn = (float)qin.sn[c] / 4096.0f;
+            float qv = (float)qin.a[c] / 256.0f, b = (float)qin.b[c] / 256.0f;
             if (A.qk_norm) {
-                qv = (qv * rq) * ((float)qnp[i] / 256.0f);
-                b = (b * rq) * ((float)qnp[jj] / 256.0f);
+                qv = (qv * rq) * ((float)qin.na[c] / 256.0f);
+                b = (b * rq) * ((float)qin.nb[c] / 256.0f);
             }
             const float o = first ? (qv * co) - (b * sn) : (b * sn) + (qv * co);
             q_split<KVB>(q16_round(o * 256.0f), i, qhw + v * g.qws, qlw + v * g.qws);
@@ -916,63 +978,117 @@ __global__ void __launch_bounds__(kThreads) attn_group_kernel(const AttnDev A, c
         for (int k = 0; k < kChunk; ++k) s += (double)Fc[k];
         cs[v * A.nchmax + c] = s;
     }
+    // the first V round's rows go to LDS beside the chunk sums; the second
+    // round's start loading
+    stage_store(0);
+    if (g.rc < nchb) stage_load(g.rc);
     __syncthreads();
-    if (tid < nq) {
-        const int v = tid, nch = (pfirst + v / hs + 1 + kChunk - 1) / kChunk;
+    // 1/sum of query vector v in lane v of every wave
+    float ivl = 0.0f;
+    if (lane < nq) {
+        const int v = lane, nch = (pfirst + v / hs + 1 + kChunk - 1) / kChunk;
+        // eight chunk sums read at a time, added in chunk order (a +0.0 past
+        // the last chunk leaves the sum as it is)
         double sum = 0.0;
-        for (int c = 0; c < nch; ++c) sum += cs[v * A.nchmax + c];
+        for (int c0 = 0; c0 < nch; c0 += 8) {
+            double t[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) t[k] = c0 + k < nch ? cs[v * A.nchmax + c0 + k] : 0.0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) sum += t[k];
+        }
         const float fs = (float)sum;
         float qs = floorf(fs * 32.0f + 0.5f);
         qs = fminf(fmaxf(qs, -32768.0f), 32767.0f);
         const float sd = qs / 32.0f;
-        st[2 * v + 1] = sd > 0.0f ? 1.0f / sd : 0.0f;
+        ivl = sd > 0.0f ? 1.0f / sd : 0.0f;
     }
 
-    // --- weighted V (att_v) in rounds of rc chunks.  Work unit (item, chunk):
-    // item = (query vector, 64*vE elements), lane = element; the unit's V
-    // values come from the round's rows in LDS, its fma chain runs in position
-    // order into the round's partials, then the item's owner wave adds them to
-    // its sums in chunk order.  Weight of position t: (double)(e*iv); the sums
+    // --- weighted V (att_v) in rounds of rc chunks.  Work unit (group of kQG
+    // query vectors, chunk, 64*vE elements), lane = element; the unit's V
+    // values come from the round's rows in LDS and are converted once for the
+    // group, each query vector's fma chain runs in position order into the
+    // round's partials of its item (query vector, elements), then the item's
+    // owner wave adds them to its sums in chunk order.  Weight of position t: (double)(e*iv); the sums
     // take the V grid unit at the end (a power of two, so every rounding on
     // the way is the one the weights times the unit would give).
     const double vunit_d = KVB == 16 ? 1.0 / 2048.0 : 1.0 / 16.0;
     constexpr int kItems = 4;  // items per wave (nq * nblk <= 32)
+    constexpr int kQG = QG;    // query vectors per work unit (one conversion of V for all)
     double acc_a[kItems], acc_b[kItems];
 #pragma unroll
     for (int k = 0; k < kItems; ++k) acc_a[k] = acc_b[k] = 0.0;
     const int wv = __builtin_amdgcn_readfirstlane(wave);  // unit indexing in scalar registers
     for (int r = 0; r * g.rc < nchb; ++r) {
-        const int c0 = r * g.rc, ncr = min(g.rc, nchb - c0), nunit = nitem * ncr;
-        __syncthreads();  // the stats are done / the previous round's rows and partials are read
-        stage_store(c0);
-        if (c0 + g.rc < nchb) stage_load(c0 + g.rc);  // the next round's rows load during this one
-        __syncthreads();
+        const int c0 = r * g.rc, ncr = min(g.rc, nchb - c0), nunit = (nq + kQG - 1) / kQG * nblk * ncr;
+        if (r > 0) {  // (the first round's rows are in place)
+            __syncthreads();  // the previous round's rows and partials are read
+            stage_store(c0);
+            if (c0 + g.rc < nchb) stage_load(c0 + g.rc);  // the next round's rows load during this one
+            __syncthreads();
+        }
         for (int unit = wv; unit < nunit; unit += kThreads / 64) {
-            const int item = unit / ncr, c = c0 + unit - item * ncr;
-            const int v = item / nblk, eb = item - v * nblk;
-            if (c * kChunk > pfirst + v / hs) continue;  // a chunk this query does not reach
+            const int grp = unit / ncr, c = c0 + unit - grp * ncr;  // grp = query group * nblk + eb
+            const int qg = grp / nblk, eb = grp - qg * nblk, v0 = qg * kQG;
+            // the group's query vectors that reach chunk c: rows j with c*kChunk <= pfirst + j
+            const int vlo = max(v0, (c * kChunk - pfirst) * hs), vhi = min(v0 + kQG, nq);
+            if (vlo >= vhi) continue;
             const int vi = min((eb * 64 + lane) * vE, hd - vE);
             const uint8_t* rows = vs + (size_t)(c - c0) * kChunk * A.pstride;
             int vch[kChunk];
 #pragma unroll
             for (int u = 0; u < kChunk; ++u) vch[u] = vpk_word<KVB>(rows + u * A.pstride, vE, vi);
-            const float* Fv = F + v * g.fstride;
-            const double wl = (double)(Fv[fidx(c * kChunk + (lane & (kChunk - 1)))] * st[2 * v + 1]);
-            double a = 0.0, b = 0.0;
-            if (vE == 2) {
+            // a query vector of the group that does not reach the chunk runs
+            // with zero weights (its sums are not stored): the group's chains
+            // interleave without branches
+            double wlo[kQG], whi[kQG];
 #pragma unroll
-                for (int u = 0; u < kChunk; ++u) {
-                    const double wu = readlane_d(wl, u);
-                    a = fma(wu, (double)v_lo<KVB>(vch[u]), a);
-                    b = fma(wu, (double)v_hi<KVB>(vch[u]), b);
-                }
-            } else {
-#pragma unroll
-                for (int u = 0; u < kChunk; ++u) a = fma(readlane_d(wl, u), (double)v_lo<KVB>(vch[u]), a);
+            for (int q = 0; q < kQG; ++q) {
+                const int v = min(v0 + q, nq - 1);
+                const bool on = v0 + q >= vlo && v0 + q < vhi;
+                const float* Fc = F + v * g.fstride + fidx(c * kChunk);
+                const float iv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ivl), v));
+                wlo[q] = on ? (double)(Fc[lane & 15] * iv) : 0.0;
+                whi[q] = on ? (double)(Fc[16 + (lane & 15)] * iv) : 0.0;
             }
-            double* pp = part + ((size_t)item * g.rc + (c - c0)) * 64 * vE + lane * vE;
-            pp[0] = a;
-            if (vE == 2) pp[1] = b;
+            double acc[kQG][vE];
+#pragma unroll
+            for (int q = 0; q < kQG; ++q)
+#pragma unroll
+                for (int e = 0; e < vE; ++e) acc[q][e] = 0.0;
+            // eight positions at a time: each V value converted once for the group
+            static_for<0, kChunk / 8>([&](auto UB) {
+                constexpr int u0 = decltype(UB)::value * 8;
+                double x[8][vE];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    x[j][0] = (double)v_lo<KVB>(vch[u0 + j]);
+                    if (vE == 2) x[j][vE - 1] = (double)v_hi<KVB>(vch[u0 + j]);
+                }
+                static_for<0, 8>([&](auto J) {
+                    constexpr int j = decltype(J)::value;
+#pragma unroll
+                    for (int q = 0; q < kQG; ++q) {
+                        // the weight registers pass through the chain here, so
+                        // this position's broadcast follows the last fma (hoisted,
+                        // a whole chunk's weights would not fit in registers)
+                        if constexpr (vE == 2)
+                            asm volatile("" : "+v"(wlo[q]), "+v"(whi[q]), "+v"(acc[q][0]), "+v"(acc[q][vE - 1]));
+                        else
+                            asm volatile("" : "+v"(wlo[q]), "+v"(whi[q]), "+v"(acc[q][0]));
+                        const double wu = chunk_w<u0 + j>(wlo[q], whi[q]);
+#pragma unroll
+                        for (int e = 0; e < vE; ++e) acc[q][e] = fma(wu, x[j][e], acc[q][e]);
+                    }
+                });
+            });
+#pragma unroll
+            for (int q = 0; q < kQG; ++q) {
+                if (v0 + q < vlo || v0 + q >= vhi) continue;
+                double* pp = part + ((size_t)((v0 + q) * nblk + eb) * g.rc + (c - c0)) * 64 * vE + lane * vE;
+#pragma unroll
+                for (int e = 0; e < vE; ++e) pp[e] = acc[q][e];
+            }
         }
         __syncthreads();
 #pragma unroll
@@ -980,9 +1096,20 @@ __global__ void __launch_bounds__(kThreads) attn_group_kernel(const AttnDev A, c
             const int it = wv + k * (kThreads / 64);
             const int nch = it < nitem ? (pfirst + (it / nblk) / hs + 1 + kChunk - 1) / kChunk : 0;
             const double* pp = part + (size_t)it * g.rc * 64 * vE + lane * vE;
-            for (int cc = c0; cc < min(nch, c0 + ncr); ++cc) {
-                acc_a[k] += pp[(cc - c0) * 64 * vE];
-                if (vE == 2) acc_b[k] += pp[(cc - c0) * 64 * vE + 1];
+            const int ncc = min(nch, c0 + ncr) - c0;  // this round's chunks of the item
+            // eight partials read at a time, added in chunk order (+0.0 past the last)
+            for (int b = 0; b < ncc; b += 8) {
+                double ta[8], tb[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    ta[u] = b + u < ncc ? pp[(b + u) * 64 * vE] : 0.0;
+                    tb[u] = vE == 2 && b + u < ncc ? pp[(b + u) * 64 * vE + 1] : 0.0;
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    acc_a[k] += ta[u];
+                    if (vE == 2) acc_b[k] += tb[u];
+                }
             }
         }
     }
@@ -1143,6 +1270,19 @@ size_t group_plan(const AttnDev& A, bool seqs, int pos0, int n, int num_cu, Grou
     return lds;
 }
 
+using GroupKernel = void (*)(AttnDev, GroupArgs);
+
+// The query-block kernel instance for KV bits, V elements per lane and query
+// vectors per V work unit.
+GroupKernel group_kernel(int kvb, int ve, int qg) {
+    if (kvb == 16) {
+        if (ve == 2) return qg == 2 ? attn_group_kernel<16, 2, 2> : attn_group_kernel<16, 2, 4>;
+        return qg == 2 ? attn_group_kernel<16, 1, 2> : attn_group_kernel<16, 1, 4>;
+    }
+    if (ve == 2) return qg == 2 ? attn_group_kernel<8, 2, 2> : attn_group_kernel<8, 2, 4>;
+    return qg == 2 ? attn_group_kernel<8, 1, 2> : attn_group_kernel<8, 1, 4>;
+}
+
 // The query-block kernel over rows 0..ntok-1 (positions pos .. pos+ntok-1 of
 // one sequence), or over position pos of ntok sequences (seqs: packing the
 // row first).  Returns VGX_ESTATE when no block plan fits (the caller then
@@ -1165,14 +1305,8 @@ int launch_group(vgx_attn* at, int layer, int pos, int ntok, const int16_t* qkv,
     g.write = seqs ? 1 : 0;
     const int nsl = A.group / g.hs;
     const dim3 grid(A.kv_heads * nsl, seqs ? 1 : (ntok + g.tq - 1) / g.tq, seqs ? ntok : 1);
-    const bool ve2 = A.hd > 64;
-    if (A.kv_bits == 16) {
-        if (ve2) hipLaunchKernelGGL((attn_group_kernel<16, 2>), grid, dim3(kThreads), lds, at->ctx->stream, A, g);
-        else hipLaunchKernelGGL((attn_group_kernel<16, 1>), grid, dim3(kThreads), lds, at->ctx->stream, A, g);
-    } else {
-        if (ve2) hipLaunchKernelGGL((attn_group_kernel<8, 2>), grid, dim3(kThreads), lds, at->ctx->stream, A, g);
-        else hipLaunchKernelGGL((attn_group_kernel<8, 1>), grid, dim3(kThreads), lds, at->ctx->stream, A, g);
-    }
+    hipLaunchKernelGGL(group_kernel(A.kv_bits, A.hd > 64 ? 2 : 1, g.hs * g.tq <= 2 ? 2 : 4), grid, dim3(kThreads), lds,
+                       at->ctx->stream, A, g);
     VGX_LAUNCH_CHECK("query-block attention launch");
     return VGX_OK;
 }
@@ -1251,11 +1385,13 @@ int vgx_attn_create_seqs(vgx_ctx* ctx, const vgx_attn_desc* d, int nseq, vgx_att
         if (a1 != hipSuccess) return fail(a1, "hipFuncSetAttribute");
         if (a2 != hipSuccess) return fail(a2, "hipFuncSetAttribute");
     }
-    for (const void* k : {(const void*)attn_group_kernel<16, 1>, (const void*)attn_group_kernel<16, 2>,
-                          (const void*)attn_group_kernel<8, 1>, (const void*)attn_group_kernel<8, 2>}) {
-        const hipError_t a = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax);
-        if (a != hipSuccess) return fail(a, "hipFuncSetAttribute");
-    }
+    for (int kvb : {16, 8})
+        for (int ve : {1, 2})
+            for (int qg : {2, 4}) {
+                const hipError_t a = hipFuncSetAttribute((const void*)group_kernel(kvb, ve, qg),
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax);
+                if (a != hipSuccess) return fail(a, "hipFuncSetAttribute");
+            }
     *out = at;
     return VGX_OK;
 }
