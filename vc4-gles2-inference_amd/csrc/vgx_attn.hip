@@ -634,6 +634,60 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
 }
 
 // ---------------------------------------------------------------------------
+// KV pack of ntok consecutive positions pos0.. of one sequence (att_kv_rope,
+// the batch's rows written before its attention): a wave per (row, KV head),
+// lane l taking elements l, l+64, ...; the attention kernels' own-row pack,
+// step for step.
+constexpr int kPackWaves = 4;
+
+template <int KVB>
+__global__ void __launch_bounds__(64 * kPackWaves) kv_pack_kernel(const AttnDev A, uint8_t* kv, const int32_t* rtab,
+                                                                  const int16_t* kn, const int16_t* qkv, int pos0,
+                                                                  int ntok) {
+    const int item = blockIdx.x * kPackWaves + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (item >= ntok * A.kv_heads) return;  // (a whole wave)
+    const int row = item / A.kv_heads, kvh = item - row * A.kv_heads;
+    const int hd = A.hd, kv_dim = A.kv_heads * hd, pos = pos0 + row;
+    const int16_t* kq = qkv + (size_t)row * (A.dim + 2 * kv_dim) + A.dim + kvh * hd;
+    RopeIn kin;
+    int vin[4];
+    rope_load(A.rope_half, A.qk_norm, hd, kq, kn, rtab + (size_t)pos * (hd / 2) * 2, lane, kin);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) vin[c] = 64 * c < hd ? kq[kv_dim + min(lane + 64 * c, hd - 1)] : 0;
+    double ssk = 0.0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int k = lane + 64 * c < hd ? kin.a[c] : 0;
+        ssk += (double)(k * k);
+    }
+    ssk = wave_sum_exact(ssk);
+    float rk = 1.0f;
+    if (A.qk_norm) {
+        const float ss = (float)ssk * (1.0f / 65536.0f);
+        rk = rsqrt_d(ss / (float)hd + 1e-6f);
+    }
+    uint8_t* const krow = kv + ((size_t)kvh * A.seq + pos) * A.pstride;
+    uint8_t* const vrow = kv + ((size_t)(A.kv_heads + kvh) * A.seq + pos) * A.pstride;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int i = lane + 64 * c;
+        if (i >= hd) continue;
+        int j, ti;
+        bool first;
+        rope_pair(A.rope_half, hd, i, j, ti, first);
+        const float co = (float)kin.co[c] / 4096.0f, sn = (float)kin.sn[c] / 4096.0f;
+        float vv = (float)kin.a[c] / 256.0f, bb = (float)kin.b[c] / 256.0f;
+        if (A.qk_norm) {
+            vv = (vv * rk) * ((float)kin.na[c] / 256.0f);
+            bb = (bb * rk) * ((float)kin.nb[c] / 256.0f);
+        }
+        const float o = first ? (vv * co) - (bb * sn) : (bb * sn) + (vv * co);
+        kv_put<KVB>(krow, i, kv_enc<KVB>(o));
+        kv_put<KVB>(vrow, i, kv_enc<KVB>((float)vin[c] / 256.0f));
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Query-block attention: one workgroup per (KV head, slice of its query heads)
 // and block of query vectors -- the slice's heads at tq consecutive positions
 // of one sequence (batched prefill), or at one position of sequence blockIdx.z
@@ -1195,6 +1249,18 @@ int launch(vgx_attn* at, int layer, int pos, int ntok, const int16_t* qkv, int16
     if (att && !pos_ptr && ((!seqs && !w && ntok > 1) || (seqs && w && A.group >= kGroupSeqsG))) {
         const int st = launch_group(at, layer, pos, ntok, qkv, out, seqs);
         if (st != VGX_ESTATE) return st;
+    }
+    // the rows of a batch of one sequence: the pack kernel
+    if (!att && !seqs && !pos_ptr) {
+        const dim3 pg((ntok * A.kv_heads + kPackWaves - 1) / kPackWaves);
+        if (A.kv_bits == 16)
+            hipLaunchKernelGGL(kv_pack_kernel<16>, pg, dim3(64 * kPackWaves), 0, at->ctx->stream, A, at->kv[layer],
+                               at->rtab, kn, qkv, pos, ntok);
+        else
+            hipLaunchKernelGGL(kv_pack_kernel<8>, pg, dim3(64 * kPackWaves), 0, at->ctx->stream, A, at->kv[layer],
+                               at->rtab, kn, qkv, pos, ntok);
+        VGX_LAUNCH_CHECK("KV pack launch");
+        return VGX_OK;
     }
     const dim3 grid(att ? A.heads : A.kv_heads, ntok);
     const size_t stride = seqs ? at->seq_bytes : 0;
