@@ -235,9 +235,9 @@ __device__ __forceinline__ void rms_stats(const GemmLaunch& G, int t0, unsigned 
 
 // One workgroup: a 32-token x 32-weight-row output tile.  Its NW waves take
 // contiguous runs of the k-steps (32 columns each); every wave keeps the raw
-// operand bytes of its next NPF steps in flight, and the waves' exact partial
-// sums (doubles for q4, added in wave order) meet in wave 0, RC accumulator
-// registers a round, before the epilogue.  NW = 4 when the launch has many
+// operand bytes of its next NPF steps in flight, then leaves its exact partial
+// sums in LDS, and every thread adds the waves' sums for its outputs of the
+// tile and applies the epilogue.  NW = 4 when the launch has many
 // tiles; 8 when it has few (the decode batch of up to 32 sequences), so that
 // each wave walks fewer steps.  RMS: the input rows go through RMSNorm first,
 // the statistics formed in the workgroup.
@@ -245,13 +245,12 @@ template <int KIND, int EPI, int NW, bool RMS, bool PART>
 __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmLaunch G) {
     constexpr int NT = 64 * NW;
     constexpr int NA = EPI == BEPI_STORE ? 1 : 2;  // accumulator sets: W1/W3 or the two halves
-    constexpr int RC = 16 / NA;                    // accumulator registers a reduction round
     constexpr int NPF = 4;                         // k-steps a round
     // LDS: each wave's activation block for a round (32 tokens x NPF steps of
     // 32 columns, int16: 256 bytes a token), reused for the reduction once
     // every wave is past its last round
     extern __shared__ __align__(16) unsigned char s_dyn[];
-    __shared__ int s_ws[NW - 1][NA][64];
+    __shared__ int s_wsum[NW][NA][64];  // each wave's weight sums per lane
     __shared__ int s_xg[NW][kTile];  // q4: this step's group sum of x per token
     __shared__ unsigned long long s_tot[kTile];
     __shared__ float s_inv[kTile];
@@ -357,25 +356,25 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmLaunch G) {
 #pragma unroll
         for (int j = 0; j < NPF; ++j) raw_load(min(s_beg + j, s_end - 1), rb[j]);
     }
-    // wave 0's epilogue operands (row scales, residuals), loaded before
-    // anything waits: issued at the epilogue they cost a memory round trip
-    // there
-    float wsr_e = 0.0f, wsr3_e = 0.0f;
-    int res_e[16];
+    // this thread's epilogue operands (row scales, residuals) for its
+    // outputs of the tile (below), loaded before anything waits: issued at
+    // the epilogue they cost a memory round trip there
+    constexpr int kOutPer = kTile * kTile / NT;  // outputs a thread takes
+    float e_wsr[kOutPer], e_wsr3[kOutPer];
+    int e_res[kOutPer];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) res_e[r] = 0;
-    if (!PART && wave == 0) {
+    for (int k = 0; k < kOutPer; ++k) {
+        const int p = threadIdx.x + k * NT, l = p & 63, r = p >> 6;
+        const int on = min(n0 + (l & 31), M.rows - 1);
+        const int ot = min(t0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3), G.ntok - 1);
+        e_wsr[k] = e_wsr3[k] = 0.0f;
+        e_res[k] = 0;
+        if (PART) continue;
         if (KIND != VGX_Q4) {
-            wsr_e = M.wsr[nn];
-            if (EPI == BEPI_GATE) wsr3_e = G.M3.wsr[nn];
+            e_wsr[k] = M.wsr[on];
+            if (EPI == BEPI_GATE) e_wsr3[k] = G.M3.wsr[on];
         }
-        if (EPI != BEPI_GATE && G.res) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int tt = min(t0 + 8 * (r >> 2) + 4 * half + (r & 3), G.ntok - 1);
-                res_e[r] = G.res[(size_t)tt * G.ldy + nn];
-            }
-        }
+        if (EPI != BEPI_GATE && G.res) e_res[k] = G.res[(size_t)ot * G.ldy + on];
     }
     if (RMS) rms_stats<NT>(G, t0, s_tot, s_inv);
     auto do_round = [&](int s0, uint4 (&xv)[8], uint4& wv, Raw* rr) {
@@ -458,127 +457,64 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmLaunch G) {
     };
     for (int s0 = s_beg; s0 < s_end; s0 += NPF) do_round(s0, xn, wn, rb);
     __syncthreads();  // every wave is past its blocks: the LDS becomes the reduction buffer
-    unsigned char* s_red = s_dyn;
 
-    // the waves' partial sums meet in wave 0, RC accumulator registers a
-    // round, added in wave order (exact integers)
+    // Every wave leaves its exact partial sums in LDS -- per accumulator set a
+    // and register r of lane l: the q4 group sums, or 256*hi + lo as one int64
+    // (its row's weight sums apart) -- then every thread takes outputs of the
+    // tile: the waves' sums added (integers: any order gives the same total)
+    // and the epilogue.  Output (l, r): weight row n0 + l%32, token
+    // t0 + 8*(r/4) + 4*(l/32) + r%4.
+    long long* s_red = reinterpret_cast<long long*>(s_dyn);  // [NW][NA][16][64]
 #pragma unroll
-    for (int r0 = 0; r0 < 16; r0 += RC) {
-        if (wave > 0) {
-            if (KIND == VGX_Q4) {
-                long long* p = reinterpret_cast<long long*>(s_red) + (size_t)(wave - 1) * NA * RC * 64;
+    for (int a = 0; a < NA; ++a)
 #pragma unroll
-                for (int a = 0; a < NA; ++a)
-#pragma unroll
-                    for (int c = 0; c < RC; ++c) p[(a * RC + c) * 64 + lane] = dacc[a][r0 + c];
-            } else {
-                int* p = reinterpret_cast<int*>(s_red) + (size_t)(wave - 1) * NA * 2 * RC * 64;
-#pragma unroll
-                for (int a = 0; a < NA; ++a)
-#pragma unroll
-                    for (int c = 0; c < RC; ++c) {
-                        p[(a * 2 * RC + c) * 64 + lane] = ch[a][r0 + c];
-                        p[(a * 2 * RC + RC + c) * 64 + lane] = cl[a][r0 + c];
-                    }
-            }
-        }
-        __syncthreads();
-        if (wave == 0) {
-            for (int wv = 1; wv < NW; ++wv) {
-                if (KIND == VGX_Q4) {
-                    const long long* p = reinterpret_cast<const long long*>(s_red) + (size_t)(wv - 1) * NA * RC * 64;
-#pragma unroll
-                    for (int a = 0; a < NA; ++a)
-#pragma unroll
-                        for (int c = 0; c < RC; ++c) dacc[a][r0 + c] += p[(a * RC + c) * 64 + lane];
-                } else {
-                    const int* p = reinterpret_cast<const int*>(s_red) + (size_t)(wv - 1) * NA * 2 * RC * 64;
-#pragma unroll
-                    for (int a = 0; a < NA; ++a)
-#pragma unroll
-                        for (int c = 0; c < RC; ++c) {
-                            ch[a][r0 + c] += p[(a * 2 * RC + c) * 64 + lane];
-                            cl[a][r0 + c] += p[(a * 2 * RC + RC + c) * 64 + lane];
-                        }
-                }
-            }
-        }
-        __syncthreads();
-    }
+        for (int r = 0; r < 16; ++r)
+            s_red[((wave * NA + a) * 16 + r) * 64 + lane] =
+                KIND == VGX_Q4 ? dacc[a][r] : 256LL * ch[a][r] + (long long)cl[a][r];
     if (KIND != VGX_Q4) {
-        if (wave > 0)
 #pragma unroll
-            for (int a = 0; a < NA; ++a) s_ws[wave - 1][a][lane] = wsum[a];
-        __syncthreads();
-        if (wave == 0)
-            for (int wv = 1; wv < NW; ++wv)
-#pragma unroll
-                for (int a = 0; a < NA; ++a) wsum[a] += s_ws[wv - 1][a][lane];
+        for (int a = 0; a < NA; ++a) s_wsum[wave][a][lane] = wsum[a];
     }
-    // the gate's epilogue spreads its exponentials over every wave (below);
-    // the others run in wave 0
-    constexpr bool GSPREAD = EPI == BEPI_GATE && !PART;
-    if (wave != 0 && !GSPREAD) return;
-
-    // epilogue: this lane holds column n for 16 token rows
-    int wtot[NA];
+    __syncthreads();
 #pragma unroll
-    for (int a = 0; a < NA; ++a) wtot[a] = wsum[a] + __shfl_xor(wsum[a], 32, 64);
-    if (PART) {
-        // this split's exact sums: the q4 group sums, or 256*hi + lo + 128*sum(w)
+    for (int k = 0; k < kOutPer; ++k) {
+        const int p = threadIdx.x + k * NT, l = p & 63, r = p >> 6;
+        const int on = n0 + (l & 31), ot = t0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+        if (on >= M.rows || ot >= G.ntok) continue;
+        long long S[NA];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int tt = t0 + 8 * (r >> 2) + 4 * half + (r & 3);
-            if (!nok || tt >= G.ntok) continue;
+        for (int a = 0; a < NA; ++a) {
+            long long t = 0;
 #pragma unroll
-            for (int a = 0; a < NA; ++a) {
-                const long long S = KIND == VGX_Q4 ? dacc[a][r]
-                                                   : 256LL * ch[a][r] + (long long)cl[a][r] + 128LL * wtot[a];
-                G.part[(((size_t)blockIdx.z * NA + a) * G.ntok + tt) * M.rows + n] = S;
+            for (int w = 0; w < NW; ++w) t += s_red[((w * NA + a) * 16 + r) * 64 + l];
+            if (KIND != VGX_Q4) {
+                int wt = 0;  // the row's weight sum over both column halves
+#pragma unroll
+                for (int w = 0; w < NW; ++w) wt += s_wsum[w][a][l] + s_wsum[w][a][l ^ 32];
+                t += 128LL * wt;
             }
+            S[a] = t;
         }
-        return;
-    }
-    const float wsr = nok ? wsr_e : 0.0f;
-    const float wsr3 = nok ? wsr3_e : 0.0f;
-    // gate: wave 0 leaves the tile's (W1, W3) row values in LDS, then every
-    // thread takes outputs of the tile
-    float2* gv = reinterpret_cast<float2*>(s_dyn);  // [32 tokens][32 rows]
+        if (PART) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        if (GSPREAD && wave != 0) break;
-        const int m = 8 * (r >> 2) + 4 * half + (r & 3);
-        const int tt = t0 + m;
-        if (!nok || tt >= G.ntok) continue;
+            for (int a = 0; a < NA; ++a) G.part[(((size_t)blockIdx.z * NA + a) * G.ntok + ot) * M.rows + on] = S[a];
+            continue;
+        }
         float v[NA];
 #pragma unroll
         for (int a = 0; a < NA; ++a) {
-            if (KIND == VGX_Q4) {
-                v[a] = (float)dacc[a][r] * ((EPI == BEPI_GATE && a == 1) ? ps3 : ps);
-            } else {
-                const long long S = 256LL * ch[a][r] + (long long)cl[a][r] + 128LL * wtot[a];
-                const float sc = (EPI == BEPI_GATE && a == 1) ? wsr3 : wsr;
-                v[a] = (float)S * sc;
-            }
+            const float sc = KIND == VGX_Q4 ? ((EPI == BEPI_GATE && a == 1) ? ps3 : ps)
+                                            : ((EPI == BEPI_GATE && a == 1) ? e_wsr3[k] : e_wsr[k]);
+            v[a] = (float)S[a] * sc;
         }
-        int16_t* yo = G.y + (size_t)tt * G.ldy + n;
+        int16_t* yo = G.y + (size_t)ot * G.ldy + on;
         if (EPI == BEPI_STORE) {
-            const float o = G.res ? v[0] + (float)res_e[r] : v[0];
-            *yo = (int16_t)q16_round(o);
+            *yo = (int16_t)q16_round(G.res ? v[0] + (float)e_res[k] : v[0]);
         } else if (EPI == BEPI_SPLIT) {
-            const float y1 = (float)q16_round(v[0] + (float)res_e[r]);
+            const float y1 = (float)q16_round(v[0] + (float)e_res[k]);
             *yo = (int16_t)q16_round(v[NA - 1] + y1);
         } else {
-            gv[m * kTile + li] = make_float2(v[0], v[NA - 1]);
-        }
-    }
-    if (GSPREAD) {
-        __syncthreads();
-        for (int i = threadIdx.x; i < kTile * kTile; i += NT) {
-            const int m = i / kTile, c = i - m * kTile;
-            const int tt = t0 + m, nr = n0 + c;
-            if (tt < G.ntok && nr < M.rows)
-                G.y[(size_t)tt * G.ldy + nr] = (int16_t)q16_round(gate_value(gv[i].x, gv[i].y, G.hs));
+            *yo = (int16_t)q16_round(gate_value(v[0], v[NA - 1], G.hs));
         }
     }
 }
@@ -779,11 +715,13 @@ int launch(vgx_ctx* ctx, const vgx_mat* W, const vgx_mat* W3, int ntok, const in
     const int nw = nz > 1 ? 4 : waves_for((int)(grid.x * grid.y), nsteps, ctx->num_cu);
     GemmFn fn = pick(epi, M.kind, nw, rw != nullptr, nz > 1);
     if (!fn) return vgx_fail(VGX_EINVAL, std::string(who) + ": unknown weight kind");
-    // each wave's activation block: 32 tokens x 4 k-steps of 32 int16
-    const int lds = nw * kTile * 4 * kTile * 2;
+    // each wave's activation block (32 tokens x 4 k-steps of 32 int16), then
+    // each wave's exact sums (16 int64 a lane per accumulator set)
+    const int na = epi == BEPI_STORE ? 1 : 2;
+    const int lds = std::max(nw * kTile * 4 * kTile * 2, nw * na * 16 * 64 * 8);
     if (lds > 48 * 1024) {
-        static bool lds_set[64];
-        const int slot = ((epi * 2 + (rw ? 1 : 0)) * 4 + M.kind) * 2 + (nw == 8 ? 1 : 0);
+        static bool lds_set[128];
+        const int slot = (((epi * 2 + (rw ? 1 : 0)) * 4 + M.kind) * 2 + (nw == 8 ? 1 : 0)) * 2 + (nz > 1 ? 1 : 0);
         if (!lds_set[slot]) {
             VGX_HIP(hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds));
             lds_set[slot] = true;
