@@ -42,9 +42,16 @@ def weight_bytes(rows, cols, kind):
 
 
 def make_matrix(rng, rows, cols, kind):
-    """N(0, 0.02) fp32 weights packed by the container packer (vgx.mmcf)."""
+    """N(0, 0.02) fp32 weights packed by the container packer (vgx.mmcf); for
+    t3, the synthetic per-row ternary weights of the t3 models (vgx.synth)."""
     import numpy as np
     from vgx import mmcf
+    if kind == "t3":
+        from vgx import synth
+        packed, unit, plane = mmcf.t3mat(synth.ternary_matrix(rng, rows, cols))
+        return mmcf.Matrix("t3", rows, cols, np.frombuffer(packed, np.uint8), unit, plane=plane)
+    if kind != "q4" and kind != "q8":
+        raise ValueError("make_matrix: kind must be q8, q4 or t3")
     w = rng.standard_normal((rows, cols)).astype(np.float32) * np.float32(0.02)
     if kind == "q4":
         packed, s16, m16, ps, _ = mmcf.q4mat(w)
@@ -232,7 +239,54 @@ def ternary_batch_bench(runs, nseq=32):
     return {"model": "0.5B Llama-shaped t3 (per-row ternary P(0)=0.4), seed 0", "sequences": nseq, "prompt": 128,
             "gen": 256, "seq": 512, "kv": "q16", "tokens_per_s": round(nseq * 1000.0 / ms_step, 1),
             "ms_per_step": round(ms_step, 4), "prefill_ms_all_sequences": round(float(np.median(pf)), 2),
-            "runs": runs}
+            "runs": runs, "gemm_int8_peak_TOPS": INT8_PEAK_TOPS, "gemms": decode_batch_gemms()}
+
+
+def decode_batch_gemms(reps=200):
+    """The C5 batch-32 step's GEMMs alone, at its shapes (32 tokens, the 0.5B
+    t3 layer): qkv (split K, then its epilogue), wo + residual with the FFN
+    RMSNorm in its split epilogue, the gate, w2 + residual (split at the
+    chunk) with the next RMSNorm -- the calls the batched decode loop makes --
+    timed with HIP events on the launch stream; algorithmic int8 ops 2*M*N*K
+    (the gate: both matrices) against the matrix-core peak."""
+    import numpy as np
+    import torch
+    from vgx import gpu as vg
+
+    g = vg.GPU(0)
+    rng = np.random.default_rng(0)
+    M, dim, hidden = 32, 1024, 4096
+    x = torch.from_numpy(rng.integers(-3000, 3000, (M, dim)).astype(np.int16)).cuda()
+    xh = torch.from_numpy(rng.integers(-3000, 3000, (M, hidden)).astype(np.int16)).cuda()
+    res = torch.from_numpy(rng.integers(-3000, 3000, (M, dim)).astype(np.int16)).cuda()
+    nw = torch.from_numpy(rng.integers(100, 400, dim).astype(np.int16)).cuda()
+    mats = {k: g.upload(make_matrix(rng, r, c, "t3"))
+            for k, (r, c) in {"qkv": (1280, dim), "wo": (dim, dim), "w1": (hidden, dim), "w3": (hidden, dim),
+                              "w2": (dim, hidden)}.items()}
+    calls = [
+        ("qkv", 1280, dim, lambda: g.gemm(mats["qkv"], x)),
+        ("wo + norm", dim, dim, lambda: g.gemm_norm(mats["wo"], x, res, nw)),
+        ("gate (w1, w3)", 2 * hidden, dim, lambda: g.ffn_gate_batch(mats["w1"], mats["w3"], x)),
+        ("w2 + split + norm", dim, hidden, lambda: g.gemm_norm(mats["w2"], xh, res, nw, split=hidden // 2)),
+    ]
+    out = []
+    for name, rows, cols, f in calls:
+        for _ in range(5):
+            f()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            f()
+        b.record()
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / reps
+        tops = 2.0 * M * rows * cols / (us * 1e-6) / 1e12
+        out.append({"gemm": name, "M_tokens": M, "N": rows, "K": cols, "kind": "t3", "us": round(us, 2),
+                    "int8_TOPS": round(tops, 2), "frac_of_peak": round(tops / INT8_PEAK_TOPS, 5)})
+    for m in mats.values():
+        m.free()
+    g.close()
+    return out
 
 
 def attention_bench(reps=200):
@@ -397,7 +451,8 @@ def main():
     ap.add_argument("--skip-decode", action="store_true")
     ap.add_argument("--copy-mb", type=int, default=0, help="also time a device copy of this many MiB")
     ap.add_argument("--skip-stream-ref", action="store_true", help="skip the library read/copy bandwidth reference")
-    ap.add_argument("--only", choices=["gemv", "decode", "prefill", "hybrid", "ternary", "ternary32", "attention"],
+    ap.add_argument("--only", choices=["gemv", "decode", "prefill", "hybrid", "ternary", "ternary32", "attention",
+                                       "gemm32"],
                     default=None,
                     help="run one leg (for profiling); the JSON line then carries that leg only")
     ap.add_argument("--prefill-runs", type=int, default=5)
@@ -429,6 +484,9 @@ def main():
         return
     if args.only == "ternary32":
         print(json.dumps({"decode_c5_batch32": ternary_batch_bench(args.decode_runs)}))
+        return
+    if args.only == "gemm32":
+        print(json.dumps({"decode_c5_batch32_gemms": decode_batch_gemms()}))
         return
     if args.only in ("hybrid", "ternary"):
         fn = hybrid_decode_bench if args.only == "hybrid" else ternary_decode_bench
