@@ -114,6 +114,21 @@ _SIGS = {
 _lib = None
 
 
+def _share_hip_runtime():
+    """Load torch's HIP runtime ahead of libvgx when torch is installed.
+
+    torch's HIP libraries request `libamdhip64.so` from their own directory;
+    libvgx requests `libamdhip64.so.7`, the soname that both runtimes carry.
+    In that order libvgx binds to the runtime torch brought in. In the other
+    order torch finds no loaded library named `libamdhip64.so`, maps a second
+    copy of the runtime, and that copy cannot open the GPU that the first one
+    holds: torch then reports that no HIP GPUs are available."""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 def load():
     """The loaded library; raises when it has not been built."""
     global _lib
@@ -121,6 +136,7 @@ def load():
         if not os.path.exists(LIB_PATH):
             raise RuntimeError("libvgx is not built (%s): run `make -C vc4-gles2-inference_amd` "
                                "or __graft_entry__.build()" % LIB_PATH)
+        _share_hip_runtime()
         L = ctypes.CDLL(LIB_PATH)
         for name, (res, args) in _SIGS.items():
             fn = getattr(L, name)
