@@ -166,6 +166,31 @@ def cpu_baseline(seconds):
 GRAPHS = True  # decode steps replayed as one HIP graph (--no-graphs: individual launches)
 
 
+def decode_step_bytes(blob, kv_bits, n_prompt, n_gen, nseq=1):
+    """Algorithmic HBM bytes of one timed decode step: every tensor a step
+    reads once whatever the batch (each layer's matrices, their scale planes
+    and norm weights, the LM head -- rendered from the embedding when the
+    container has no head tiles), plus per sequence its embedding row and, in
+    every attention layer, the K and V rows it reads and the row it writes.
+    The timed steps attend over n_prompt + 1 .. n_prompt + n_gen - 1 rows, so
+    the KV term is taken at their mean, n_prompt + n_gen / 2."""
+    from vgx import mmcf
+    c = mmcf.Container(blob)
+    s = c.spec
+    weights = sum(len(r.body) for r in c.records if r.kind not in (mmcf.T_EMB, mmcf.T_EMB_SCALE))
+    if not any(r.kind == mmcf.T_LOGITS for r in c.records):
+        weights += s.vocab * s.dim + s.vocab * 4
+    attn_layers = sum(1 for t in (s.layer_types or ["attn"] * s.layers) if t == "attn")
+    kv_row = 2 * s.kv_heads * s.head_dim * kv_bits // 8
+    per_seq = s.dim + 4 + attn_layers * kv_row * (n_prompt + n_gen / 2.0 + 1)
+    return int(weights + nseq * per_seq)
+
+
+def decode_roofline(step_bytes, ms_step):
+    gbps = step_bytes / (ms_step * 1e-3) / 1e9
+    return {"bytes_per_step": step_bytes, "achieved_GBps": round(gbps, 1), "frac_of_hbm_peak": round(gbps / HBM_PEAK_GBS, 4)}
+
+
 def model_decode(name, spec, scheme, kv_bits, n_prompt, n_gen, runs):
     """A seeded synthetic model through the engine: n_prompt prompt tokens
     (batched prefill) then n_gen greedy tokens; decode tokens/s over the
@@ -189,7 +214,8 @@ def model_decode(name, spec, scheme, kv_bits, n_prompt, n_gen, runs):
     return blob, prompt, toks, {
         "model": name, "prompt": n_prompt, "gen": n_gen, "seq": spec.seq, "kv": "q%d" % kv_bits,
         "tokens_per_s": round(1000.0 / ms_tok, 1), "ms_per_token": round(ms_tok, 4),
-        "prefill_ms": round(float(np.median(pf)), 3), "runs": runs, "graphs": GRAPHS}
+        "prefill_ms": round(float(np.median(pf)), 3), "runs": runs, "graphs": GRAPHS,
+        "hbm": decode_roofline(decode_step_bytes(blob, kv_bits, n_prompt, n_gen), ms_tok)}
 
 
 def decode_bench(runs):
@@ -239,7 +265,8 @@ def ternary_batch_bench(runs, nseq=32):
     return {"model": "0.5B Llama-shaped t3 (per-row ternary P(0)=0.4), seed 0", "sequences": nseq, "prompt": 128,
             "gen": 256, "seq": 512, "kv": "q16", "tokens_per_s": round(nseq * 1000.0 / ms_step, 1),
             "ms_per_step": round(ms_step, 4), "prefill_ms_all_sequences": round(float(np.median(pf)), 2),
-            "runs": runs, "gemm_int8_peak_TOPS": INT8_PEAK_TOPS, "gemms": decode_batch_gemms()}
+            "runs": runs, "hbm": decode_roofline(decode_step_bytes(blob, 16, 128, 256, nseq), ms_step),
+            "gemm_int8_peak_TOPS": INT8_PEAK_TOPS, "gemms": decode_batch_gemms()}
 
 
 def decode_batch_gemms(reps=200):

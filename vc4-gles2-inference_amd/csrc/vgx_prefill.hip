@@ -639,10 +639,13 @@ GemmFn pick(int epi, int kind, int nw, bool rms, bool part) {
 }
 
 // Splits of K for a launch of one token tile whose row tiles leave most CUs
-// idle (the decode batch): enough workgroups to cover the CUs, at least four
-// k-steps (one per wave) a split; 1 = no split.
+// idle (the decode batch) and whose rows are longer than 32 k-steps (four a
+// wave of an 8-wave workgroup): enough workgroups to cover the CUs, at least
+// four k-steps (one per wave) a split; 1 = no split.  Up to 32 k-steps the
+// whole row in one 8-wave workgroup beats the split and its epilogue launch
+// (C5 batch-32 qkv, 1280 x 1024: 5.7 against 8.3 us).
 int k_splits(int tiles_x, int tiles_y, int nsteps, int num_cu) {
-    if (tiles_y != 1 || tiles_x >= num_cu / 2) return 1;
+    if (tiles_y != 1 || tiles_x >= num_cu / 2 || nsteps <= 32) return 1;
     return std::max(1, std::min({num_cu / tiles_x, nsteps / 4, kMaxSplit}));
 }
 

@@ -6,7 +6,9 @@ import numpy as np
 
 from . import lib as _l
 
-LIB_PATH = os.path.join(_l.PKG, "lib", "libvgx_engine.so")
+# VGX_ENGINE_LIB names another build of the engine library; by default the
+# in-tree build.
+LIB_PATH = os.environ.get("VGX_ENGINE_LIB") or os.path.join(_l.PKG, "lib", "libvgx_engine.so")
 CLI_PATH = os.path.join(_l.PKG, "bin", "engine_mm3")
 
 _P = ctypes.c_void_p
