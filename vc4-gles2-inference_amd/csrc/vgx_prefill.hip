@@ -26,8 +26,9 @@
 // weight operands stream from global memory 4 steps ahead.  Loading the A
 // operands straight into the matrix-core layout made every load instruction
 // touch 32 token rows 2 bytes x cols apart; on MI355X that cost up to 3.4 us
-// per 32-token launch.  Wave 0 adds the other waves' partial sums (exact
-// integers) before the epilogue.  Epilogues restate the batch-1 GEMV's fp32
+// per 32-token launch.  The waves leave their partial sums (exact integers)
+// in LDS once and every thread adds them for its share of the tile's outputs
+// and runs the epilogue for those.  Epilogues restate the batch-1 GEMV's fp32
 // expressions: q16 store (+ residual, one rounding), the SwiGLU gate over W1
 // and W3, and the two-half residual add of the split w2.  q4 folds each
 // 32-column group's scale and minimum in after its k-step (one MFMA k-step =
