@@ -819,6 +819,42 @@ __global__ void __launch_bounds__(kThreads) attn_group_kernel(const AttnDev A, c
     };
     if (wave < nq) q_load(wave);
 
+    // The V rows of a round, staged in LDS: rows c0*kChunk .. of the head's
+    // plane are contiguous, so the round is one byte range read in 16-byte
+    // pieces, kVStage a thread at most.  Rows at or past npmax read zero; the
+    // own row (sequences mode) comes from its LDS copy, as its cache row is
+    // being written.  The first round's pieces are issued after the query
+    // and own-row inputs (loads return in order: issued first, they would
+    // hold up the query prep) and arrive during the scores and the stats.
+    uint8_t* const vs = smem + g.o_vs;  // [rc * kChunk][pstride]
+    const int per_row = A.pstride / 16;
+    uint4 vst[kVStage];
+    int vs_n = 0;  // pieces of the round in flight
+    auto stage_load = [&](int c0) {
+        const int row0 = c0 * kChunk;
+        vs_n = (min(row0 + g.rc * kChunk, npmax) - row0) * per_row;
+        const int base = row0 * A.pstride;
+#pragma unroll
+        for (int k = 0; k < kVStage; ++k)
+            if (k * kThreads < vs_n)
+                vst[k] = __builtin_bit_cast(
+                    uint4, __builtin_amdgcn_raw_buffer_load_b128(vrs, base + 16 * min(tid + k * kThreads, vs_n - 1), 0, 0));
+    };
+    auto stage_store = [&](int c0) {
+        const int own_piece = own ? (npmax - 1 - c0 * kChunk) * per_row : -1;
+#pragma unroll
+        for (int k = 0; k < kVStage; ++k) {
+            const int i = tid + k * kThreads;
+            if (k * kThreads < vs_n && i < vs_n) {
+                uint4 x = vst[k];
+                if (i >= own_piece && i < own_piece + per_row && own_piece >= 0)
+                    x = reinterpret_cast<const uint4*>(vpk)[i - own_piece];
+                reinterpret_cast<uint4*>(vs)[i] = x;
+            }
+        }
+    };
+    stage_load(0);
+
     // the query planes' words past the row stay zero, so the scores need no mask
     for (int i = tid; i < nq * g.qws; i += kThreads) qhw[i] = qlw[i] = 0;
     __syncthreads();
@@ -969,39 +1005,6 @@ __global__ void __launch_bounds__(kThreads) attn_group_kernel(const AttnDev A, c
     }
     __syncthreads();
 
-    // The V rows of a round, staged in LDS: rows c0*kChunk .. of the head's
-    // plane are contiguous, so the round is one byte range read in 16-byte
-    // pieces, kVStage a thread at most.  Rows at or past npmax read zero; the
-    // own row (sequences mode) comes from its LDS copy, as its cache row is
-    // being written.  The first round's pieces load while the stats run.
-    uint8_t* const vs = smem + g.o_vs;  // [rc * kChunk][pstride]
-    const int per_row = A.pstride / 16;
-    uint4 vst[kVStage];
-    int vs_n = 0;  // pieces of the round in flight
-    auto stage_load = [&](int c0) {
-        const int row0 = c0 * kChunk;
-        vs_n = (min(row0 + g.rc * kChunk, npmax) - row0) * per_row;
-        const int base = row0 * A.pstride;
-#pragma unroll
-        for (int k = 0; k < kVStage; ++k)
-            if (k * kThreads < vs_n)
-                vst[k] = __builtin_bit_cast(
-                    uint4, __builtin_amdgcn_raw_buffer_load_b128(vrs, base + 16 * min(tid + k * kThreads, vs_n - 1), 0, 0));
-    };
-    auto stage_store = [&](int c0) {
-        const int own_piece = own ? (npmax - 1 - c0 * kChunk) * per_row : -1;
-#pragma unroll
-        for (int k = 0; k < kVStage; ++k) {
-            const int i = tid + k * kThreads;
-            if (k * kThreads < vs_n && i < vs_n) {
-                uint4 x = vst[k];
-                if (i >= own_piece && i < own_piece + per_row && own_piece >= 0)
-                    x = reinterpret_cast<const uint4*>(vpk)[i - own_piece];
-                reinterpret_cast<uint4*>(vs)[i] = x;
-            }
-        }
-    };
-    stage_load(0);
 
     // --- stats (att_stats): the max per query vector (a wave each), the
     // exponentials (+0.0 to the end of the last chunk), chunk sums in position
