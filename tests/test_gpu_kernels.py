@@ -199,7 +199,9 @@ def test_group_and_logits_argmax(gpu):
     assert np.array_equal(host(g.gemv_f32(dev(xf))), wantf)
 
 
-@pytest.mark.parametrize("dim", [768, 1024, 64, 100])
+# rows held in registers up to 2048 values (per-thread elements <= 8), reread
+# above; 33 and 100 leave the last slices short
+@pytest.mark.parametrize("dim", [768, 1024, 64, 100, 33, 2048, 2049, 4096])
 def test_rmsnorm(gpu, dim):
     rng = np.random.default_rng(dim)
     for scale in (256, 4000):
@@ -207,6 +209,11 @@ def test_rmsnorm(gpu, dim):
         w = o.quantize_act(rng.uniform(0.5, 1.5, dim).astype(np.float32))
         for eps in (1e-5, 1e-6):
             assert np.array_equal(host(gpu.rmsnorm(dev(x), dev(w), eps)), o.rmsnorm(x, w, eps))
+    xs = np.clip(rng.standard_normal((3, dim)) * 3000, -32768, 32767).astype(np.int16)
+    xs[1, :] = 32767
+    got = host(gpu.rmsnorm_batch(dev(xs), dev(w), 1e-5))
+    for t in range(3):
+        assert np.array_equal(got[t], o.rmsnorm(xs[t], w, 1e-5)), t
 
 
 def _rms_case(rng, dim, scale):

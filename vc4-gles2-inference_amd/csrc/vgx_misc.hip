@@ -19,41 +19,66 @@ __device__ __forceinline__ int q16_round(float v) {
 // rms_stats_split's 32 partial sums of v^2 over contiguous slices of
 // ceil(dim/32) values, each on the 1/4096 grid (P = sum x^2 in Q units, stored
 // value floor(P/16 + 1/2)), their total ss, inv = inversesqrt(ss/dim + eps),
-// y = q16(x * inv * w).  One workgroup per row of x (rows `dim` apart).
+// y = q16(x * inv * w).  One workgroup per row of x (rows `dim` apart): slice
+// p is 8 threads, thread `sub` taking elements p*per + sub + 8k.  REG (dim up
+// to 2048, at most kNormRegs elements a thread): every x and w value is
+// loaded at the start and kept in registers for the output, so the row is
+// read once.  The slices' partials meet in LDS once and every wave adds the
+// 32 itself (exact integers, so any order gives the same total).
+constexpr int kNormRegs = 8;
+
+template <bool REG>
 __global__ void __launch_bounds__(256) rmsnorm_kernel(const int16_t* x, const int16_t* w, int dim,
                                                        float eps, int16_t* y) {
     __shared__ long long part[32];
-    __shared__ float s_inv;
     x += (size_t)blockIdx.x * dim;
     y += (size_t)blockIdx.x * dim;
     const int per = (dim + 31) / 32;
-    const int tid = threadIdx.x;
-    // 8 threads per partial slice
-    {
-        const int p = tid >> 3, sub = tid & 7;
-        long long P = 0;
-        for (int k = sub; k < per; k += 8) {
-            const int i = p * per + k;
-            if (i < dim) P += (long long)x[i] * x[i];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int p = tid >> 3, sub = tid & 7, i0 = p * per + sub;
+    auto in = [&](int k) { return sub + 8 * k < per && i0 + 8 * k < dim; };
+    int xr[kNormRegs], wr[kNormRegs];
+    long long P = 0;
+    if (REG) {
+#pragma unroll
+        for (int k = 0; k < kNormRegs; ++k) {
+            const int i = min(i0 + 8 * k, dim - 1);
+            xr[k] = x[i];
+            wr[k] = w[i];
         }
-        for (int o = 4; o >= 1; o >>= 1) P += __shfl_xor(P, o, 64);
-        if (sub == 0) part[p] = (P + 8) >> 4;
+#pragma unroll
+        for (int k = 0; k < kNormRegs; ++k)
+            if (in(k)) P += (long long)xr[k] * xr[k];
+    } else {
+        for (int k = 0; sub + 8 * k < per; ++k)
+            if (in(k)) P += (long long)x[i0 + 8 * k] * x[i0 + 8 * k];
     }
+    for (int o = 4; o >= 1; o >>= 1) P += __shfl_xor(P, o, 64);
+    if (sub == 0) part[p] = (P + 8) >> 4;
     __syncthreads();
-    if (tid == 0) {
-        long long tot = 0;
-        for (int p = 0; p < 32; ++p) tot += part[p];
-        const float ss = (float)tot / 4096.0f;
-        s_inv = (float)(1.0 / sqrt((double)(ss / (float)dim + eps)));
-    }
-    __syncthreads();
-    const float inv = s_inv;
-    for (int i = tid; i < dim; i += blockDim.x) {
-        const float xv = (float)x[i] / 256.0f;
-        const float wv = (float)w[i] / 256.0f;
+    long long tot = lane < 32 ? part[lane] : 0;
+    for (int o = 32; o >= 1; o >>= 1) tot += __shfl_xor(tot, o, 64);
+    const float ss = (float)tot / 4096.0f;
+    const float inv = (float)(1.0 / sqrt((double)(ss / (float)dim + eps)));
+    auto put = [&](int i, int xi, int wi) {
+        const float xv = (float)xi / 256.0f;
+        const float wv = (float)wi / 256.0f;
         const float v = (xv * inv) * wv;
         y[i] = (int16_t)q16_round(v * 256.0f);
+    };
+    if (REG) {
+#pragma unroll
+        for (int k = 0; k < kNormRegs; ++k)
+            if (in(k)) put(i0 + 8 * k, xr[k], wr[k]);
+    } else {
+        for (int k = 0; sub + 8 * k < per; ++k)
+            if (in(k)) put(i0 + 8 * k, x[i0 + 8 * k], w[i0 + 8 * k]);
     }
+}
+
+// The instance for a row of dim values.
+void (*rmsnorm_for(int dim))(const int16_t*, const int16_t*, int, float, int16_t*) {
+    return (dim + 31) / 32 <= 8 * kNormRegs ? rmsnorm_kernel<true> : rmsnorm_kernel<false>;
 }
 
 // Session::embedding, q8 rows (engine/src/session.cpp:362-365).  Row
@@ -148,7 +173,7 @@ int vgx_rmsnorm(vgx_ctx* ctx, int dim, const int16_t* x, const int16_t* w, float
     if (!ctx || !x || !w || !y) return vgx_fail(VGX_EINVAL, "vgx_rmsnorm: NULL argument");
     if (dim <= 0 || dim > 65536) return vgx_fail(VGX_EINVAL, "vgx_rmsnorm: dim outside 1..65536");
     VGX_HIP(hipSetDevice(ctx->device));
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(256), 0, ctx->stream, x, w, dim, eps, y);
+    hipLaunchKernelGGL(rmsnorm_for(dim), dim3(1), dim3(256), 0, ctx->stream, x, w, dim, eps, y);
     VGX_LAUNCH_CHECK("rmsnorm launch");
     return VGX_OK;
 }
@@ -169,7 +194,7 @@ int vgx_rmsnorm_batch(vgx_ctx* ctx, int ntok, int dim, const int16_t* x, const i
     if (dim <= 0 || dim > 65536) return vgx_fail(VGX_EINVAL, "vgx_rmsnorm_batch: dim outside 1..65536");
     if (ntok <= 0 || ntok > 65535) return vgx_fail(VGX_EINVAL, "vgx_rmsnorm_batch: ntok outside 1..65535");
     VGX_HIP(hipSetDevice(ctx->device));
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(ntok), dim3(256), 0, ctx->stream, x, w, dim, eps, y);
+    hipLaunchKernelGGL(rmsnorm_for(dim), dim3(ntok), dim3(256), 0, ctx->stream, x, w, dim, eps, y);
     VGX_LAUNCH_CHECK("rmsnorm launch");
     return VGX_OK;
 }
