@@ -228,13 +228,15 @@ def test_split_k_decode_batch(gpu, kind, rows, cols, ntok):
         assert np.array_equal(got_r[t], o.store(oracle_rowval(m, xn))), t
 
 
-@pytest.mark.parametrize("kind,rows,cols", [("t3", 1024, 1024), ("q8", 768, 2432), ("q4", 768, 768)])
+@pytest.mark.parametrize("kind,rows,cols", [("t3", 1024, 1024), ("q8", 768, 2432), ("q4", 768, 768),
+                                            ("t3", 1024, 4096), ("q8", 1040, 2432)])
 @pytest.mark.parametrize("ntok", [1, 32, 40])
 def test_gemm_norm_equals_gemm_then_rmsnorm(gpu, kind, rows, cols, ntok):
     # the GEMM that writes the residual stream and the RMSNorm of its rows:
-    # in the split-K epilogue launch (32 rows or fewer) or as a launch of its
-    # own (40), the same bytes as vgx_gemm / vgx_gemm_add_split then
-    # vgx_rmsnorm_batch, and the oracle's rows
+    # in the split-K epilogue launch (32 rows or fewer and rows longer than 32
+    # k-steps: norm slices of 24, 32 and 33 values) or as a launch of its own
+    # (40 rows, or K = 1024), the same bytes as vgx_gemm / vgx_gemm_add_split
+    # then vgx_rmsnorm_batch, and the oracle's rows
     rng = np.random.default_rng(rows + ntok)
     m = MK[kind](rng, rows, cols)
     W = gpu.upload(m)

@@ -344,6 +344,9 @@ __global__ void __launch_bounds__(256) argmax_keys_kernel(const unsigned long lo
                                                           const StepTail T) {
     __shared__ unsigned long long s_k[4];
     __shared__ int s_tok;
+    // the position (read before the keys: only this launch writes it, at its
+    // end) so the bookkeeping below waits for no further round trip
+    const int p = T.pos && threadIdx.x == 0 ? *T.pos : 0;
     unsigned long long key = 0ull;
     for (int i = threadIdx.x; i < n; i += blockDim.x) key = keys[i] > key ? keys[i] : key;
     for (int o = 32; o >= 1; o >>= 1) {
@@ -359,7 +362,6 @@ __global__ void __launch_bounds__(256) argmax_keys_kernel(const unsigned long lo
         if (T.pos) {
             // the decode step's bookkeeping: the token joins the history at
             // position *pos + 1, and the position advances
-            const int p = *T.pos;
             if (p + 1 >= 0 && p + 1 < T.hist_len) T.hist[p + 1] = tok;
             *T.pos = p + 1;
             s_tok = tok;
@@ -527,6 +529,20 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
     // of each per thread, into LDS (after the planes); the statistics and the
     // normalised planes below read the copies (measured: the second global
     // read of x and the weight cost ~1 us per launch on the decode shapes)
+    //
+    // RMSNorm statistics (rms_stats_split, engine/src/gpu_upload.cpp:280-365):
+    // 32 partial sums of x^2 over contiguous slices of ceil(K/32) values, each
+    // stored as floor(P/16 + 1/2).  When K is a multiple of 256 (a slice is
+    // whole 8-value pieces of the copy; at most kRmsPieces of them), each
+    // thread's sum of squares over the piece it copied goes to LDS with the
+    // copy, and after the copy's barrier lane p of every wave adds slice p's
+    // pieces and every wave the rounded slices (exact integers): no second
+    // pass over the copy and no second barrier.  Otherwise 8 lanes per slice
+    // from the copy, then every thread adds the 32 slices.
+    constexpr int kRmsPieces = 512;
+    __shared__ long long s_rms[32];
+    __shared__ long long s_rpiece[kRmsPieces];
+    const bool rms_fast = XM == X_RMS && K % 256 == 0 && K / 8 <= kRmsPieces;
     lmem_t<int16_t>* xr = nullptr;
     lmem_t<int16_t>* wr = nullptr;
     if (XM == X_RMS) {
@@ -537,14 +553,19 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
             const u32x4_t b = gld(reinterpret_cast<const u32x4_t*>(L.rw + i));
             *reinterpret_cast<lmem_t<u32x4_t>*>(xr + i) = a;
             *reinterpret_cast<lmem_t<u32x4_t>*>(wr + i) = b;
+            if (rms_fast) {
+                long long P = 0;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const long long lo = (int16_t)(a[k] & 0xFFFFu), hi = (int16_t)(a[k] >> 16);
+                    P += lo * lo + hi * hi;
+                }
+                s_rpiece[i >> 3] = P;
+            }
         }
         __syncthreads();
     }
-    // RMSNorm statistics (rms_stats_split, engine/src/gpu_upload.cpp:280-365):
-    // 32 partial sums of x^2 over contiguous slices of ceil(K/32) values, each
-    // stored as floor(P/16 + 1/2); 8 lanes per slice.
-    __shared__ long long s_rms[32];
-    if (XM == X_RMS) {
+    if (XM == X_RMS && !rms_fast) {
         const int per = (K + 31) / 32;
         const int p = threadIdx.x >> 3, sub = threadIdx.x & 7;
         long long P = 0;
@@ -558,11 +579,23 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
         for (int o = 4; o >= 1; o >>= 1) P += shfl_xor(P, o);
         if (sub == 0) s_rms[p] = (P + 8) >> 4;
     }
-    __syncthreads();
+    if (!rms_fast) __syncthreads();
     float rinv = 0.0f;
     if (XM == X_RMS) {
         long long tot = 0;
-        for (int p = 0; p < 32; ++p) tot += s_rms[p];
+        if (rms_fast) {
+            const int pps = K / 256;  // pieces per slice
+            long long t = 0;
+            if (lane < 32) {
+                long long P = 0;
+                for (int k = 0; k < pps; ++k) P += s_rpiece[lane * pps + k];
+                t = (P + 8) >> 4;
+            }
+            for (int o = 32; o >= 1; o >>= 1) t += shfl_xor(t, o);
+            tot = t;
+        } else {
+            for (int p = 0; p < 32; ++p) tot += s_rms[p];
+        }
         const float ss = (float)tot / 4096.0f;
         rinv = (float)(1.0 / sqrt((double)(ss / (float)K + L.eps)));
     }
