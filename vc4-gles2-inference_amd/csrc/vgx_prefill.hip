@@ -668,13 +668,16 @@ int workspace(vgx_ctx* ctx, size_t bytes, long long** out) {
     return VGX_OK;
 }
 
-// Waves per workgroup: 4 when the launch has at least two tiles per CU;
-// otherwise (a few row tiles of a decode batch) 8 when the row has more than
+// Waves per workgroup: 4 when the launch has at least one tile per CU (two
+// 4-wave workgroups fit a CU's registers where one 8-wave workgroup does, so
+// up to two tiles a CU run in one round: the 256-token qkv, 384 tiles, took
+// 0.8% less of the C3 prefill than with 8 waves in two rounds); otherwise (a
+// few row tiles: a decode batch, a short prompt) 8 when the row has more than
 // 16 k-steps, so the tiles' k-steps are spread over more waves.  (16 waves
 // would cap a lane at 128 registers and spill the operands in flight; 8 waves
 // with four steps in flight keep as many bytes in flight per CU.)
 int waves_for(int tiles, int nsteps, int num_cu) {
-    return tiles < 2 * num_cu && nsteps > 16 ? 8 : 4;
+    return tiles < num_cu && nsteps > 16 ? 8 : 4;
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
