@@ -220,7 +220,8 @@ int vgx_logits_argmax_rms_noalloc(vgx_ctx* ctx, const vgx_group* g, const int16_
  *     position attends to its prefix (att_stage, att_scores_batch,
  *     att_stats_row, att_v_row: engine/src/gpu_attn.cpp:433-532).
  * A vgx_gemm, vgx_gemm_add_split or vgx_ffn_gate_batch launch of at most 32
- * tokens whose row tiles leave most CUs idle splits K over up to 8 workgroups
+ * tokens whose row tiles leave most CUs idle and whose rows are longer than
+ * 32 k-steps (of 32 columns) splits K over up to 8 workgroups
  * and adds their exact integer sums in a second launch; the sums live in a
  * workspace of the context (hipMalloc at the first such call, at least 8 MiB,
  * grown on demand, freed by vgx_ctx_destroy).  Results are identical either
@@ -244,6 +245,13 @@ int vgx_ffn_gate_batch_rms(vgx_ctx* ctx, const vgx_mat* W1, const vgx_mat* W3, i
                            const int16_t* rms_w, float eps, int hs, int16_t* h);
 int vgx_embed_q8_batch(vgx_ctx* ctx, const int8_t* emb, const float* emb_scale, int vocab, int dim, int ntok,
                        const int* tokens, int16_t* x);
+/* The embedding rows of a batch and their RMSNorm: per token vgx_embed_q8
+ * into x (the residual stream), then vgx_rmsnorm(x, rms_w, eps) into y, in
+ * one launch with identical bytes -- Session::embedding
+ * (engine/src/session.cpp:362-365) and the first layer's attention norm
+ * (:1483).  rms_w: dim q16 values. */
+int vgx_embed_q8_rms_batch(vgx_ctx* ctx, const int8_t* emb, const float* emb_scale, int vocab, int dim, int ntok,
+                           const int* tokens, int16_t* x, const int16_t* rms_w, float eps, int16_t* y);
 /* The other side of the same fusion: a GEMM that writes the residual stream
  * also normalises the rows it wrote, per token,
  *   vgx_gemm_norm            vgx_gemm, then vgx_rmsnorm_batch(y, rms_w, eps) -> yn

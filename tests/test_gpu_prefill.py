@@ -132,6 +132,23 @@ def test_rmsnorm_and_embed_batch(gpu):
         assert np.array_equal(got[t], o.embed_q8(emb, es, int(tk))), t
 
 
+@pytest.mark.parametrize("dim", [768, 1024, 100, 2304])
+def test_embed_rms_batch(gpu, dim):
+    # the embedding rows and their RMSNorm in one launch (dim up to 2048; 2304
+    # takes the two launches): the oracle's embedding, then its rmsnorm
+    rng = np.random.default_rng(dim)
+    emb = rng.integers(-127, 128, (500, dim)).astype(np.int8)
+    es = rng.uniform(1e-4, 1.05, 500).astype(np.float32)  # the largest values clamp at the int16 rail
+    w = o.quantize_act(rng.uniform(0.5, 1.5, dim).astype(np.float32))
+    toks = np.array([0, 499, 17, 17, 250, 3, 0], np.int32)
+    x, y = gpu.embed_q8_rms_batch(dev(emb), dev(es), dev(toks), dev(w), 1e-5)
+    x, y = host(x), host(y)
+    for t, tk in enumerate(toks):
+        e = o.embed_q8(emb, es, int(tk))
+        assert np.array_equal(x[t], e), t
+        assert np.array_equal(y[t], o.rmsnorm(e, w, 1e-5)), t
+
+
 @pytest.mark.parametrize("kv_bits", [16, 8])
 def test_attention_batch_equals_serial(gpu, kv_bits):
     # MiniMind3 heads: 20 positions one at a time against batches of 7 and 13

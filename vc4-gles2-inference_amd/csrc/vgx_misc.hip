@@ -81,6 +81,59 @@ void (*rmsnorm_for(int dim))(const int16_t*, const int16_t*, int, float, int16_t
     return (dim + 31) / 32 <= 8 * kNormRegs ? rmsnorm_kernel<true> : rmsnorm_kernel<false>;
 }
 
+// The q8 embedding row of token[blockIdx.x] (embed_q8_kernel's arithmetic)
+// into x and its RMSNorm (rmsnorm_kernel's) into y, in one workgroup per row:
+// rmsnorm_kernel<true>'s element mapping with the row formed in registers
+// (rows of up to 2048 values), the norm weight loaded with the token.
+__global__ void __launch_bounds__(256) embed_rms_kernel(const int8_t* emb, const float* scale, int vocab, int dim,
+                                                         const int* token, const int16_t* w, float eps, int16_t* x,
+                                                         int16_t* y) {
+    __shared__ long long part[32];
+    x += (size_t)blockIdx.x * dim;
+    y += (size_t)blockIdx.x * dim;
+    const int per = (dim + 31) / 32;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int p = tid >> 3, sub = tid & 7, i0 = p * per + sub;
+    auto in = [&](int k) { return sub + 8 * k < per && i0 + 8 * k < dim; };
+    int wr[kNormRegs];
+#pragma unroll
+    for (int k = 0; k < kNormRegs; ++k) wr[k] = w[min(i0 + 8 * k, dim - 1)];
+    int tok = token[blockIdx.x];
+    tok = min(max(tok, 0), vocab - 1);
+    const float sc = scale[tok];
+    const int8_t* er = emb + (size_t)tok * dim;
+    int xr[kNormRegs];
+#pragma unroll
+    for (int k = 0; k < kNormRegs; ++k) {
+        const float v = (float)er[min(i0 + 8 * k, dim - 1)] * sc;
+        float r = __builtin_rintf(v * 256.0f);
+        r = fminf(fmaxf(r, -32768.0f), 32767.0f);
+        xr[k] = (int)r;
+    }
+    long long P = 0;
+#pragma unroll
+    for (int k = 0; k < kNormRegs; ++k)
+        if (in(k)) {
+            P += (long long)xr[k] * xr[k];
+            x[i0 + 8 * k] = (int16_t)xr[k];
+        }
+    for (int o = 4; o >= 1; o >>= 1) P += __shfl_xor(P, o, 64);
+    if (sub == 0) part[p] = (P + 8) >> 4;
+    __syncthreads();
+    long long tot = lane < 32 ? part[lane] : 0;
+    for (int o = 32; o >= 1; o >>= 1) tot += __shfl_xor(tot, o, 64);
+    const float ss = (float)tot / 4096.0f;
+    const float inv = (float)(1.0 / sqrt((double)(ss / (float)dim + eps)));
+#pragma unroll
+    for (int k = 0; k < kNormRegs; ++k)
+        if (in(k)) {
+            const float xv = (float)xr[k] / 256.0f;
+            const float wv = (float)wr[k] / 256.0f;
+            const float v = (xv * inv) * wv;
+            y[i0 + 8 * k] = (int16_t)q16_round(v * 256.0f);
+        }
+}
+
 // Session::embedding, q8 rows (engine/src/session.cpp:362-365).  Row
 // blockIdx.y of x takes token[blockIdx.y].
 __global__ void embed_q8_kernel(const int8_t* emb, const float* scale, int vocab, int dim,
@@ -208,6 +261,23 @@ int vgx_embed_q8_batch(vgx_ctx* ctx, const int8_t* emb, const float* emb_scale, 
     hipLaunchKernelGGL(embed_q8_kernel, dim3(1, ntok), dim3(256), 0, ctx->stream, emb, emb_scale, vocab, dim, tokens,
                        x);
     VGX_LAUNCH_CHECK("embed launch");
+    return VGX_OK;
+}
+
+int vgx_embed_q8_rms_batch(vgx_ctx* ctx, const int8_t* emb, const float* emb_scale, int vocab, int dim, int ntok,
+                           const int* tokens, int16_t* x, const int16_t* rms_w, float eps, int16_t* y) {
+    if (!ctx || !emb || !emb_scale || !tokens || !x || !rms_w || !y)
+        return vgx_fail(VGX_EINVAL, "vgx_embed_q8_rms_batch: NULL argument");
+    if (vocab <= 0 || dim <= 0 || dim > 65536) return vgx_fail(VGX_EINVAL, "vgx_embed_q8_rms_batch: empty or oversized shape");
+    if (ntok <= 0 || ntok > 65535) return vgx_fail(VGX_EINVAL, "vgx_embed_q8_rms_batch: ntok outside 1..65535");
+    if ((dim + 31) / 32 > 8 * kNormRegs) {  // a row too long for the registers: the two launches
+        const int st = vgx_embed_q8_batch(ctx, emb, emb_scale, vocab, dim, ntok, tokens, x);
+        return st ? st : vgx_rmsnorm_batch(ctx, ntok, dim, x, rms_w, eps, y);
+    }
+    VGX_HIP(hipSetDevice(ctx->device));
+    hipLaunchKernelGGL(embed_rms_kernel, dim3(ntok), dim3(256), 0, ctx->stream, emb, emb_scale, vocab, dim, tokens,
+                       rms_w, eps, x, y);
+    VGX_LAUNCH_CHECK("embed + rmsnorm launch");
     return VGX_OK;
 }
 

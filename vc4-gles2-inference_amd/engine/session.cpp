@@ -386,13 +386,16 @@ struct vgx_engine {
         const float eps = m.rms_eps;
         if (n <= 0 || n > pcap) return fail(VGX_EINVAL, "prefill: batch outside 1.." + std::to_string(pcap));
         if (pos0 == 0 && conv && (st = vgx_conv_reset(conv))) return st;  // a new sequence
-        if ((st = vgx_embed_q8_batch(ctx, emb, emb_scale, m.vocab, D, n, toks_dev, bh))) return st;
+        // RMSNorm in the consuming GEMM up to 32 positions (one token tile:
+        // the normalisation runs once per row tile); above, on its own (the
+        // first layer's in the embedding launch)
+        const bool fuse = n <= 32;
+        st = fuse ? vgx_embed_q8_batch(ctx, emb, emb_scale, m.vocab, D, n, toks_dev, bh)
+                  : vgx_embed_q8_rms_batch(ctx, emb, emb_scale, m.vocab, D, n, toks_dev, bh, L[0].rms_att, eps, bxn);
+        if (st) return st;
         for (int l = 0; l < m.layers; ++l) {
             Layer& ly = L[l];
-            // RMSNorm in the consuming GEMM up to 32 positions (one token tile:
-            // the normalisation runs once per row tile); above, on its own
-            const bool fuse = n <= 32;
-            if (!fuse && (st = vgx_rmsnorm_batch(ctx, n, D, bh, ly.rms_att, eps, bxn))) return st;
+            if (!fuse && l > 0 && (st = vgx_rmsnorm_batch(ctx, n, D, bh, ly.rms_att, eps, bxn))) return st;
             const vgx_mat* in_mat = is_conv(l) ? ly.conv_in : ly.qkv;
             st = fuse ? vgx_gemm_rms(ctx, in_mat, n, bh, ly.rms_att, eps, nullptr, bqkv)
                       : vgx_gemm(ctx, in_mat, n, bxn, nullptr, bqkv);
@@ -496,12 +499,12 @@ struct vgx_engine {
         int st;
         const int D = m.dim;
         const float eps = m.rms_eps;
-        if ((st = vgx_embed_q8_batch(ctx, emb, emb_scale, m.vocab, D, nseq, toks_dev, bh))) return st;
-        // the first attention norm; every later norm comes out of the GEMM that
-        // writes the residual stream (wo: the FFN norm; w2: the next layer's
-        // attention norm, or the final norm after the last layer), so qkv, the
-        // gate and the head read normalised rows
-        if ((st = vgx_rmsnorm_batch(ctx, nseq, D, bh, L[0].rms_att, eps, bxn))) return st;
+        // the embedding rows with the first attention norm; every later norm
+        // comes out of the GEMM that writes the residual stream (wo: the FFN
+        // norm; w2: the next layer's attention norm, or the final norm after
+        // the last layer), so qkv, the gate and the head read normalised rows
+        if ((st = vgx_embed_q8_rms_batch(ctx, emb, emb_scale, m.vocab, D, nseq, toks_dev, bh, L[0].rms_att, eps, bxn)))
+            return st;
         for (int l = 0; l < m.layers; ++l) {
             Layer& ly = L[l];
             const int16_t* next_norm = l + 1 < m.layers ? L[l + 1].rms_att : rms_final;

@@ -406,6 +406,16 @@ class GPU:
                                               _ptr(out)))
         return out
 
+    def embed_q8_rms_batch(self, emb, emb_scale, tokens, rms_w, eps=1e-5):
+        """(embedding rows, their RMSNorm) of a batch of tokens, one launch."""
+        vocab, dim = emb.shape
+        n = tokens.numel()
+        x = torch.empty((n, dim), dtype=torch.int16, device=emb.device)
+        y = torch.empty((n, dim), dtype=torch.int16, device=emb.device)
+        _l.check(_l.load().vgx_embed_q8_rms_batch(self.ctx, _ptr(emb), _ptr(emb_scale), vocab, dim, n, _ptr(tokens),
+                                                  _ptr(x), _ptr(rms_w), ctypes.c_float(eps), _ptr(y)))
+        return x, y
+
     def matvec_rms(self, mat, x, rms_w, eps=1e-5, res=None, out=None):
         """rmsnorm(x, rms_w, eps) then matvec_add, one launch."""
         out = out if out is not None else torch.empty(mat.rows, dtype=torch.int16, device=x.device)

@@ -82,6 +82,7 @@ _SIGS = {
     "vgx_gemm_rms": (_I, [_P, _P, _I, _P, _P, ctypes.c_float, _P, _P]),
     "vgx_ffn_gate_batch_rms": (_I, [_P, _P, _P, _I, _P, _P, ctypes.c_float, _I, _P]),
     "vgx_embed_q8_batch": (_I, [_P, _P, _P, _I, _I, _I, _P, _P]),
+    "vgx_embed_q8_rms_batch": (_I, [_P, _P, _P, _I, _I, _I, _P, _P, _P, ctypes.c_float, _P]),
     "vgx_gemm_norm": (_I, [_P, _P, _I, _P, _P, _P, _P, ctypes.c_float, _P]),
     "vgx_gemm_add_split_norm": (_I, [_P, _P, _I, _I, _P, _P, _P, _P, ctypes.c_float, _P]),
     "vgx_kv_append_batch": (_I, [_P, _I, _I, _I, _P]),
