@@ -274,6 +274,23 @@ __device__ __forceinline__ double wave_sum_exact(double x) {
     return (readlane_d(x, 0) + readlane_d(x, 16)) + (readlane_d(x, 32) + readlane_d(x, 48));
 }
 
+// Compile-time loop: f(integral_constant<int, U>) for U = B .. E-1.
+template <int B, int E, class Fn>
+__device__ __forceinline__ void static_for(Fn&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+// The weight of position U of a chunk in every lane: lane 16r + n of lo holds
+// the weight of position n (of hi: 16 + n) in each row r of 16 lanes, and the
+// row broadcast (DPP row_newbcast) gives lane n of each row to the whole row.
+template <int U>
+__device__ __forceinline__ double chunk_w(double lo, double hi) {
+    return __builtin_amdgcn_mov_dpp(U < 16 ? lo : hi, 0x150 + (U & 15), 0xf, 0xf, false);
+}
+
 template <int KVB>
 __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t* kv, const int32_t* rtab,
                                                         const int16_t* qn, const int16_t* kn,
@@ -547,12 +564,15 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     __syncthreads();
     float iv;
     {
-        // lane l reads chunk sum l; the wave adds them in chunk order
+        // every thread adds the chunk sums in chunk order, eight read at a
+        // time (a +0.0 past the last chunk leaves the sum as it is)
         double sum = 0.0;
-        for (int c0 = 0; c0 < nch; c0 += 64) {
-            const double cv = csum[min(c0 + lane, A.nchmax - 1)];
-            const int nn = min(64, nch - c0);
-            for (int k = 0; k < nn; ++k) sum += readlane_d(cv, k);
+        for (int c0 = 0; c0 < nch; c0 += 8) {
+            double t[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) t[k] = c0 + k < nch ? csum[c0 + k] : 0.0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) sum += t[k];
         }
         const float fs = (float)sum;
         float qs = floorf(fs * 32.0f + 0.5f);
@@ -568,9 +588,10 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     // The weight of position t, p = e*iv (float) times the V grid unit: a +=
     // p*v with v = q*vunit, and p (24-bit mantissa) times q (at most 16 bits)
     // is exact in double, so fma(p*vunit, q, a) rounds exactly as the add of
-    // the product does.  Lane u < kChunk forms the weight of the chunk's
-    // position u; the wave reads it through readlane.  Positions past npos
-    // have weight zero (a + 0*q is a), so all 32 slots run without a branch.
+    // the product does.  Each row of 16 lanes forms the weights of the
+    // chunk's 32 positions in two registers and every position's weight
+    // reaches the row by a DPP row broadcast.  Positions past npos have
+    // weight zero (a + 0*q is a), so all 32 slots run without a branch.
     const double vunit_d = KVB == 16 ? 1.0 / 2048.0 : 1.0 / 16.0;
     for (int c0 = 0; c0 < nch; c0 += vC) {
         const int nr = min(vC, nch - c0);
@@ -580,8 +601,11 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
         if (more) v_chunk_load<KVB>(A, vrs, vE, slot < vC ? c0 + vC + slot : A.nchmax, vi, vnx);
         if (slot < nr) {
             const int c = c0 + slot;
-            const int tl = c * kChunk + (lane & (kChunk - 1));
-            const double w = tl < npos ? (double)((float)ep[tl] * iv) * vunit_d : 0.0;
+            // lane 16r + n: the weights of the chunk's positions n (lo) and
+            // 16 + n (hi), broadcast along the row to every lane in the chain
+            const int tlo = c * kChunk + (lane & 15), thi = tlo + 16;
+            double wlo = tlo < npos ? (double)((float)ep[tlo] * iv) * vunit_d : 0.0;
+            double whi = thi < npos ? (double)((float)ep[thi] * iv) * vunit_d : 0.0;
             // the last position of a launch that appends is pos: its V comes
             // from the LDS copy (its cache row is being written)
             if (own_row && c == nch - 1) {
@@ -594,17 +618,24 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
                 for (int u = 0; u < kChunk; ++u) vch[u] = u == uo ? own : vch[u];
             }
             // every slot, without a branch: past npos the weight is zero
+            // (the weight registers pass through the chain, so each position's
+            // broadcast follows the previous fma: hoisted, a chunk's 32
+            // broadcasts would not fit in registers)
             double a = 0.0, b = 0.0;
             if (vE == 2) {
-#pragma unroll
-                for (int u = 0; u < kChunk; ++u) {
-                    const double wu = readlane_d(w, u);
+                static_for<0, kChunk>([&](auto U) {
+                    constexpr int u = decltype(U)::value;
+                    asm volatile("" : "+v"(wlo), "+v"(whi), "+v"(a), "+v"(b));
+                    const double wu = chunk_w<u>(wlo, whi);
                     a = fma(wu, (double)v_lo<KVB>(vch[u]), a);
                     b = fma(wu, (double)v_hi<KVB>(vch[u]), b);
-                }
+                });
             } else {
-#pragma unroll
-                for (int u = 0; u < kChunk; ++u) a = fma(readlane_d(w, u), (double)v_lo<KVB>(vch[u]), a);
+                static_for<0, kChunk>([&](auto U) {
+                    constexpr int u = decltype(U)::value;
+                    asm volatile("" : "+v"(wlo), "+v"(whi), "+v"(a));
+                    a = fma(chunk_w<u>(wlo, whi), (double)v_lo<KVB>(vch[u]), a);
+                });
             }
             if (ve < hd) {
                 vpart[slot * hd + ve] = a;
@@ -733,23 +764,6 @@ __device__ __forceinline__ int vpk_word(const uint8_t* vpk, int vE, int i) {
 // A query vector's score row: position t at t + t/32 (one pad float per chunk,
 // so a lane per chunk reads distinct banks).
 __device__ __forceinline__ int fidx(int t) { return t + (t >> 5); }
-
-// Compile-time loop: f(integral_constant<int, U>) for U = B .. E-1.
-template <int B, int E, class Fn>
-__device__ __forceinline__ void static_for(Fn&& f) {
-    if constexpr (B < E) {
-        f(std::integral_constant<int, B>{});
-        static_for<B + 1, E>(f);
-    }
-}
-
-// The weight of position U of a chunk in every lane: lane 16r + n of lo holds
-// the weight of position n (of hi: 16 + n) in each row r of 16 lanes, and the
-// row broadcast (DPP row_newbcast) gives lane n of each row to the whole row.
-template <int U>
-__device__ __forceinline__ double chunk_w(double lo, double hi) {
-    return __builtin_amdgcn_mov_dpp(U < 16 ? lo : hi, 0x150 + (U & 15), 0xf, 0xf, false);
-}
 
 // VE: V elements per lane of the weighted-V pass, 2 above head_dim 64.  QG:
 // query vectors per work unit of that pass (2 for blocks of at most two).
