@@ -118,6 +118,9 @@ def test_attention_rails(gpu, bits, hd):
 LONG = [(8, 96, 4, 2, 320, (32, 129, 200, 257, 319)), (16, 128, 4, 2, 320, (32, 129, 200, 257, 319)),
         (8, 128, 4, 2, 320, (32, 129, 200, 257, 319)), (16, 256, 4, 2, 320, (32, 129, 200, 257, 319)),
         (8, 256, 4, 2, 320, (32, 129, 200, 257, 319)),
+        # KV q8 at head_dim 64 and 32: one round of the one-element plan up to
+        # 256 positions, the two-chunks-a-wave plan past it
+        (8, 64, 4, 2, 320, (32, 255, 257, 319)), (8, 32, 4, 2, 320, (255, 257, 319)),
         # MiniMind3 q4 / KV q8 at SEQ 768: 8 Q / 4 KV heads of 96, to the last row
         (8, 96, 8, 4, 768, (383, 511, 640, 767)),
         # MiniMind3 q8 / KV q16 at SEQ 768
@@ -126,9 +129,11 @@ LONG = [(8, 96, 4, 2, 320, (32, 129, 200, 257, 319)), (16, 128, 4, 2, 320, (32, 
 
 @pytest.mark.parametrize("bits,hd,heads,kvh,seq,positions", LONG)
 def test_attention_long_contexts(gpu, bits, hd, heads, kvh, seq, positions):
-    """Contexts of several rounds of the weighted-V pass (and, above head_dim
-    64, the two-elements-per-lane plan it switches to there), over random
-    cached rows, through both the appending and the reading entry points."""
+    """Contexts of several rounds of the weighted-V pass (and the plans it
+    switches to there: two elements a lane above head_dim 64; with a q8 cache
+    up to head_dim 128, two chunks a wave of four elements a lane), over
+    random cached rows, through both the appending and the reading entry
+    points."""
     dim = heads * hd
     rng = np.random.default_rng(bits * 7 + hd)
     rc, rs = o.rope_cos_sin(10000.0, hd, seq)

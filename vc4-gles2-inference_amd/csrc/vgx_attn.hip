@@ -232,6 +232,16 @@ __device__ __forceinline__ void v_chunk_load(const AttnDev& A, __amdgpu_buffer_r
         }
     }
 }
+// The pair plan's V loads (q8 cache, head_dim up to 128): the 32-bit field of
+// elements vi .. vi+3 (vi a multiple of 4) at position c*kChunk + u in
+// vch[u]; rows at or past npos read zero, as in v_chunk_load.
+__device__ __forceinline__ void v_pair_load(const AttnDev& A, __amdgpu_buffer_rsrc_t vrs, int c, int vi,
+                                            int (&vch)[kChunk]) {
+    const int base = c * kChunk * A.pstride + vi;
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u)
+        vch[u] = (int)__builtin_amdgcn_raw_buffer_load_b32(vrs, base + u * A.pstride, 0, 0);
+}
 // The first and second element of a loaded V field.
 template <int KVB>
 __device__ __forceinline__ int v_lo(int p) { return KVB == 16 ? (int)(int16_t)(p & 0xffff) : (int)(int8_t)(p & 0xff); }
@@ -391,6 +401,13 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     // (slot is wave-uniform; readfirstlane lets the compiler see it)
     const bool wide = A.vC2 > A.vC1 && nch > A.vC1;
     const int vE = wide ? 2 : 1, vG = wide ? A.vG2 : A.vG1, vC = wide ? A.vC2 : A.vC1;
+    // pair plan (q8 cache, head_dim up to 128, more chunks than one round of
+    // the one-element plan): every wave takes two chunks of a round, lanes
+    // 0..31 chunk 2*wave and lanes 32..63 chunk 2*wave + 1, four elements a
+    // lane from one 32-bit field, so one load per position serves two
+    // chunks: 16 chunks a round
+    const bool pair = KVB == 8 && hd <= 128 && nch > A.vC1;
+    const int pe = (lane & 31) * 4, pvi = min(pe, hd - 4), pch = 2 * wave + (lane >> 5);
     const int slot = __builtin_amdgcn_readfirstlane(wave / vG);
     const int ve = ((wave - slot * vG) * 64 + lane) * vE, vi = min(ve, hd - vE);
     uint4 kreg[KP];
@@ -408,7 +425,8 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     }
     // the K loads first: the scores wait for them, not for the V loads after
     asm volatile("" ::: "memory");
-    v_chunk_load<KVB>(A, vrs, vE, slot < vC ? slot : A.nchmax, vi, vch);
+    if (pair) v_pair_load(A, vrs, pch, pvi, vch);
+    else v_chunk_load<KVB>(A, vrs, vE, slot < vC ? slot : A.nchmax, vi, vch);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         keep(ke[c]);
@@ -593,6 +611,71 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     // reaches the row by a DPP row broadcast.  Positions past npos have
     // weight zero (a + 0*q is a), so all 32 slots run without a branch.
     const double vunit_d = KVB == 16 ? 1.0 / 2048.0 : 1.0 / 16.0;
+    if (pair) {
+        // the same arithmetic as the plans below -- a chain per element in
+        // position order, the round's chunk partials joined in chunk order --
+        // over two chunks a wave (lanes 32..63 the second); the DPP row
+        // broadcast stays inside a chunk (16-lane rows)
+        constexpr int kPC = 2 * (kThreads / 64);  // chunks a round
+        for (int c0 = 0; c0 < nch; c0 += kPC) {
+            const int nr = min(kPC, nch - c0);
+            const bool more = c0 + kPC < nch;
+            int vnx[kChunk];
+            if (more) v_pair_load(A, vrs, c0 + kPC + pch, pvi, vnx);
+            if (2 * wave < nr) {
+                const int c = c0 + pch;  // this lane's chunk (past nch: weights zero)
+                const int tlo = c * kChunk + (lane & 15), thi = tlo + 16, tmax = A.nchmax * kChunk - 1;
+                double wlo = tlo < npos ? (double)((float)ep[min(tlo, tmax)] * iv) * vunit_d : 0.0;
+                double whi = thi < npos ? (double)((float)ep[min(thi, tmax)] * iv) * vunit_d : 0.0;
+                // the last position of a launch that appends is pos: its V
+                // comes from the LDS copy (its cache row is being written)
+                if (own_row) {
+                    const int own = (int)*reinterpret_cast<const uint32_t*>(vpk + pvi);
+                    const int uo = c == nch - 1 ? npos - 1 - c * kChunk : -1;
+#pragma unroll
+                    for (int u = 0; u < kChunk; ++u) vch[u] = u == uo ? own : vch[u];
+                }
+                double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+                static_for<0, kChunk>([&](auto U) {
+                    constexpr int u = decltype(U)::value;
+                    asm volatile("" : "+v"(wlo), "+v"(whi), "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3));
+                    const double wu = chunk_w<u>(wlo, whi);
+                    const int x = vch[u];
+                    a0 = fma(wu, (double)(int8_t)(x & 0xff), a0);
+                    a1 = fma(wu, (double)(int8_t)((x >> 8) & 0xff), a1);
+                    a2 = fma(wu, (double)(int8_t)((x >> 16) & 0xff), a2);
+                    a3 = fma(wu, (double)(int8_t)((x >> 24) & 0xff), a3);
+                });
+                if (pe < hd && c < nch) {
+                    double* vp = vpart + (c - c0) * hd + pe;
+                    vp[0] = a0;
+                    vp[1] = a1;
+                    vp[2] = a2;
+                    vp[3] = a3;
+                }
+            }
+            __syncthreads();
+            const bool last = c0 + nr >= nch;
+            for (int i = tid; i < hd; i += kThreads) {
+                double sacc = c0 == 0 ? 0.0 : acc[i];
+                for (int r0 = 0; r0 < nr; r0 += 8) {
+                    double pv[8];
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) pv[k] = vpart[min(r0 + k, kPC - 1) * hd + i];
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) sacc += r0 + k < nr ? pv[k] : 0.0;
+                }
+                if (last) out[h * hd + i] = (int16_t)q16_round((float)sacc * 256.0f);
+                else acc[i] = sacc;
+            }
+            if (!last) __syncthreads();
+            if (more) {
+#pragma unroll
+                for (int u = 0; u < kChunk; ++u) vch[u] = vnx[u];
+            }
+        }
+        return;
+    }
     for (int c0 = 0; c0 < nch; c0 += vC) {
         const int nr = min(vC, nch - c0);
         // the next round's V values load while this round is summed
@@ -1225,7 +1308,9 @@ size_t attn_layout(AttnDev& A) {
     A.o_sc = take(2 * (size_t)A.seq);
     A.o_ep = take(8 * (size_t)A.nchmax * kChunk);
     A.o_csum = take(8 * (size_t)A.nchmax);
-    A.o_vpart = take(8 * (size_t)(A.vC1 > A.vC2 ? A.vC1 : A.vC2) * hd);
+    // (the pair plan of a q8 cache up to head_dim 128: 16 chunks a round)
+    const int vcm = std::max({A.vC1, A.vC2, A.kv_bits == 8 && hd <= 128 ? 2 * (kThreads / 64) : 0});
+    A.o_vpart = take(8 * (size_t)vcm * hd);
     A.o_acc = take(8 * (size_t)hd);
     return off;
 }
