@@ -118,9 +118,10 @@ def test_attention_rails(gpu, bits, hd):
 LONG = [(8, 96, 4, 2, 320, (32, 129, 200, 257, 319)), (16, 128, 4, 2, 320, (32, 129, 200, 257, 319)),
         (8, 128, 4, 2, 320, (32, 129, 200, 257, 319)), (16, 256, 4, 2, 320, (32, 129, 200, 257, 319)),
         (8, 256, 4, 2, 320, (32, 129, 200, 257, 319)),
-        # KV q8 at head_dim 64 and 32: one round of the one-element plan up to
-        # 256 positions, the two-chunks-a-wave plan past it
+        # KV q8 at head_dim 64 and 32, KV q16 at 64 and 32: one round of the
+        # one-element plan up to 256 positions, the two-chunks-a-wave plan past it
         (8, 64, 4, 2, 320, (32, 255, 257, 319)), (8, 32, 4, 2, 320, (255, 257, 319)),
+        (16, 64, 4, 2, 320, (32, 255, 257, 319)), (16, 32, 4, 2, 320, (255, 257, 319)),
         # MiniMind3 q4 / KV q8 at SEQ 768: 8 Q / 4 KV heads of 96, to the last row
         (8, 96, 8, 4, 768, (383, 511, 640, 767)),
         # MiniMind3 q8 / KV q16 at SEQ 768
@@ -130,8 +131,9 @@ LONG = [(8, 96, 4, 2, 320, (32, 129, 200, 257, 319)), (16, 128, 4, 2, 320, (32, 
 @pytest.mark.parametrize("bits,hd,heads,kvh,seq,positions", LONG)
 def test_attention_long_contexts(gpu, bits, hd, heads, kvh, seq, positions):
     """Contexts of several rounds of the weighted-V pass (and the plans it
-    switches to there: two elements a lane above head_dim 64; with a q8 cache
-    up to head_dim 128, two chunks a wave of four elements a lane), over
+    switches to there: two elements a lane above head_dim 64; up to 32 fields
+    of 32 bits a head -- head_dim 128 at q8, 64 at q16 -- two chunks a wave of
+    one field a lane), over
     random cached rows, through both the appending and the reading entry
     points."""
     dim = heads * hd

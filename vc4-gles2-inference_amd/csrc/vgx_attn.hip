@@ -232,12 +232,14 @@ __device__ __forceinline__ void v_chunk_load(const AttnDev& A, __amdgpu_buffer_r
         }
     }
 }
-// The pair plan's V loads (q8 cache, head_dim up to 128): the 32-bit field of
-// elements vi .. vi+3 (vi a multiple of 4) at position c*kChunk + u in
-// vch[u]; rows at or past npos read zero, as in v_chunk_load.
+// The pair plan's V loads (head_dim up to 32 fields of 32 bits: 64 at a q16
+// cache, 128 at q8): the 32-bit field of elements vi .. vi + 32/KVB - 1 (vi a
+// multiple of that) at position c*kChunk + u in vch[u]; rows at or past npos
+// read zero, as in v_chunk_load.
+template <int KVB>
 __device__ __forceinline__ void v_pair_load(const AttnDev& A, __amdgpu_buffer_rsrc_t vrs, int c, int vi,
                                             int (&vch)[kChunk]) {
-    const int base = c * kChunk * A.pstride + vi;
+    const int base = c * kChunk * A.pstride + vi * (KVB / 8);
 #pragma unroll
     for (int u = 0; u < kChunk; ++u)
         vch[u] = (int)__builtin_amdgcn_raw_buffer_load_b32(vrs, base + u * A.pstride, 0, 0);
@@ -301,7 +303,10 @@ __device__ __forceinline__ double chunk_w(double lo, double hi) {
     return __builtin_amdgcn_mov_dpp(U < 16 ? lo : hi, 0x150 + (U & 15), 0xf, 0xf, false);
 }
 
-template <int KVB>
+// PAIR: the pair plan below is compiled in (the host sets it for heads of at
+// most 32 fields of 32 bits; without it the kernel of a wider head keeps the
+// registers and schedule of the one- and two-element plans alone).
+template <int KVB, bool PAIR>
 __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t* kv, const int32_t* rtab,
                                                         const int16_t* qn, const int16_t* kn,
                                                         const int16_t* qkv, int16_t* out, int pos0,
@@ -401,13 +406,15 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     // (slot is wave-uniform; readfirstlane lets the compiler see it)
     const bool wide = A.vC2 > A.vC1 && nch > A.vC1;
     const int vE = wide ? 2 : 1, vG = wide ? A.vG2 : A.vG1, vC = wide ? A.vC2 : A.vC1;
-    // pair plan (q8 cache, head_dim up to 128, more chunks than one round of
-    // the one-element plan): every wave takes two chunks of a round, lanes
-    // 0..31 chunk 2*wave and lanes 32..63 chunk 2*wave + 1, four elements a
-    // lane from one 32-bit field, so one load per position serves two
-    // chunks: 16 chunks a round
-    const bool pair = KVB == 8 && hd <= 128 && nch > A.vC1;
-    const int pe = (lane & 31) * 4, pvi = min(pe, hd - 4), pch = 2 * wave + (lane >> 5);
+    // pair plan (a head of at most 32 fields of 32 bits -- head_dim 64 at a
+    // q16 cache, 128 at q8 -- and more chunks than one round of the
+    // one-element plan): every wave takes two chunks of a round, lanes 0..31
+    // chunk 2*wave and lanes 32..63 chunk 2*wave + 1, the elements of one
+    // 32-bit field a lane, so one load per position serves two chunks: 16
+    // chunks a round
+    constexpr int EPL = 32 / KVB;  // elements a field
+    const bool pair = PAIR && hd <= 32 * EPL && nch > A.vC1;
+    const int pe = (lane & 31) * EPL, pvi = min(pe, hd - EPL), pch = 2 * wave + (lane >> 5);
     const int slot = __builtin_amdgcn_readfirstlane(wave / vG);
     const int ve = ((wave - slot * vG) * 64 + lane) * vE, vi = min(ve, hd - vE);
     uint4 kreg[KP];
@@ -425,7 +432,7 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     }
     // the K loads first: the scores wait for them, not for the V loads after
     asm volatile("" ::: "memory");
-    if (pair) v_pair_load(A, vrs, pch, pvi, vch);
+    if (pair) v_pair_load<KVB>(A, vrs, pch, pvi, vch);
     else v_chunk_load<KVB>(A, vrs, vE, slot < vC ? slot : A.nchmax, vi, vch);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -621,7 +628,7 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
             const int nr = min(kPC, nch - c0);
             const bool more = c0 + kPC < nch;
             int vnx[kChunk];
-            if (more) v_pair_load(A, vrs, c0 + kPC + pch, pvi, vnx);
+            if (more) v_pair_load<KVB>(A, vrs, c0 + kPC + pch, pvi, vnx);
             if (2 * wave < nr) {
                 const int c = c0 + pch;  // this lane's chunk (past nch: weights zero)
                 const int tlo = c * kChunk + (lane & 15), thi = tlo + 16, tmax = A.nchmax * kChunk - 1;
@@ -630,28 +637,32 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
                 // the last position of a launch that appends is pos: its V
                 // comes from the LDS copy (its cache row is being written)
                 if (own_row) {
-                    const int own = (int)*reinterpret_cast<const uint32_t*>(vpk + pvi);
+                    const int own = (int)*reinterpret_cast<const uint32_t*>(vpk + pvi * (KVB / 8));
                     const int uo = c == nch - 1 ? npos - 1 - c * kChunk : -1;
 #pragma unroll
                     for (int u = 0; u < kChunk; ++u) vch[u] = u == uo ? own : vch[u];
                 }
-                double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+                double a[EPL];
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) a[e] = 0.0;
                 static_for<0, kChunk>([&](auto U) {
                     constexpr int u = decltype(U)::value;
-                    asm volatile("" : "+v"(wlo), "+v"(whi), "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3));
+                    if constexpr (EPL == 4)
+                        asm volatile("" : "+v"(wlo), "+v"(whi), "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]));
+                    else
+                        asm volatile("" : "+v"(wlo), "+v"(whi), "+v"(a[0]), "+v"(a[1]));
                     const double wu = chunk_w<u>(wlo, whi);
-                    const int x = vch[u];
-                    a0 = fma(wu, (double)(int8_t)(x & 0xff), a0);
-                    a1 = fma(wu, (double)(int8_t)((x >> 8) & 0xff), a1);
-                    a2 = fma(wu, (double)(int8_t)((x >> 16) & 0xff), a2);
-                    a3 = fma(wu, (double)(int8_t)((x >> 24) & 0xff), a3);
+                    const unsigned x = (unsigned)vch[u];
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) {
+                        const int q = KVB == 16 ? (int)(int16_t)(x >> (16 * e)) : (int)(int8_t)(x >> (8 * e));
+                        a[e] = fma(wu, (double)q, a[e]);
+                    }
                 });
                 if (pe < hd && c < nch) {
                     double* vp = vpart + (c - c0) * hd + pe;
-                    vp[0] = a0;
-                    vp[1] = a1;
-                    vp[2] = a2;
-                    vp[3] = a3;
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) vp[e] = a[e];
                 }
             }
             __syncthreads();
@@ -1282,6 +1293,17 @@ __global__ void __launch_bounds__(kThreads) attn_group_kernel(const AttnDev A, c
 }
 
 // LDS carve-up of one workgroup and the lane plan; returns the bytes used.
+// The per-head kernel for A's cache width (A laid out by attn_layout), with the
+// pair plan for a head of at most 32 fields of 32 bits whose cache holds more
+// chunks than one round of the one-element plan.
+using AttnKernelFn = void (*)(const AttnDev, uint8_t*, const int32_t*, const int16_t*, const int16_t*,
+                              const int16_t*, int16_t*, int, int, int, size_t, int, const int*);
+AttnKernelFn attn_kernel_for(const AttnDev& A) {
+    const bool pair = A.hd * A.kv_bits <= 32 * 32 && A.nchmax > A.vC1;
+    if (A.kv_bits == 16) return pair ? attn_kernel<16, true> : attn_kernel<16, false>;
+    return pair ? attn_kernel<8, true> : attn_kernel<8, false>;
+}
+
 size_t attn_layout(AttnDev& A) {
     const int hd = A.hd;
     const int nv = hd * A.kv_bits / 128;
@@ -1308,8 +1330,8 @@ size_t attn_layout(AttnDev& A) {
     A.o_sc = take(2 * (size_t)A.seq);
     A.o_ep = take(8 * (size_t)A.nchmax * kChunk);
     A.o_csum = take(8 * (size_t)A.nchmax);
-    // (the pair plan of a q8 cache up to head_dim 128: 16 chunks a round)
-    const int vcm = std::max({A.vC1, A.vC2, A.kv_bits == 8 && hd <= 128 ? 2 * (kThreads / 64) : 0});
+    // (the pair plan, a head of at most 32 fields of 32 bits: 16 chunks a round)
+    const int vcm = std::max({A.vC1, A.vC2, hd * A.kv_bits <= 32 * 32 ? 2 * (kThreads / 64) : 0});
     A.o_vpart = take(8 * (size_t)vcm * hd);
     A.o_acc = take(8 * (size_t)hd);
     return off;
@@ -1367,12 +1389,8 @@ int launch(vgx_attn* at, int layer, int pos, int ntok, const int16_t* qkv, int16
     const dim3 grid(att ? A.heads : A.kv_heads, ntok);
     const size_t stride = seqs ? at->seq_bytes : 0;
     const int step = seqs ? 0 : 1;
-    if (A.kv_bits == 16)
-        hipLaunchKernelGGL(attn_kernel<16>, grid, dim3(kThreads), at->lds, at->ctx->stream, A,
-                           at->kv[layer], at->rtab, qn, kn, qkv, out, pos, w, att, stride, step, pos_ptr);
-    else
-        hipLaunchKernelGGL(attn_kernel<8>, grid, dim3(kThreads), at->lds, at->ctx->stream, A,
-                           at->kv[layer], at->rtab, qn, kn, qkv, out, pos, w, att, stride, step, pos_ptr);
+    hipLaunchKernelGGL(attn_kernel_for(A), grid, dim3(kThreads), at->lds, at->ctx->stream, A, at->kv[layer],
+                       at->rtab, qn, kn, qkv, out, pos, w, att, stride, step, pos_ptr);
     VGX_LAUNCH_CHECK("attention launch");
     return VGX_OK;
 }
@@ -1511,7 +1529,7 @@ int vgx_attn_create_seqs(vgx_ctx* ctx, const vgx_attn_desc* d, int nseq, vgx_att
     A.row_bytes = 2 * d->kv_heads * d->head_dim * (d->kv_bits / 8);
     A.pstride = d->head_dim * (d->kv_bits / 8);
     at->lds = attn_layout(A);
-    if (at->lds > 160 * 1024) {
+    if (at->lds > kLdsMax) {
         delete at;
         return vgx_fail(VGX_EINVAL, "vgx_attn_create: seq too long for one workgroup's LDS");
     }
@@ -1547,12 +1565,11 @@ int vgx_attn_create_seqs(vgx_ctx* ctx, const vgx_attn_desc* d, int nseq, vgx_att
         if (e == hipSuccess) e = hipMemcpy(at->kn, k.data(), k.size() * 2, hipMemcpyHostToDevice);
         if (e != hipSuccess) return fail(e, "q/k norm weights");
     }
-    if (at->lds > 64 * 1024) {
-        hipError_t a1 = hipFuncSetAttribute((const void*)attn_kernel<16>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)at->lds);
-        hipError_t a2 = hipFuncSetAttribute((const void*)attn_kernel<8>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)at->lds);
-        if (a1 != hipSuccess) return fail(a1, "hipFuncSetAttribute");
-        if (a2 != hipSuccess) return fail(a2, "hipFuncSetAttribute");
-    }
+    // the per-head kernel's limit at the most any layout takes (another handle
+    // of another shape shares the kernel)
+    const hipError_t a1 = hipFuncSetAttribute((const void*)attn_kernel_for(A),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax);
+    if (a1 != hipSuccess) return fail(a1, "hipFuncSetAttribute");
     for (int kvb : {16, 8})
         for (int ve : {1, 2})
             for (int qg : {2, 4}) {
