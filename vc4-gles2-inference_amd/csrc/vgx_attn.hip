@@ -31,6 +31,7 @@
 #include <vector>
 
 #include "vgx_internal.h"
+#include "vgx_qrow.h"
 
 #pragma clang fp contract(off)
 
@@ -75,11 +76,6 @@ struct vgx_attn {
 
 namespace {
 
-__device__ __forceinline__ int q16_round(float v) {
-    float f = floorf(v + 0.5f);
-    f = fminf(fmaxf(f, -32768.0f), 32767.0f);
-    return (int)f;
-}
 
 __device__ __forceinline__ float rsqrt_d(float x) { return (float)(1.0 / sqrt((double)x)); }
 __device__ __forceinline__ float exp_d(float x) { return (float)exp((double)x); }

@@ -21,6 +21,7 @@
 // butterfly that halves the row set per step, so RI rows cost RI-1+log2(LPR)
 // exchanges instead of RI*log2(LPR).
 #include "vgx_internal.h"
+#include "vgx_qrow.h"
 
 #pragma clang fp contract(off)
 
@@ -29,15 +30,6 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 
-__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
-    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
-}
-__device__ __forceinline__ uint32_t udot4(uint32_t a, uint32_t b, uint32_t c) {
-    return __builtin_amdgcn_udot4(a, b, c, false);
-}
-__device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) {
-    return __builtin_amdgcn_perm(s0, s1, sel);
-}
 
 // quantize_act on the device: rint half-even of v*256, int16 rail.
 __device__ __forceinline__ int q16_host(float v) {
@@ -46,12 +38,6 @@ __device__ __forceinline__ int q16_host(float v) {
     return (int)r;
 }
 
-// clamp(floor(v + 0.5)) -- the shader's q16 store of a value in Q units.
-__device__ __forceinline__ int q16_round(float v) {
-    float f = floorf(v + 0.5f);
-    f = fminf(fmaxf(f, -32768.0f), 32767.0f);
-    return (int)f;
-}
 
 template <typename T>
 __device__ __forceinline__ T shfl_xor(T v, int o) {
@@ -135,16 +121,6 @@ __device__ __forceinline__ T pick(const T (&a)[R][C], int r, int c) {
     return v;
 }
 
-// Pack 16 q16 values (8 dwords, two per dword, element 2k in the low half)
-// into the natural-order planes: xl[k] / xh[k] = low / high bytes of elements
-// 4k..4k+3.
-__device__ __forceinline__ void planes16(const uint32_t d[8], uint32_t xh[4], uint32_t xl[4]) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        xl[k] = perm(d[2 * k + 1], d[2 * k], 0x06040200u);
-        xh[k] = perm(d[2 * k + 1], d[2 * k], 0x07050301u);
-    }
-}
 
 // 4x4 byte transpose of dwords d[0..3] (each = two q16 values, even element
 // low): returns the even-column low bytes, even high, odd low, odd high.
@@ -160,14 +136,6 @@ __device__ __forceinline__ void planes8eo(const uint32_t d[4], uint32_t& xle, ui
     xho = perm(D, B, 0x07060302u);
 }
 
-// GPU::rmsnorm's output element (engine/src/gpu_upload.cpp:280-365):
-// q16(x * inv * w) with the shader's floor(v + 0.5) store.
-__device__ __forceinline__ uint32_t rms_elem(uint32_t xv16, uint32_t wv16, float inv) {
-    const float xv = (float)(int16_t)xv16 / 256.0f;
-    const float wv = (float)(int16_t)wv16 / 256.0f;
-    const float v = (xv * inv) * wv;
-    return (uint32_t)(uint16_t)(int16_t)q16_round(v * 256.0f);
-}
 
 // Load 16 consecutive activations as q16 dwords: from int16, from f32 with
 // the host quantisation, or through RMSNorm from the workgroup's LDS copies of
@@ -276,18 +244,6 @@ __device__ __forceinline__ int seg_reduce(T (&v)[R][NV], int cl) {
 // ---------------------------------------------------------------------------
 // Per-format chunk math.
 
-// q8: one chunk = 16 bytes of one row = 16 columns; planes: xh, xl (4 dwords).
-__device__ __forceinline__ void q8_chunk(const uint4 w, const uint4 xh, const uint4 xl, int& s1,
-                                         uint32_t& s2) {
-    s1 = sdot4(w.x ^ 0x80808080u, xh.x, s1);
-    s1 = sdot4(w.y ^ 0x80808080u, xh.y, s1);
-    s1 = sdot4(w.z ^ 0x80808080u, xh.z, s1);
-    s1 = sdot4(w.w ^ 0x80808080u, xh.w, s1);
-    s2 = udot4(w.x, xl.x, s2);
-    s2 = udot4(w.y, xl.y, s2);
-    s2 = udot4(w.z, xl.z, s2);
-    s2 = udot4(w.w, xl.w, s2);
-}
 
 // q4: one chunk = one 32-column group (16 nibble bytes); planes per dword j:
 // even-column high/low bytes and odd-column high/low bytes.

@@ -4,16 +4,12 @@
 #include <string>
 
 #include "vgx_internal.h"
+#include "vgx_qrow.h"
 
 #pragma clang fp contract(off)
 
 namespace {
 
-__device__ __forceinline__ int q16_round(float v) {
-    float f = floorf(v + 0.5f);
-    f = fminf(fmaxf(f, -32768.0f), 32767.0f);
-    return (int)f;
-}
 
 // GPU::rmsnorm (engine/src/gpu_upload.cpp:280-365) as one workgroup:
 // rms_stats_split's 32 partial sums of v^2 over contiguous slices of

@@ -41,6 +41,7 @@
 #include <string>
 
 #include "vgx_internal.h"
+#include "vgx_qrow.h"
 
 #pragma clang fp contract(off)
 
@@ -73,32 +74,12 @@ union Op {
     uint32_t d[4];
 };
 
-__device__ __forceinline__ int q16_round(float v) {
-    float f = floorf(v + 0.5f);
-    f = fminf(fmaxf(f, -32768.0f), 32767.0f);
-    return (int)f;
-}
 
-__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
-    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
-}
-__device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) {
-    return __builtin_amdgcn_perm(s0, s1, sel);
-}
 
 __device__ __forceinline__ i32x16 mfma(const Op& a, const Op& b, const i32x16& c) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(a.v, b.v, c, 0, 0, 0);
 }
 
-// GPU::rmsnorm's output element (engine/src/gpu_upload.cpp:280-365):
-// q16(x * inv * w) with the shader's floor(v + 0.5) store; the same
-// expression as the batch-1 GEMV's fused prologue.
-__device__ __forceinline__ uint32_t rms_elem(uint32_t xv16, uint32_t wv16, float inv) {
-    const float xv = (float)(int16_t)xv16 / 256.0f;
-    const float wv = (float)(int16_t)wv16 / 256.0f;
-    const float v = (xv * inv) * wv;
-    return (uint32_t)(uint16_t)(int16_t)q16_round(v * 256.0f);
-}
 
 // A operands: 16 q16 activations (two 16-byte loads of one token row) as the
 // high-byte plane and the low-byte plane minus 128; xsum = their exact sum.
