@@ -271,11 +271,11 @@ def ternary_batch_bench(runs, nseq=32):
 
 def decode_batch_gemms(reps=200):
     """The C5 batch-32 step's GEMMs alone, at its shapes (32 tokens, the 0.5B
-    t3 layer): qkv (split K, then its epilogue), wo + residual with the FFN
-    RMSNorm in its split epilogue, the gate, w2 + residual (split at the
-    chunk) with the next RMSNorm -- the calls the batched decode loop makes --
-    timed with HIP events on the launch stream; algorithmic int8 ops 2*M*N*K
-    (the gate: both matrices) against the matrix-core peak."""
+    t3 layer): qkv, wo + residual then the FFN RMSNorm (rows of 32 k-steps
+    are not split), the gate, w2 + residual split over workgroups with the
+    next RMSNorm in its epilogue launch -- the calls the batched decode loop
+    makes -- timed with HIP events on the launch stream; algorithmic int8 ops
+    2*M*N*K (the gate: both matrices) against the matrix-core peak."""
     import numpy as np
     import torch
     from vgx import gpu as vg
