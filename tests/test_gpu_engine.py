@@ -132,6 +132,71 @@ def test_prefill_batches_equal_serial(gpu, scheme):
     ser.close()
 
 
+def test_minimind3_q4_kv8_float_tolerance(gpu):
+    """The C3 run against the float path: MiniMind3 q4, KV q8, SEQ 768, a
+    256-token prompt in one batch, then 512 greedy steps (positions 256..767,
+    so every per-head attention plan runs, the pair V plan past one round).
+
+    Bars, at every greedy step (the engine's logits against CFModel, the float
+    forward of engine/tools/ref_forward.py:47-115 on the dequantised weights,
+    fed the engine's tokens):
+    - max |logit difference| <= 0.6 and mean <= 0.12 (float logits' std
+      0.55); measured on seed 0: max 0.465, mean <= 0.086;
+    - top-1 agreement >= 70% of the steps (measured 412 of 512), the greedy
+      token within the float top 5 at >= 95% (506 of 512) and always within
+      its top 32 (worst rank 16).
+    The KV cache's q8 grid (1/16, clamped to [-128, 127]:
+    engine/src/shaders_attn.cpp:141-156) adds to the activation grid's gap.
+    Its share is isolated by a second engine with a q16 cache fed the same
+    tokens: |logits(KV q8) - logits(KV q16)| <= 0.4 (measured 0.289, mean
+    0.053).  The clamp itself never engages on this workload: no cached value
+    sits on a rail (the largest |q| is 70 of 128, i.e. |k|, |v| <= 4.4), which
+    the oracle's cache shows at the end.  q16 logits equal the oracle's (QModel,
+    KV q8) bit for bit at the prompt's last position and at every 64th step."""
+    import oracle as o
+    spec = synth.minimind3_spec(seq=768)
+    blob = synth.container(spec, "q4", seed=0)
+    prompt = synth.prompt(256, spec.vocab, seed=0)
+    eng8, eng16 = Engine(blob, kv_bits=8), Engine(blob, kv_bits=16)
+    ref, f = QModel(blob, kv_bits=8), CFModel(blob)
+    got, tok = eng8.prefill(prompt)
+    eng16.prefill(prompt, logits=False)
+    for pos in range(256):
+        lq = ref.step(int(prompt[pos]), pos, want_logits=pos == 255)
+        lf = f.step(int(prompt[pos]), pos, logits=pos == 255)
+    assert np.array_equal(got, lq)
+    assert tok == int(np.argmax(lq))
+    stats, grid = [], []
+    for pos in range(256, 768):
+        d = np.abs(got / 256.0 - lf)
+        stats.append((d.max(), d.mean(), int((lf > lf[tok]).sum())))
+        if pos == 767:
+            break
+        got, nxt = eng8.step(tok, pos)
+        g16, _ = eng16.step(tok, pos)
+        grid.append(np.abs(got.astype(np.int64) - g16).max() / 256.0)
+        lq = ref.step(tok, pos, want_logits=pos % 64 == 0)
+        if lq is not None:
+            assert np.array_equal(got, lq), pos
+        assert nxt == int(np.argmax(got)), pos
+        lf = f.step(tok, pos)
+        tok = nxt
+    eng8.close()
+    eng16.close()
+    n = len(stats)
+    assert n == 512
+    assert max(s[0] for s in stats) <= 0.6, max(s[0] for s in stats)
+    assert max(s[1] for s in stats) <= 0.12, max(s[1] for s in stats)
+    assert sum(s[2] == 0 for s in stats) >= 0.70 * n, sum(s[2] == 0 for s in stats)
+    assert sum(s[2] < 5 for s in stats) >= 0.95 * n, sum(s[2] < 5 for s in stats)
+    assert max(s[2] for s in stats) < 32, max(s[2] for s in stats)
+    assert max(grid) <= 0.4, max(grid)
+    rb = o.kv_row_bytes(ref.cfg)
+    for l in range(spec.layers):
+        kv = ref.kv[l][:767 * rb].view(np.int8)
+        assert not ((kv == -128) | (kv == 127)).any(), l
+
+
 def test_minimind3_q4_prefill_256_kv8(gpu):
     """The C3 shape: MiniMind3 q4, KV q8, SEQ 768, a 256-token prompt in one
     batch against the serial loop, then greedy decode from both."""
@@ -194,52 +259,62 @@ def test_hybrid_engine_bit_exact(gpu, scheme):
 
 
 def test_lfm2_230m_shape(gpu):
-    """The C4 shape (LFM2.5-230M-shaped q8: 8 conv + 6 attention layers, dim
-    1024, vocab 64402): bit-exact against the oracle over a batched prompt and
-    greedy steps, and within the stated tolerance of the float path.
+    """The C4 run (LFM2.5-230M-shaped q8: 8 conv + 6 attention layers, dim
+    1024, vocab 64402; a 64-token prompt in one batch, 128 greedy steps, KV
+    q16, SEQ 256): bit-exact against the oracle at the prompt's end and at
+    every 16th step, and within the stated tolerance of the float path at
+    every step.
 
-    The tolerance for this shape: max |logit difference| <= 1.5 and mean <=
-    0.25 (the float logits' std is 0.64), and at every step the q16 path's
-    greedy token within the float path's top 64 of 64402.  The gap is the
-    reference's own q16 activation grid on a residual of order 0.02 over 14
-    layers, which the reference documents for LFM2.5 (2-3 significant bits per
-    component after the embedding, engine/src/session.cpp:328-333); measured
-    on seed 0: max 0.78-1.18, mean 0.14-0.21, ranks 0-52.  Top-1 agreement
-    (the greedy token is the float path's argmax) at least 25% of the steps,
-    and within its top 5 at least half of them."""
+    The gap is the reference's own q16 activation grid on a residual of order
+    0.02 over 14 layers, which the reference documents for LFM2.5 (2-3
+    significant bits per component after the embedding,
+    engine/src/session.cpp:328-333).  Measured on seed 0 (prompt seed 4): max
+    |logit difference| 1.38, mean <= 0.24, against float logits of std 0.64.
+    Random N(0, 0.02) weights give a flat top: at 49 of the 128 steps the
+    float path's two largest logits lie within 0.1 of each other, well inside
+    the grid's mean gap, so top-1 agreement (measured 45 of 128) and rank
+    (worst 364 of 64402) measure that flatness more than the error.  The
+    bound that follows from the error is the float-path regret of the greedy
+    token, max(lf) - lf[token] <= 2 max |lq - lf|: measured <= 1.07, mean 0.23.
+    Bars: max <= 1.6, mean <= 0.3, regret <= 1.3 and its mean <= 0.3, top-1
+    >= 25% and top-5 >= 50% (measured 78 of 128)."""
     spec = synth.lfm2_spec(seq=256)
     blob = synth.container(spec, "q8", seed=0, q8_row=True)
-    prompt = synth.prompt(6, spec.vocab, seed=4)
+    prompt = synth.prompt(64, spec.vocab, seed=4)
     eng = Engine(blob)
     ref, f = QModel(blob), CFModel(blob)
     got, tok = eng.prefill(prompt)
     for pos in range(len(prompt)):
         lq = ref.step(int(prompt[pos]), pos, want_logits=pos == len(prompt) - 1)
-        lf = f.step(int(prompt[pos]), pos)
+        lf = f.step(int(prompt[pos]), pos, logits=pos == len(prompt) - 1)
     assert np.array_equal(got, lq)
 
-    def gap(lq, lf):
+    def gap(lq, lf, tok):
         d = np.abs(lq / 256.0 - lf)
-        rank = int((lf > lf[int(np.argmax(lq))]).sum())
-        return d.max(), d.mean(), rank
+        return d.max(), d.mean(), int((lf > lf[tok]).sum()), float(lf.max() - lf[tok])
 
-    gaps = [gap(lq, lf)]
-    for pos in range(len(prompt), len(prompt) + 24):
+    gaps = []
+    for pos in range(len(prompt), len(prompt) + 128):
+        gaps.append(gap(got, lf, tok))
+        if pos == len(prompt) + 127:
+            break
         got, nxt = eng.step(tok, pos)
-        lq, lf = ref.step(tok, pos), f.step(tok, pos)
-        if pos < len(prompt) + 4 or pos % 8 == 0:
+        lq = ref.step(tok, pos, want_logits=pos < len(prompt) + 4 or pos % 16 == 0)
+        if lq is not None:
             assert np.array_equal(got, lq), pos
-        assert nxt == int(np.argmax(lq)), pos
-        gaps.append(gap(lq, lf))
+        assert nxt == int(np.argmax(got)), pos
+        lf = f.step(tok, pos)
         tok = nxt
-    assert max(g[0] for g in gaps) <= 1.5, gaps
-    assert max(g[1] for g in gaps) <= 0.25, gaps
-    assert max(g[2] for g in gaps) < 64, gaps
-    # top-1 agreement: measured 10 of 25 on seed 0, the greedy token within
-    # the float path's top 5 at 15 of 25
-    assert sum(g[2] == 0 for g in gaps) >= 0.25 * len(gaps), gaps
-    assert sum(g[2] < 5 for g in gaps) >= 0.5 * len(gaps), gaps
     eng.close()
+    n = len(gaps)
+    assert n == 128
+    assert max(g[0] for g in gaps) <= 1.6, max(g[0] for g in gaps)
+    assert max(g[1] for g in gaps) <= 0.3, max(g[1] for g in gaps)
+    assert max(g[3] for g in gaps) <= 1.3, max(g[3] for g in gaps)
+    assert np.mean([g[3] for g in gaps]) <= 0.3, np.mean([g[3] for g in gaps])
+    assert all(g[3] <= 2 * g[0] + 1e-6 for g in gaps)
+    assert sum(g[2] == 0 for g in gaps) >= 0.25 * n, sum(g[2] == 0 for g in gaps)
+    assert sum(g[2] < 5 for g in gaps) >= 0.5 * n, sum(g[2] < 5 for g in gaps)
 
 
 def test_engine_refusals(gpu):

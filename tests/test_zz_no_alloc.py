@@ -65,7 +65,30 @@ def test_noalloc_argmax_equals_group_slots(gpu):
 
 
 def test_noalloc_argmax_refusals(gpu):
+    """Each refusal with every other argument valid, so the check named is
+    the one that fires: NULL outputs, a NULL norm weight, no context, no
+    group; nothing is launched."""
     L = vl.load()
     z = ctypes.c_void_p(0)
-    assert L.vgx_logits_argmax_rms_noalloc(gpu.ctx, z, z, z, ctypes.c_float(1e-5), z, z) == vl.VGX_EINVAL
-    assert L.vgx_logits_argmax_rms_noalloc(z, z, z, z, ctypes.c_float(1e-5), z, z) == vl.VGX_EINVAL
+    rng = np.random.default_rng(3)
+    mats, tiles, G = _head(gpu, rng, 2000, 1e-3)
+    x = torch.zeros(1024, dtype=torch.int16, device="cuda")
+    w = torch.ones(1024, dtype=torch.int16, device="cuda")
+    lg = torch.empty(2000, dtype=torch.int16, device="cuda")
+    tk = torch.full((1,), -7, dtype=torch.int32, device="cuda")
+    eps = ctypes.c_float(1e-5)
+
+    def refused(ctx, g, xp, wp, lp, tp, what):
+        assert L.vgx_logits_argmax_rms_noalloc(ctx, g, xp, wp, eps, lp, tp) == vl.VGX_EINVAL
+        assert what in L.vgx_last_error().decode()
+
+    refused(gpu.ctx, G.h, _p(x), _p(w), z, _p(tk), "NULL output")
+    refused(gpu.ctx, G.h, _p(x), _p(w), _p(lg), z, "NULL output")
+    refused(gpu.ctx, G.h, _p(x), z, _p(lg), _p(tk), "NULL RMSNorm weight")
+    refused(z, G.h, _p(x), _p(w), _p(lg), _p(tk), "no context")
+    refused(gpu.ctx, z, _p(x), _p(w), _p(lg), _p(tk), "NULL argument")
+    torch.cuda.synchronize()
+    assert int(tk.item()) == -7  # nothing ran
+    G.free()
+    for t in tiles:
+        t.free()

@@ -1034,11 +1034,12 @@ int vgx_gemv_plan(int kind, int rows, int cols, int num_cu, int* lpr, int* ri, i
     } else if (kind == VGX_T3) {
         l = 8;
         while (l < 64 && l < nch) l <<= 1;
-    } else if (l < 64 && l * 4 == nch) {
-        // rows of exactly four chunks a lane take twice the lanes (measured
-        // on the 1024-column decode rows of the hybrid: 16 -> 32 lanes +0.9%
-        // decode; at 768 columns 32 lanes were 0.7% slower)
-        l <<= 1;
+    } else if (kind == VGX_Q8 && nch == 64) {
+        // 1024-column q8 rows take 32 lanes, two chunks a lane (measured on
+        // the hybrid's decode rows: 16 -> 32 lanes +0.9% decode; at 768
+        // columns 32 lanes were 0.7% slower, and no other row length was
+        // measured, so the rule stays on this one)
+        l = 32;
     }
     const int rpi = 64 / l;
     *lpr = l;

@@ -66,8 +66,8 @@ struct vgx_ctx {
     // this device's address of the library's static key-slot array (the
     // no-allocation argmax entry point), resolved once per device at create
     unsigned long long* scratch_keys = nullptr;
-    // split-K GEMM partial sums, allocated at the first launch that splits
-    // and grown on demand (freed at destroy)
+    // split-K GEMM partial sums: the bound of every split launch, allocated
+    // once at the first launch that splits, never regrown (freed at destroy)
     void* ws = nullptr;
     size_t ws_bytes = 0;
     std::mutex ws_mu;

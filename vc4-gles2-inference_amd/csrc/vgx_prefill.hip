@@ -631,22 +631,35 @@ int k_splits(int tiles_x, int tiles_y, int nsteps, int num_cu) {
     return std::max(1, std::min({num_cu / tiles_x, nsteps / 4, kMaxSplit}));
 }
 
-// The context's split-K workspace, grown to at least `bytes`.
-int workspace(vgx_ctx* ctx, size_t bytes, long long** out) {
+// The context's split-K workspace.  k_splits splits only one token tile
+// (ntok <= 32) of fewer than num_cu/2 row tiles, at most kMaxSplit ways, with
+// at most two accumulator sets, so every split launch fits
+//   kMaxSplit * 2 * 32 * (num_cu/2 * 32) int64 sums
+// (16 MiB at 256 CUs).  That much is allocated once, at the first launch that
+// splits, and never regrown: a graph captured with a split GEMM keeps a valid
+// address for the context's life.  No allocation happens under stream capture
+// (such a launch runs unsplit until an uncaptured split has allocated the
+// buffer).  Returns false when the launch must run unsplit.
+size_t ws_bound(int num_cu) {
+    return (size_t)kMaxSplit * 2 * kTile * (size_t)(std::max(num_cu, 2) / 2 * kTile) * sizeof(long long);
+}
+
+bool workspace(vgx_ctx* ctx, size_t bytes, long long** out) {
     std::lock_guard<std::mutex> lock(ctx->ws_mu);
-    if (ctx->ws_bytes < bytes) {
-        if (ctx->ws) {
-            VGX_HIP(hipStreamSynchronize(ctx->stream));
-            VGX_HIP(hipFree(ctx->ws));
+    if (!ctx->ws) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(ctx->stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return false;
+        const size_t want = ws_bound(ctx->num_cu);
+        if (hipMalloc(&ctx->ws, want) != hipSuccess) {
+            (void)hipGetLastError();
             ctx->ws = nullptr;
-            ctx->ws_bytes = 0;
+            return false;
         }
-        const size_t want = std::max(bytes, (size_t)8 << 20);
-        VGX_HIP(hipMalloc(&ctx->ws, want));
         ctx->ws_bytes = want;
     }
+    if (bytes > ctx->ws_bytes) return false;
     *out = static_cast<long long*>(ctx->ws);
-    return VGX_OK;
+    return true;
 }
 
 // Waves per workgroup: 4 when the launch has at least one tile per CU (two
@@ -697,7 +710,7 @@ int launch(vgx_ctx* ctx, const vgx_mat* W, const vgx_mat* W3, int ntok, const in
     if (nz > 1) {
         const int na = epi == BEPI_STORE ? 1 : 2;
         const size_t bytes = (size_t)nz * na * ntok * M.rows * sizeof(long long);
-        if (workspace(ctx, bytes, &L.part) != VGX_OK) nz = 1;  // no workspace: one pass
+        if (!workspace(ctx, bytes, &L.part)) nz = 1;  // no workspace: one pass
         grid.z = nz;
     }
     const int nw = nz > 1 ? 4 : waves_for((int)(grid.x * grid.y), nsteps, ctx->num_cu);
