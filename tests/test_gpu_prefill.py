@@ -38,6 +38,24 @@ def test_gemm_rows_equal_gemv(gpu, kind, rows, cols, ntok):
         assert np.array_equal(got_r[t], o.store(v, res[t])), t
 
 
+@pytest.mark.parametrize("kind,rows,cols", [("q8", 1536, 768), ("q4", 1536, 768), ("t3", 1280, 1024),
+                                            ("q4", 768, 2432), ("q8", 2432, 768)])
+def test_gemm_256_tokens(gpu, kind, rows, cols):
+    """The prefill launches of 256 tokens: four waves a workgroup over many
+    tiles (eight over the 2432-column rows' few), each wave's k-steps in
+    rounds of eight, the last token tile ragged at 250 tokens; every row
+    equals the batch-1 oracle."""
+    rng = np.random.default_rng(rows * 3 + cols)
+    m = MK[kind](rng, rows, cols)
+    W = gpu.upload(m)
+    for ntok in (256, 250):
+        x = x_rows(rng, ntok, cols)
+        res = x_rows(rng, ntok, rows)
+        got = host(gpu.gemm(W, dev(x), res=dev(res)))
+        for t in range(ntok):
+            assert np.array_equal(got[t], o.store(oracle_rowval(m, x[t]), res[t])), (ntok, t)
+
+
 @pytest.mark.parametrize("kind", ["q8", "t3"])
 def test_gemm_full_range(gpu, kind):
     # int16 extremes and every weight byte: the byte-plane split and its
