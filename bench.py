@@ -76,7 +76,10 @@ def pmc_summary(fetch_csv, write_csv, bench_log):
         return rows
 
     def scale(rows, known):
-        v = [float(r["Counter_Value"]) for r in rows if "AUnaryFunctor" in r["Kernel_Name"]]
+        # the copy calibration's dispatches: the last three elementwise
+        # kernels of the run (--copy-mb runs after the library references,
+        # whose cache-resident copy must not enter the scale)
+        v = [float(r["Counter_Value"]) for r in rows if "AUnaryFunctor" in r["Kernel_Name"]][-3:]
         return known / (sum(v) / len(v) * 1024.0), v
 
     fe, wr = load(fetch_csv), load(write_csv)
@@ -472,6 +475,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cold-mb", type=int, default=512, help="distinct weight MiB per shape")
     ap.add_argument("--warm-reps", type=int, default=1000)
+    ap.add_argument("--warm-mb", type=int, default=64,
+                    help="distinct weight MiB per shape of the warm (Infinity-Cache-resident) sweep")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-runs", type=int, default=5)
@@ -533,7 +538,12 @@ def main():
     def cold_sweep(kind, timed):
         """One launch per shape over >= --cold-mb MiB of distinct copies (a
         group sharing x); `timed` steps of the five launches between two
-        events, then per-shape cold and warm launch times."""
+        events, then per shape: the cold launch time, the warm sweep (one
+        launch over --warm-mb MiB of the same copies, resident in the
+        Infinity Cache after a warm-up launch: the kernel streaming from the
+        cache), and the back-to-back launch interval of one matrix (1000 reps,
+        the reference's warm measurement; at these sizes a launch-latency
+        figure, not a kernel duration)."""
         rng = np.random.default_rng(0 if kind == "q8" else 1)
         xs, per_shape = {}, []
         for rows, cols in SHAPES:
@@ -541,11 +551,13 @@ def main():
             copies = max(1, (args.cold_mb << 20) // weight_bytes(rows, cols, kind))
             mats = [base] + [g.clone(base) for _ in range(copies - 1)]
             grp = g.group(mats)
+            wcopies = max(1, min(copies, (args.warm_mb << 20) // weight_bytes(rows, cols, kind)))
+            wgrp = g.group(mats[:wcopies])
             if cols not in xs:
                 xs[cols] = torch.from_numpy(rng.standard_normal(cols).astype(np.float32)).cuda()
             y = torch.empty(grp.rows, dtype=torch.float32, device="cuda")
-            per_shape.append(dict(rows=rows, cols=cols, copies=copies, mats=mats, grp=grp, y=y,
-                                  y1=torch.empty(rows, dtype=torch.float32, device="cuda")))
+            per_shape.append(dict(rows=rows, cols=cols, copies=copies, mats=mats, grp=grp, y=y, wcopies=wcopies,
+                                  wgrp=wgrp, y1=torch.empty(rows, dtype=torch.float32, device="cuda")))
         torch.cuda.synchronize()
 
         def step():
@@ -574,6 +586,14 @@ def main():
             b.record()
             torch.cuda.synchronize()
             cold_us = a.elapsed_time(b) * 1e3 / timed
+            for _ in range(3):  # bring the warm copies into the Infinity Cache
+                s["wgrp"].gemv_f32(xs[s["cols"]], s["y"])
+            a.record()
+            for _ in range(timed):
+                s["wgrp"].gemv_f32(xs[s["cols"]], s["y"])
+            b.record()
+            torch.cuda.synchronize()
+            wsweep_us = a.elapsed_time(b) * 1e3 / timed
             a.record()
             for _ in range(args.warm_reps):
                 g.matvec_f32(s["mats"][0], xs[s["cols"]], s["y1"])
@@ -585,10 +605,13 @@ def main():
                                "bytes_per_launch": s["copies"] * ab,
                                "cold_us_per_launch": round(cold_us, 2),
                                "cold_GBps": round(s["copies"] * ab / (cold_us * 1e-6) / 1e9, 1),
-                               "warm_us_per_gemv": round(warm_us, 3),
-                               "warm_GBps": round(ab / (warm_us * 1e-6) / 1e9, 1)})
+                               "warm_sweep_copies": s["wcopies"], "warm_sweep_bytes": s["wcopies"] * ab,
+                               "warm_sweep_us_per_launch": round(wsweep_us, 2),
+                               "warm_sweep_GBps": round(s["wcopies"] * ab / (wsweep_us * 1e-6) / 1e9, 1),
+                               "launch_interval_us_one_matrix": round(warm_us, 3)})
         for s in per_shape:
             s["grp"].free()
+            s["wgrp"].free()
             for mm in s["mats"]:
                 mm.free()
         torch.cuda.synchronize()
@@ -643,8 +666,27 @@ def main():
             torch.cuda.synchronize()
             gbps = nbytes * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9
             ref[name] = {"GBps": round(gbps, 1), "frac_of_peak": round(gbps / 8000.0, 4)}
+        # the same two kernels on a working set the Infinity Cache holds (the
+        # warm sweep's size), after a warm-up pass
+        small = torch.ones(args.warm_mb << 17, dtype=torch.float32, device="cuda")  # warm_mb / 2 MiB
+        sdst = torch.empty_like(small)
+        for name, fn, nbytes in (("torch.sum, float32, %d MiB read, cache-resident" % (args.warm_mb // 2),
+                                  lambda: small.sum(), small.numel() * 4),
+                                 ("torch.mul, float32, %d MiB read + %d MiB written, cache-resident"
+                                  % (args.warm_mb // 2, args.warm_mb // 2),
+                                  lambda: torch.mul(small, 1.0, out=sdst), small.numel() * 8)):
+            for _ in range(5):
+                fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(50):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ref[name] = {"GBps": round(nbytes * 50 / (e0.elapsed_time(e1) * 1e-3) / 1e9, 1)}
         out["stream_reference"] = ref
-        del big, dst
+        del big, dst, small, sdst
     if args.copy_mb:
         # a plain device copy of known size: the scale for the FETCH_SIZE /
         # WRITE_SIZE counters of a profiling run of this command

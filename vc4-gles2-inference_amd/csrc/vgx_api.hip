@@ -188,10 +188,7 @@ int vgx_mat_upload(vgx_ctx* ctx, const vgx_weight_desc* w, vgx_mat** out) {
     m->d.rows = rows;
     m->d.cols = cols;
     m->body_bytes = need;
-    // q4 rows of 128 bytes or more start at 128-byte multiples (q4_rstride):
-    // a row that ended mid cache line was fetched partly twice
-    const size_t rstride = w->kind == VGX_Q4 ? (size_t)q4_rstride(cols) : 0;
-    m->body_alloc_bytes = w->kind == VGX_Q4 ? (size_t)rows * rstride : need;
+    m->body_alloc_bytes = need;
     hipError_t e = hipMalloc(&m->body_alloc, m->body_alloc_bytes);
     if (e != hipSuccess) { delete m; return vgx_hip_fail(e, "hipMalloc(body)"); }
     m->d.body = static_cast<const uint8_t*>(m->body_alloc);
@@ -203,11 +200,6 @@ int vgx_mat_upload(vgx_ctx* ctx, const vgx_weight_desc* w, vgx_mat** out) {
         const uint8_t* src = static_cast<const uint8_t*>(w->body);
         for (size_t i = 0; i < need; ++i) tmp[i] = src[i] ^ 0x80u;
         e = hipMemcpy(m->body_alloc, tmp.data(), need, hipMemcpyHostToDevice);
-    } else if (w->kind == VGX_Q4 && rstride != (size_t)cols / 2) {
-        e = hipMemset(m->body_alloc, 0, m->body_alloc_bytes);
-        if (e == hipSuccess)
-            e = hipMemcpy2D(m->body_alloc, rstride, w->body, (size_t)cols / 2, (size_t)cols / 2, (size_t)rows,
-                            hipMemcpyHostToDevice);
     } else {
         e = hipMemcpy(m->body_alloc, w->body, need, hipMemcpyHostToDevice);
     }

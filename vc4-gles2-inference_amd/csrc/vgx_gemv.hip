@@ -398,6 +398,17 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
     // a predicated load would be waited for before the next one is issued.
     constexpr bool PF = RI == 1;
     constexpr int NPF = PF ? 4 : 1;
+    // q4 rows lie back to back in HBM (cols/2 bytes each), so consecutive
+    // rows share a cache line where a row ends mid line (768 x 2432: 1216-byte
+    // rows).  Odd rows walk their chunks last to first: the last chunk of row
+    // 2p and the first of row 2p+1 (and the last of 2p+1 and the first of
+    // 2p+2) are then loaded by the same instruction, so the shared line is
+    // fetched once.  (A row's sum is exact, so its chunk order does not
+    // change the result.)  A lane's row slots share one parity when RPI is
+    // even, so they keep sharing the x planes of a chunk.
+    constexpr bool SNAKE = KIND == VGX_Q4 && (RI == 1 || RPI % 2 == 0);
+    bool rev = false;  // SNAKE: this lane's rows are odd
+    auto chk = [&](int c) { return (SNAKE && rev) ? nch - 1 - c : c; };
     MatDev M;
     int units = 0, unit0 = 0;
     const uint8_t* body = nullptr;
@@ -409,7 +420,7 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
     uint32_t psm[NPF], psm3[NPF];  // PF, q4: their scale/min words
     auto pf_load = [&](int s, int c) {
         const int u = min(unit0 + rs, units - 1);
-        const int cc = min(c, nch - 1);
+        const int cc = chk(min(c, nch - 1));
         pb[s] = wload(body + (size_t)u * ustride + (size_t)cc * 16);
         if (EPI == EPI_GATE) pb3[s] = wload(body3 + (size_t)u * ustride + (size_t)cc * 16);
         if (KIND == VGX_Q4) {
@@ -431,6 +442,7 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
         }
         units = KIND == VGX_T3 ? (M.rows + 1) / 2 : M.rows;
         unit0 = (tile - M.blk_off) * (kWaves * RPI * RI) + wave * (RPI * RI);
+        rev = SNAKE && ((unit0 + rs) & 1) != 0;
         body = M.body;
 #pragma unroll
         for (int it = 0; it < (PF ? RI : 0); ++it) {
@@ -453,15 +465,16 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
         for (int it = 0; it < RI; ++it) {
             const int u = unit0 + it * RPI + rs;
             const int c = cl;
+            const int ca = chk(c);  // the chunk in memory (q4: odd rows reversed)
             const bool ok = u < units && c < nch;
-            w[it] = ok ? wload(body + (size_t)u * ustride + (size_t)c * 16)
+            w[it] = ok ? wload(body + (size_t)u * ustride + (size_t)ca * 16)
                        : make_uint4(0, 0, 0, 0);
             if (EPI == EPI_GATE)
-                w3[it] = ok ? wload(body3 + (size_t)u * ustride + (size_t)c * 16)
+                w3[it] = ok ? wload(body3 + (size_t)u * ustride + (size_t)ca * 16)
                             : make_uint4(0, 0, 0, 0);
             if (KIND == VGX_Q4) {
-                smv[it] = ok ? gld(M.sm + (size_t)u * nch + c) : 0u;
-                if (EPI == EPI_GATE) smv3[it] = ok ? gld(M3.sm + (size_t)u * nch + c) : 0u;
+                smv[it] = ok ? gld(M.sm + (size_t)u * nch + ca) : 0u;
+                if (EPI == EPI_GATE) smv3[it] = ok ? gld(M3.sm + (size_t)u * nch + ca) : 0u;
             }
         }
     };
@@ -654,7 +667,7 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
 #pragma unroll
                 for (int s = 0; s < NPF; ++s) {
                     const int c = cl + (j0 + s) * LPR;
-                    if (c < nch) q4_step(0, c, pb[s], psm[s], pb3[s], psm3[s]);
+                    if (c < nch) q4_step(0, chk(c), pb[s], psm[s], pb3[s], psm3[s]);
                     if (j0 + s + NPF < niter) pf_load(s, c + NPF * LPR);
                 }
             }
@@ -670,20 +683,21 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
                 for (int it = 0; it < RI; ++it) {
                     const int u = unit0 + it * RPI + rs;
                     const int cn = c + LPR;
+                    const int ca = chk(cn);
                     const bool ok = u < units && cn < nch;
-                    wn[it] = ok ? wload(body + (size_t)u * ustride + (size_t)cn * 16)
+                    wn[it] = ok ? wload(body + (size_t)u * ustride + (size_t)ca * 16)
                                 : make_uint4(0, 0, 0, 0);
-                    sn[it] = ok ? gld(M.sm + (size_t)u * nch + cn) : 0u;
+                    sn[it] = ok ? gld(M.sm + (size_t)u * nch + ca) : 0u;
                     if (EPI == EPI_GATE) {
-                        wn3[it] = ok ? wload(body3 + (size_t)u * ustride + (size_t)cn * 16)
+                        wn3[it] = ok ? wload(body3 + (size_t)u * ustride + (size_t)ca * 16)
                                      : make_uint4(0, 0, 0, 0);
-                        sn3[it] = ok ? gld(M3.sm + (size_t)u * nch + cn) : 0u;
+                        sn3[it] = ok ? gld(M3.sm + (size_t)u * nch + ca) : 0u;
                     }
                 }
             }
             if (cok) {
 #pragma unroll
-                for (int it = 0; it < RI; ++it) q4_step(it, c, w[it], smv[it], w3[it], smv3[it]);
+                for (int it = 0; it < RI; ++it) q4_step(it, chk(c), w[it], smv[it], w3[it], smv3[it]);
             }
             if (more) {
 #pragma unroll

@@ -34,9 +34,9 @@ int vgx_hip_fail(hipError_t e, const char* what);
 //   Q8: body rows x cols bytes, q8u8 (level + 128), 256-byte aligned rows
 //       start at r*cols; wsr: rows f32 per-row scales (the value the kernel
 //       multiplies the exact integer dot product by).
-//   Q4: body rows of cols/2 nibble bytes (the container's), each row at a
-//       multiple of q4_rstride(cols) (rows of 128 bytes or more padded to a
-//       128-byte multiple, so no row ends mid cache line), sm: rows x groups
+//   Q4: body rows of cols/2 nibble bytes (the container's), back to back
+//       (the GEMV walks odd rows' chunks in reverse so a cache line two rows
+//       share is loaded by one instruction), sm: rows x groups
 //       u32 = (u16)s16 | (u16)m16 << 16 (parts 1 and 2 interleaved so one
 //       4-byte load carries a group's scale and minimum), ps scalar.
 //   T3: body = the container's texel grid, ceil(rows/2) x cols/8 x 4 bytes;
@@ -54,9 +54,7 @@ struct MatDev {
 };
 
 // Bytes from one q4 nibble row to the next in HBM.
-__host__ __device__ constexpr int q4_rstride(int cols) {
-    return (cols / 2 >= 128 && (cols / 2) % 128) ? (cols / 2 + 127) / 128 * 128 : cols / 2;
-}
+__host__ __device__ constexpr int q4_rstride(int cols) { return cols / 2; }
 
 struct vgx_ctx {
     int device = 0;
