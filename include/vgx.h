@@ -71,9 +71,11 @@ int vgx_ctx_sync(vgx_ctx* ctx);
  *       `scale` = record scale; `row_plane` = part 3 (rows f32) or NULL.
  *   Q4: rows x cols/2 nibble bytes (low nibble = even column); `scale` = the
  *       record's ps; `q4_scale` / `q4_min` = parts 1 and 2 (rows x cols/32 int16).
- *   T3: ceil(rows/2) x ceil(cols/8) x 4 bytes (dtype 7); `scale` = record
- *       scale (the kernels use scale*127, engine/src/model.cpp:927);
+ *   T3: ceil(rows/2) x cols/8 x 4 bytes (dtype 7; cols a multiple of 8, as
+ *       the packer pads them, engine/tools/mmcf_hf.py:151-156); `scale` =
+ *       record scale (the kernels use scale*127, engine/src/model.cpp:927);
  *       `row_plane` = part 3.
+ * Column counts: q8 a multiple of 16, q4 of 32, t3 of 8.
  * `scale_mul` is Model::apply_hidden_scale's 2^k for a w2 matrix
  * (engine/src/model.cpp:407-429), 0 or 1 for every other matrix.  */
 enum vgx_kind { VGX_Q8 = 1, VGX_Q4 = 2, VGX_T3 = 3 };

@@ -131,6 +131,45 @@ def test_t3_gemv(gpu, rows, cols):
         assert np.array_equal(host(gpu.matvec(W, dev(x), dev(res))), o.store(v, res))
 
 
+@pytest.mark.parametrize("rows,cols", [(33, 8), (64, 200), (130, 1000), (7, 40), (36864, 1000)])
+def test_t3_columns_multiple_of_8(gpu, rows, cols):
+    """t3 rows of any multiple of 8 columns, as the packer pads them
+    (engine/tools/mmcf_hf.py:151-156): upload pads each texel row to whole
+    32-column chunks of zero codes; the GEMV (decode and, at 36864 rows, the
+    four-rows-a-lane plan), the gate, the batched GEMM and the dequantisation
+    equal the oracle bit for bit."""
+    rng = np.random.default_rng(rows + cols)
+    m = t3_matrix(rng, rows, cols)
+    W = gpu.upload(m)
+    for full in (False, True):
+        x = rand_x(rng, cols, full)
+        res = rand_x(rng, rows)
+        v = oracle_rowval(m, x)
+        assert np.array_equal(host(gpu.matvec(W, dev(x))), o.store(v)), full
+        assert np.array_equal(host(gpu.matvec(W, dev(x), dev(res))), o.store(v, res)), full
+    if rows <= 1000:
+        m3 = t3_matrix(rng, rows, cols)
+        W3 = gpu.upload(m3)
+        x = rand_x(rng, cols)
+        assert np.array_equal(host(gpu.ffn_gate(W, W3, dev(x), 1)),
+                              o.gate(oracle_rowval(m, x), oracle_rowval(m3, x), 1))
+        for ntok in (5, 37):
+            xs = np.stack([rand_x(rng, cols) for _ in range(ntok)])
+            got = host(gpu.gemm(W, dev(xs)))
+            for t in range(ntok):
+                assert np.array_equal(got[t], o.store(oracle_rowval(m, xs[t]))), (ntok, t)
+        got = host(gpu.dequant(W))
+        want = o.dequant_t3(m.body, rows, cols, wsr_of(m))
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_t3_columns_refused(gpu):
+    from vgx import lib as vl
+    rng = np.random.default_rng(5)
+    with pytest.raises(vl.VgxError, match="multiple of 8"):
+        gpu.upload(t3_matrix(rng, 4, 12))  # the packer pads 12 to 16: not a kernel row length
+
+
 @pytest.mark.parametrize("kind", ["q8", "q4", "t3"])
 def test_dequant_bit_exact(gpu, kind):
     rng = np.random.default_rng(21)

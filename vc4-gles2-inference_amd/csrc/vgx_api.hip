@@ -172,7 +172,9 @@ int vgx_mat_upload(vgx_ctx* ctx, const vgx_weight_desc* w, vgx_mat** out) {
             need = (size_t)rows * cols / 2;
             break;
         case VGX_T3:
-            if (cols % 32) return vgx_fail(VGX_EINVAL, "vgx_mat_upload: t3 cols must be a multiple of 32");
+            // the packer pads a row to a multiple of 8 columns
+            // (engine/tools/mmcf_hf.py:151-156): cols/8 texels a row pair
+            if (cols % 8) return vgx_fail(VGX_EINVAL, "vgx_mat_upload: t3 cols must be a multiple of 8");
             if (!w->row_plane) return vgx_fail(VGX_EINVAL, "vgx_mat_upload: t3 needs its part-3 row plane");
             need = (size_t)((rows + 1) / 2) * (size_t)(cols / 8) * 4;
             break;
@@ -188,7 +190,9 @@ int vgx_mat_upload(vgx_ctx* ctx, const vgx_weight_desc* w, vgx_mat** out) {
     m->d.rows = rows;
     m->d.cols = cols;
     m->body_bytes = need;
-    m->body_alloc_bytes = need;
+    // t3 texel rows padded to whole 32-column chunks (t3_rstride)
+    const size_t t3_src = (size_t)(cols / 8) * 4, t3_dst = w->kind == VGX_T3 ? (size_t)t3_rstride(cols) : 0;
+    m->body_alloc_bytes = w->kind == VGX_T3 ? (size_t)((rows + 1) / 2) * t3_dst : need;
     hipError_t e = hipMalloc(&m->body_alloc, m->body_alloc_bytes);
     if (e != hipSuccess) { delete m; return vgx_hip_fail(e, "hipMalloc(body)"); }
     m->d.body = static_cast<const uint8_t*>(m->body_alloc);
@@ -200,10 +204,16 @@ int vgx_mat_upload(vgx_ctx* ctx, const vgx_weight_desc* w, vgx_mat** out) {
         const uint8_t* src = static_cast<const uint8_t*>(w->body);
         for (size_t i = 0; i < need; ++i) tmp[i] = src[i] ^ 0x80u;
         e = hipMemcpy(m->body_alloc, tmp.data(), need, hipMemcpyHostToDevice);
+    } else if (w->kind == VGX_T3 && t3_dst != t3_src) {
+        e = hipMemset(m->body_alloc, 0, m->body_alloc_bytes);
+        if (e == hipSuccess)
+            e = hipMemcpy2D(m->body_alloc, t3_dst, w->body, t3_src, t3_src, (size_t)((rows + 1) / 2),
+                            hipMemcpyHostToDevice);
     } else {
         e = hipMemcpy(m->body_alloc, w->body, need, hipMemcpyHostToDevice);
     }
     if (e != hipSuccess) { vgx_mat_free(m); return vgx_hip_fail(e, "hipMemcpy(body)"); }
+    m->body_bytes = m->body_alloc_bytes;  // the bytes in HBM a kernel reads
 
     if (w->kind == VGX_Q4) {
         const size_t groups = (size_t)rows * (cols / 32);

@@ -344,7 +344,7 @@ __global__ void __launch_bounds__(256) argmax_keys_kernel(const unsigned long lo
 // then (X_RMS) the copies of x and of the norm weight, 16-byte aligned.
 __host__ __device__ inline size_t lds_bytes(int kind, int cols, int xm) {
     size_t b = kind == VGX_Q8 ? (size_t)(cols / 16) * 32
-               : kind == VGX_T3 ? (size_t)(cols / 32) * 64 + 256 * 4
+               : kind == VGX_T3 ? (size_t)t3_chunks(cols) * 64 + 256 * 4
                                 : (size_t)(cols / 32) * 64 + (size_t)(cols / 32) * 4;
     b = (b + 15) & ~(size_t)15;
     return xm == X_RMS ? b + (size_t)((cols + 7) & ~7) * 4 : b;
@@ -377,9 +377,9 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
     const MatDev M3 = L.md3;  // W3 of the gate epilogue (single-matrix launches)
 
     // --- weight chunk geometry
-    const int nch = KIND == VGX_Q8 ? (K >> 4) : (K >> 5);
+    const int nch = KIND == VGX_Q8 ? (K >> 4) : KIND == VGX_T3 ? t3_chunks(K) : (K >> 5);
     const size_t ustride = KIND == VGX_Q8 ? (size_t)K : KIND == VGX_Q4 ? (size_t)q4_rstride(K)
-                                                                     : (size_t)(K >> 3) * 4;
+                                                                     : (size_t)t3_rstride(K);
     const uint8_t* body3 = (EPI == EPI_GATE) ? M3.body : nullptr;
     const int niter = (nch + LPR - 1) / LPR;
 
@@ -968,7 +968,7 @@ __global__ void dequant_kernel(const MatDev M, float* out) {
             const float ma = (float)(int16_t)(sm >> 16) * M.ps;
             v = (float)nb * sa + ma;
         } else {
-            const size_t stride = (size_t)(M.cols / 8) * 4;
+            const size_t stride = (size_t)t3_rstride(M.cols);
             const uint8_t b = M.body[(size_t)(r / 2) * stride + (size_t)(c >> 3) * 4 + (r & 1) * 2 + ((c >> 2) & 1)];
             const unsigned code = (b >> (2 * (c & 3))) & 3u;
             const int lv = (code & 1u) ? ((code & 2u) ? -1 : 1) : 0;
@@ -1037,7 +1037,7 @@ KernFn pick_epi(int epi, int xm, int lpr, int ri, bool one) {
 // accumulators are cheap); q4 (fp64 group sums, more registers per chunk) and
 // t3 (two rows per chunk) use 8 lanes up to 48 chunks and 16 beyond.
 int vgx_gemv_plan(int kind, int rows, int cols, int num_cu, int* lpr, int* ri, int* rows_per_block) {
-    const int nch = kind == VGX_Q8 ? cols / 16 : cols / 32;
+    const int nch = kind == VGX_Q8 ? cols / 16 : kind == VGX_T3 ? t3_chunks(cols) : cols / 32;
     int l = 8;
     while (l < 64 && l * 4 < nch) l <<= 1;
     const int units = kind == VGX_T3 ? (rows + 1) / 2 : rows;

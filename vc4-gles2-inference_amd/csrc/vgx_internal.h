@@ -39,8 +39,9 @@ int vgx_hip_fail(hipError_t e, const char* what);
 //       share is loaded by one instruction), sm: rows x groups
 //       u32 = (u16)s16 | (u16)m16 << 16 (parts 1 and 2 interleaved so one
 //       4-byte load carries a group's scale and minimum), ps scalar.
-//   T3: body = the container's texel grid, ceil(rows/2) x cols/8 x 4 bytes;
-//       wsr: rows f32.
+//   T3: body = the container's texel grid, ceil(rows/2) texel rows of cols/8
+//       texels (4 bytes: 8 columns of a row pair), each row padded with zero
+//       codes to t3_rstride(cols) bytes; wsr: rows f32.
 struct MatDev {
     const uint8_t* body;
     const float* wsr;
@@ -55,6 +56,13 @@ struct MatDev {
 
 // Bytes from one q4 nibble row to the next in HBM.
 __host__ __device__ constexpr int q4_rstride(int cols) { return cols / 2; }
+
+// t3: 32-column chunks a texel row holds, and the bytes from one texel row
+// (row pair) to the next in HBM.  The container's rows hold cols/8 texels
+// (cols a multiple of 8); upload pads each to whole 32-column chunks of zero
+// codes, so every kernel reads whole 16-byte chunks inside the row.
+__host__ __device__ constexpr int t3_chunks(int cols) { return (cols + 31) / 32; }
+__host__ __device__ constexpr int t3_rstride(int cols) { return t3_chunks(cols) * 16; }
 
 struct vgx_ctx {
     int device = 0;

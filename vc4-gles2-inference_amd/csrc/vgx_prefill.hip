@@ -120,7 +120,7 @@ __device__ __forceinline__ uint4 w_raw(const MatDev& M, int n, int k0, int K) {
     if (KIND == VGX_Q4) {
         v = *reinterpret_cast<const uint2*>(M.body + (size_t)n * q4_rstride(K) + (k0 >> 1));
     } else {
-        const size_t ustride = (size_t)(K >> 3) * 4;
+        const size_t ustride = (size_t)t3_rstride(K);
         v = *reinterpret_cast<const uint2*>(M.body + (size_t)(n >> 1) * ustride + (size_t)(k0 >> 3) * 4);
     }
     return make_uint4(v.x, v.y, 0u, 0u);
@@ -283,8 +283,11 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmLaunch G) {
         uint32_t sm, sm3;
     };
     const int nn = nok ? n : M.rows - 1;
+    // (t3 rows are padded to whole 32-column chunks, so its clamp is the
+    // padded length: a last half step past K reads zero codes of its row)
+    const int Kw = KIND == VGX_T3 ? t3_chunks(K) * kTile : K;
     auto raw_load = [&](int s, Raw& r) {
-        const int k0 = min(s * kTile + half * 16, K - 16);
+        const int k0 = min(s * kTile + half * 16, Kw - 16);
         r.w = w_raw<KIND>(M, nn, k0, K);
         if (EPI == BEPI_GATE) r.w3 = w_raw<KIND>(G.M3, nn, k0, K);
         if (KIND == VGX_Q4) {
@@ -687,7 +690,9 @@ int launch(vgx_ctx* ctx, const vgx_mat* W, const vgx_mat* W3, int ntok, const in
     if (rw && !aligned16(rw)) return vgx_fail(VGX_EINVAL, std::string(who) + ": the RMSNorm weight must be 16-byte aligned");
     if (rw && !(eps > 0.0f)) return vgx_fail(VGX_EINVAL, std::string(who) + ": the RMSNorm epsilon must be positive");
     const MatDev& M = W->d;
-    if (M.cols % 16) return vgx_fail(VGX_EINVAL, std::string(who) + ": cols must be a multiple of 16");
+    if (M.cols % (M.kind == VGX_T3 ? 8 : 16))
+        return vgx_fail(VGX_EINVAL, std::string(who) + ": cols must be a multiple of " +
+                                        std::to_string(M.kind == VGX_T3 ? 8 : 16));
     VGX_HIP(hipSetDevice(ctx->device));
     GemmLaunch L{};
     L.M = M;
