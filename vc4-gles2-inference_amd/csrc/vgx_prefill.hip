@@ -223,8 +223,12 @@ __device__ __forceinline__ void rms_stats(const GemmLaunch& G, int t0, unsigned 
 // tiles; 8 when it has few (the decode batch of up to 32 sequences), so that
 // each wave walks fewer steps.  RMS: the input rows go through RMSNorm first,
 // the statistics formed in the workgroup.
+// Four-wave workgroups are built for two a CU (at most 256 VGPRs a lane):
+// left alone the compiler gave the q8 and q4 gate 260-280, one workgroup a
+// CU, and the 608-tile C3 gate ran in 2.4 rounds (q8 gate GEMM 10.4 -> 9.1
+// us, q4 14.5 -> 13.8, no spills).
 template <int KIND, int EPI, int NW, bool RMS, bool PART>
-__global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmLaunch G) {
+__global__ void __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) gemm_kernel(const GemmLaunch G) {
     constexpr int NT = 64 * NW;
     constexpr int NA = EPI == BEPI_STORE ? 1 : 2;  // accumulator sets: W1/W3 or the two halves
     constexpr int NPF = 4;                         // k-steps a round
