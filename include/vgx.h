@@ -225,9 +225,12 @@ int vgx_logits_argmax_rms_noalloc(vgx_ctx* ctx, const vgx_group* g, const int16_
  * tokens whose row tiles leave most CUs idle and whose rows are longer than
  * 32 k-steps (of 32 columns) splits K over up to 8 workgroups
  * and adds their exact integer sums in a second launch; the sums live in a
- * workspace of the context (hipMalloc at the first such call, at least 8 MiB,
- * grown on demand, freed by vgx_ctx_destroy).  Results are identical either
- * way; a workspace that cannot be allocated leaves the launch whole. */
+ * workspace of the context, sized for every such launch (8 splits x 2 sets x
+ * 32 tokens x num_cu/2 tiles of 32 rows, int64: 16 MiB at 256 CUs), allocated
+ * at the first such call and never regrown, freed by vgx_ctx_destroy.  No
+ * allocation happens under stream capture.  Results are identical either way;
+ * a launch without a workspace (capture before the first, or an allocation
+ * failure) runs whole. */
 int vgx_gemm(vgx_ctx* ctx, const vgx_mat* W, int ntok, const int16_t* x, const int16_t* res, int16_t* y);
 int vgx_gemm_add_split(vgx_ctx* ctx, const vgx_mat* W, int split, int ntok, const int16_t* x, const int16_t* res,
                        int16_t* y);
