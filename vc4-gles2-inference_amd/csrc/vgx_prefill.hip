@@ -254,7 +254,6 @@ __global__ void __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) gemm_kernel(const Ge
     const int n = n0 + li;  // this lane's weight row (B operand) and output column
     const int t = t0 + li;  // this lane's token row (A operand)
     const bool nok = n < M.rows;
-    const bool tok = t < G.ntok;
     // split K (PART): workgroup z of the launch's gridDim.z takes k-steps
     // [zs0, zs1) and stores its exact integer sums for the epilogue kernel
     const int nsteps = (K + kTile - 1) / kTile;
@@ -265,11 +264,13 @@ __global__ void __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) gemm_kernel(const Ge
 
     i32x16 ch[NA], cl[NA];
     long long dacc[NA][16];
+    long long cw[NA];  // q4: sum over the lane's groups of s16 * (the row's nibble sum)
     int wsum[NA];
 #pragma unroll
     for (int a = 0; a < NA; ++a) {
         ch[a] = (i32x16){};
         cl[a] = (i32x16){};
+        cw[a] = 0;
         wsum[a] = 0;
 #pragma unroll
         for (int r = 0; r < 16; ++r) dacc[a][r] = 0;
@@ -304,7 +305,8 @@ __global__ void __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) gemm_kernel(const Ge
     // 4i + l/16, the 16-byte piece l%16 of its 256 bytes -- and stored in the
     // wave's LDS block with piece q of token row r at q ^ (r & 7), so the 8
     // lanes of a matrix-core read group (rows r..r+7) hit 8 bank groups.
-    // Tokens past ntok read the last token (their operands are zeroed).
+    // Tokens past ntok read the last token (only their own outputs, never
+    // stored, see them).
     const int pc = lane & 15;
     auto x_load = [&](int s0, uint4 (&v)[8], uint4& wv) {
         const int col = min(s0 * kTile + pc * 8, K - 8);
@@ -375,18 +377,24 @@ __global__ void __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) gemm_kernel(const Ge
             const int s = s0 + j;
             if (s >= s_end) break;
             const int k0 = s * kTile + half * 16;
-            const bool kok = k0 < K;
             const int q0 = 4 * j + 2 * half;
             const unsigned char* row = s_xw + li * XROW;
             const uint4 x0 = *reinterpret_cast<const uint4*>(row + ((q0 ^ (li & 7)) << 4));
             const uint4 x1 = *reinterpret_cast<const uint4*>(row + (((q0 + 1) ^ (li & 7)) << 4));
+            // Operands are not masked for tokens past ntok or rows past M.rows:
+            // they feed only their own outputs, which are never stored.  Only a
+            // q8 row's last half step can lie past K (cols % 32 == 16): its
+            // weights become zeros (and leave the weight sum), so the clamped
+            // activation bytes there multiply nothing.  q4 rows are whole
+            // 32-column groups; a t3 row's padding holds zero codes.
+            const bool wok = KIND != VGX_Q8 || (K & 31) == 0 || k0 < K;
             Op xh, xl, w, w3;
             int xs, ws, ws3 = 0;
-            x_planes(x0, x1, tok && kok, xh, xl, xs);
-            w_planes<KIND>(rr[j].w, n, nok && kok, w, ws);
-            if (EPI == BEPI_GATE) w_planes<KIND>(rr[j].w3, n, nok && kok, w3, ws3);
-            const uint32_t sm = (KIND == VGX_Q4 && nok) ? rr[j].sm : 0u;
-            const uint32_t sm3 = (KIND == VGX_Q4 && EPI == BEPI_GATE && nok) ? rr[j].sm3 : 0u;
+            x_planes(x0, x1, true, xh, xl, xs);
+            w_planes<KIND>(rr[j].w, n, wok, w, ws);
+            if (EPI == BEPI_GATE) w_planes<KIND>(rr[j].w3, n, wok, w3, ws3);
+            const uint32_t sm = KIND == VGX_Q4 ? rr[j].sm : 0u;
+            const uint32_t sm3 = (KIND == VGX_Q4 && EPI == BEPI_GATE) ? rr[j].sm3 : 0u;
             raw_load(min(s + NPF, s_end - 1), rr[j]);
             if (KIND != VGX_Q4) {
                 if (EPI == BEPI_SPLIT) {
@@ -411,7 +419,10 @@ __global__ void __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) gemm_kernel(const Ge
                 }
             } else {
                 // one step = one 32-column group g = s: D = sum n*x exactly (|D| <
-                // 2^24), then the group's exact s16*D + m16*X in int64
+                // 2^24), then the group's exact s16*D + m16*X in int64.  D's
+                // 128*wg term (wg the row's nibble sum over the group) is the
+                // same for all of a lane's outputs: s16*wg goes into the lane's
+                // cw once, and 128*cw joins every output after the loop.
                 const i32x16 zero = {};
                 const int xg = xs + __shfl_xor(xs, 32, 64);  // token li's group sum
                 if (half == 0) s_xg[wave][li] = xg;
@@ -430,13 +441,20 @@ __global__ void __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) gemm_kernel(const Ge
                     const int wl = mm == 0 ? ws : ws3;
                     const int wg = wl + __shfl_xor(wl, 32, 64);
                     const uint32_t smm = mm == 0 ? sm : sm3;
-                    const long long sa = (int16_t)(smm & 0xFFFFu), ma = (int16_t)(smm >> 16);
+                    const int sa = (int16_t)(smm & 0xFFFFu), ma = (int16_t)(smm >> 16);
                     const int slot = EPI == BEPI_GATE ? mm : side;
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
-                        const int D = 256 * dh[r] + dl[r] + 128 * wg;
-                        dacc[slot][r] += sa * D + ma * X[r];
+                        const int Dp = 256 * dh[r] + dl[r];  // |Dp| < 2^24
+                        long long acc = dacc[slot][r];
+                        acc += (long long)sa * Dp;
+                        // (two chained 64-bit multiply-adds: left alone the
+                        // compiler forms sa*Dp + ma*X first, then a third add)
+                        asm("" : "+v"(acc));
+                        acc += (long long)ma * X[r];
+                        dacc[slot][r] = acc;
                     }
+                    cw[slot] += (long long)sa * wg;
                 }
             }
         }
@@ -459,7 +477,7 @@ __global__ void __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) gemm_kernel(const Ge
 #pragma unroll
         for (int r = 0; r < 16; ++r)
             s_red[((wave * NA + a) * 16 + r) * 64 + lane] =
-                KIND == VGX_Q4 ? dacc[a][r] : 256LL * ch[a][r] + (long long)cl[a][r];
+                KIND == VGX_Q4 ? dacc[a][r] + 128LL * cw[a] : 256LL * ch[a][r] + (long long)cl[a][r];
     if (KIND != VGX_Q4) {
 #pragma unroll
         for (int a = 0; a < NA; ++a) s_wsum[wave][a][lane] = wsum[a];
