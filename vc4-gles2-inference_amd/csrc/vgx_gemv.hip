@@ -514,7 +514,32 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
     const bool rms_fast = XM == X_RMS && K % 256 == 0 && K / 8 <= kRmsPieces;
     lmem_t<int16_t>* xr = nullptr;
     lmem_t<int16_t>* wr = nullptr;
-    if (XM == X_RMS) {
+    // rms_fast: thread t holds pieces t and t + kThreads (columns 8i..8i+7)
+    // of x and of the norm weight in registers from the load to the planes
+    const int npieces = K / 8;
+    u32x4_t rxa[kRmsPieces / kThreads], rwa[kRmsPieces / kThreads];
+    if (XM == X_RMS && rms_fast) {
+#pragma unroll
+        for (int it = 0; it < kRmsPieces / kThreads; ++it) {
+            if (it * kThreads >= npieces) break;
+            const int i = min((int)threadIdx.x + it * kThreads, npieces - 1);
+            rxa[it] = gld(reinterpret_cast<const u32x4_t*>(L.x + 8 * i));
+            rwa[it] = gld(reinterpret_cast<const u32x4_t*>(L.rw + 8 * i));
+        }
+#pragma unroll
+        for (int it = 0; it < kRmsPieces / kThreads; ++it) {
+            const int i = (int)threadIdx.x + it * kThreads;
+            if (i >= npieces) break;
+            long long P = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const long long lo = (int16_t)(rxa[it][k] & 0xFFFFu), hi = (int16_t)(rxa[it][k] >> 16);
+                P += lo * lo + hi * hi;
+            }
+            s_rpiece[i] = P;
+        }
+        __syncthreads();
+    } else if (XM == X_RMS) {
         xr = (lmem_t<int16_t>*)(reinterpret_cast<uint8_t*>(lds) + lds_bytes(KIND, K, X_I16));
         wr = xr + ((K + 7) & ~7);
         for (int i = threadIdx.x * 8; i < K; i += kThreads * 8) {
@@ -522,15 +547,6 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
             const u32x4_t b = gld(reinterpret_cast<const u32x4_t*>(L.rw + i));
             *reinterpret_cast<lmem_t<u32x4_t>*>(xr + i) = a;
             *reinterpret_cast<lmem_t<u32x4_t>*>(wr + i) = b;
-            if (rms_fast) {
-                long long P = 0;
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const long long lo = (int16_t)(a[k] & 0xFFFFu), hi = (int16_t)(a[k] >> 16);
-                    P += lo * lo + hi * hi;
-                }
-                s_rpiece[i >> 3] = P;
-            }
         }
         __syncthreads();
     }
@@ -569,7 +585,59 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
         rinv = (float)(1.0 / sqrt((double)(ss / (float)K + L.eps)));
     }
     int part[2] = {0, 0};
-    if (KIND == VGX_Q8) {
+    if (XM == X_RMS && rms_fast) {
+        // each thread normalises the pieces it holds (rms_elem, as load_x16
+        // does) and writes their bytes into the plane layout: q8 chunk i/2
+        // half i%2; t3 chunk i/4, sixteen-column half (i/2)%2, eight-byte
+        // half i%2; q4 group i/4, dword i%4 of each of its four planes (the
+        // even/odd split of planes8eo), the group's x sum joined over its
+        // four pieces' threads
+#pragma unroll
+        for (int it = 0; it < kRmsPieces / kThreads; ++it) {
+            if (it * kThreads >= npieces) break;
+            const int i = (int)threadIdx.x + it * kThreads;
+            const bool ok = i < npieces;
+            uint32_t d[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                d[k] = rms_elem(rxa[it][k] & 0xFFFFu, rwa[it][k] & 0xFFFFu, rinv) |
+                       (rms_elem(rxa[it][k] >> 16, rwa[it][k] >> 16, rinv) << 16);
+            if (KIND == VGX_Q4) {
+                const int c = i >> 2, q = i & 3;
+                uint32_t le, he, lo, ho;
+                planes8eo(d, le, he, lo, ho);
+                int X = 256 * (sdot4(he, 0x01010101u, 0) + sdot4(ho, 0x01010101u, 0)) +
+                        (int)(udot4(le, 0x01010101u, 0u) + udot4(lo, 0x01010101u, 0u));
+                X = ok ? X : 0;
+                X += shfl_xor(X, 1);
+                X += shfl_xor(X, 2);
+                if (ok) {
+                    reinterpret_cast<uint32_t*>(&lds[4 * c + 0])[q] = he;
+                    reinterpret_cast<uint32_t*>(&lds[4 * c + 1])[q] = le;
+                    reinterpret_cast<uint32_t*>(&lds[4 * c + 2])[q] = ho;
+                    reinterpret_cast<uint32_t*>(&lds[4 * c + 3])[q] = lo;
+                    if (q == 0) xg[c] = X;
+                }
+            } else if (ok) {
+                const uint2 xh = make_uint2(perm(d[1], d[0], 0x07050301u), perm(d[3], d[2], 0x07050301u));
+                const uint2 xl = make_uint2(perm(d[1], d[0], 0x06040200u), perm(d[3], d[2], 0x06040200u));
+                if (KIND == VGX_Q8) {
+                    const int c = i >> 1, hf = i & 1;
+                    const int hh = (EPI == EPI_SPLIT && c >= L.split_chunk) ? 1 : 0;
+                    reinterpret_cast<uint2*>(&lds[2 * c])[hf] = xh;
+                    reinterpret_cast<uint2*>(&lds[2 * c + 1])[hf] = xl;
+                    part[hh] = (int)udot4(xl.y, 0x01010101u, udot4(xl.x, 0x01010101u, (uint32_t)part[hh]));
+                } else {  // T3
+                    const int c = i >> 2, q = i & 3;
+                    const int hh = (EPI == EPI_SPLIT && c >= L.split_chunk) ? 1 : 0;
+                    reinterpret_cast<uint2*>(&lds[4 * c + (q >> 1)])[q & 1] = xh;
+                    reinterpret_cast<uint2*>(&lds[4 * c + 2 + (q >> 1)])[q & 1] = xl;
+                    part[hh] += 256 * (sdot4(xh.x, 0x01010101u, 0) + sdot4(xh.y, 0x01010101u, 0)) +
+                                (int)(udot4(xl.x, 0x01010101u, 0u) + udot4(xl.y, 0x01010101u, 0u));
+                }
+            }
+        }
+    } else if (KIND == VGX_Q8) {
         for (int c = threadIdx.x; c < nch; c += kThreads) {
             const int hh = (EPI == EPI_SPLIT && c >= L.split_chunk) ? 1 : 0;
             uint32_t d[8], xh[4], xl[4];
