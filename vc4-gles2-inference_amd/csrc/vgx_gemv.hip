@@ -44,6 +44,31 @@ __device__ __forceinline__ T shfl_xor(T v, int o) {
     return __shfl_xor(v, o, 64);
 }
 
+// The sum over the wave of integers held in doubles, every partial sum below
+// 2^53 (exact in any order): DPP exchanges within rows of 16 lanes
+// (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror),
+// then the four rows' totals by readlane.  Called with every lane active.
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double x) {
+    const unsigned long long b = __builtin_bit_cast(unsigned long long, x);
+    const unsigned lo = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)b, CTRL, 0xF, 0xF, false);
+    const unsigned hi = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)(b >> 32), CTRL, 0xF, 0xF, false);
+    return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+__device__ __forceinline__ double readlane_d(double x, int l) {
+    const unsigned long long b = __builtin_bit_cast(unsigned long long, x);
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, l);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(b >> 32), l);
+    return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+__device__ __forceinline__ double wave_sum_d(double x) {
+    x += dpp_d<0xB1>(x);
+    x += dpp_d<0x4E>(x);
+    x += dpp_d<0x141>(x);
+    x += dpp_d<0x140>(x);
+    return (readlane_d(x, 0) + readlane_d(x, 16)) + (readlane_d(x, 32) + readlane_d(x, 48));
+}
+
 // Global-memory views of the pointers in the launch descriptor.  The
 // descriptor arrives by value, so the compiler cannot tell that its pointers
 // address global memory and would emit flat accesses; a flat load also counts
@@ -576,8 +601,11 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
                 for (int k = 0; k < pps; ++k) P += s_rpiece[lane * pps + k];
                 t = (P + 8) >> 4;
             }
-            for (int o = 32; o >= 1; o >>= 1) t += shfl_xor(t, o);
-            tot = t;
+            // the 32 rounded slices (each below 2^32) added as doubles: every
+            // partial sum is an integer below 2^53, so the DPP row sums and
+            // the four rows' readlanes give the exact total (six dependent
+            // 64-bit cross-lane shuffles took longer)
+            tot = (long long)wave_sum_d((double)t);
         } else {
             for (int p = 0; p < 32; ++p) tot += s_rms[p];
         }
@@ -845,17 +873,30 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
             const uint4 xl0 = lds[4 * c + 2], xl1 = lds[4 * c + 3];
             const uint32_t xh[8] = {xh0.x, xh0.y, xh0.z, xh0.w, xh1.x, xh1.y, xh1.z, xh1.w};
             const uint32_t xl[8] = {xl0.x, xl0.y, xl0.z, xl0.w, xl1.x, xl1.y, xl1.z, xl1.w};
+            // every table entry of the chunk (both matrices) is read before
+            // the first product: left to the scheduler the lookups went out a
+            // few at a time, each group waited for in turn (one chunk a lane
+            // at the decode shapes, so nothing else covered those waits)
+            constexpr int NM = EPI == EPI_GATE ? 2 : 1;
+            uint32_t lv[NM][16];
 #pragma unroll
-            for (int m = 0; m < (EPI == EPI_GATE ? 2 : 1); ++m) {
+            for (int m = 0; m < NM; ++m) {
                 const uint4 wv = m == 0 ? wa : wb;
                 const uint32_t td[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) lv[m][4 * t + b] = lut[(td[t] >> (8 * b)) & 0xFFu];
+            }
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
                 int a1 = 0, b1 = 0;
                 uint32_t a2 = 0, b2 = 0;
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    const uint32_t T = td[t];
-                    const uint32_t l0 = lut[T & 0xFFu], l1 = lut[(T >> 8) & 0xFFu];
-                    const uint32_t l2 = lut[(T >> 16) & 0xFFu], l3 = lut[T >> 24];
+                    const uint32_t l0 = lv[m][4 * t], l1 = lv[m][4 * t + 1];
+                    const uint32_t l2 = lv[m][4 * t + 2], l3 = lv[m][4 * t + 3];
                     a1 = sdot4(l0, xh[2 * t], a1);
                     a1 = sdot4(l1, xh[2 * t + 1], a1);
                     a2 = udot4(l0, xl[2 * t], a2);
