@@ -408,7 +408,7 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
     const uint8_t* body3 = (EPI == EPI_GATE) ? M3.body : nullptr;
     const int niter = (nch + LPR - 1) / LPR;
 
-    // A workgroup takes row tiles blockIdx.x, blockIdx.x + gridDim.x, ...;
+    // A workgroup takes row tiles blockIdx.x, blockIdx.x + L.grid, ...;
     // x is staged once for all of them.  Per tile: the matrix descriptor (by
     // value in the launch arguments for up to kInlineMats matrices, else from
     // the device table), the tile's first weight chunk, and -- for one row per
@@ -1004,7 +1004,10 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
     }
     }
     }
-    tile += gridDim.x;
+    // the stride from the launch descriptor (L.grid is the launch's grid):
+    // gridDim.x is an implicit kernel argument in a cache line nothing else
+    // touches, and its load cost a memory round trip before the first tile
+    tile += L.grid;
     if (tile >= L.blocks) break;
     begin_tile(tile);
     }
@@ -1191,7 +1194,9 @@ int vgx_gemv_launch(const GemvLaunch& L, hipStream_t s) {
     if (L.blocks <= 0) return vgx_fail(VGX_EINVAL, "gemv: empty launch");
     const int grid = L.grid > 0 && L.grid < L.blocks ? L.grid : L.blocks;
     if (epi == EPI_STORE_ARGMAX && grid > L.nkeys) return vgx_fail(VGX_EINVAL, "gemv: more workgroups than key slots");
-    hipLaunchKernelGGL(fn, dim3(grid), dim3(kThreads), shm, s, L);
+    GemvLaunch Lk = L;
+    Lk.grid = grid;  // the kernel's tile stride
+    hipLaunchKernelGGL(fn, dim3(grid), dim3(kThreads), shm, s, Lk);
     VGX_LAUNCH_CHECK("gemv launch");
     if (epi == EPI_STORE_ARGMAX) {
         hipLaunchKernelGGL(argmax_keys_kernel, dim3(1), dim3(256), 0, s, L.argmax_key, grid, L.argmax_out, L.tail);

@@ -67,6 +67,8 @@ struct GemmLaunch {
     const int16_t* rw;      // RMS prologue: the q16 norm weight (cols values)
     float eps;              // RMS prologue: epsilon
     long long* part;        // split K: [split][set][ntok][rows] exact partial sums
+    int nz;                 // split K: the launch's splits (its grid's z; from here, not from
+                            // gridDim.z, an implicit argument whose load would delay the first weights)
 };
 
 union Op {
@@ -254,11 +256,11 @@ __global__ void __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) gemm_kernel(const Ge
     const int n = n0 + li;  // this lane's weight row (B operand) and output column
     const int t = t0 + li;  // this lane's token row (A operand)
     const bool nok = n < M.rows;
-    // split K (PART): workgroup z of the launch's gridDim.z takes k-steps
+    // split K (PART): workgroup z of the launch's G.nz takes k-steps
     // [zs0, zs1) and stores its exact integer sums for the epilogue kernel
     const int nsteps = (K + kTile - 1) / kTile;
-    const int zs0 = PART ? (int)(((long)nsteps * blockIdx.z) / gridDim.z) : 0;
-    const int zs1 = PART ? (int)(((long)nsteps * (blockIdx.z + 1)) / gridDim.z) : nsteps;
+    const int zs0 = PART ? (int)(((long)nsteps * blockIdx.z) / G.nz) : 0;
+    const int zs1 = PART ? (int)(((long)nsteps * (blockIdx.z + 1)) / G.nz) : nsteps;
     const int s_beg = zs0 + ((zs1 - zs0) * wave) / NW, s_end = zs0 + ((zs1 - zs0) * (wave + 1)) / NW;
     unsigned char* s_xw = s_dyn + (size_t)wave * XB;
 
@@ -740,6 +742,7 @@ int launch(vgx_ctx* ctx, const vgx_mat* W, const vgx_mat* W3, int ntok, const in
         if (!workspace(ctx, bytes, &L.part)) nz = 1;  // no workspace: one pass
         grid.z = nz;
     }
+    L.nz = nz;
     const int nw = nz > 1 ? 4 : waves_for((int)(grid.x * grid.y), nsteps, ctx->num_cu);
     GemmFn fn = pick(epi, M.kind, nw, rw != nullptr, nz > 1);
     if (!fn) return vgx_fail(VGX_EINVAL, std::string(who) + ": unknown weight kind");
