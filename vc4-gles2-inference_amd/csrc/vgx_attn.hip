@@ -334,13 +334,49 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     // (blockIdx.y: a batch of consecutive positions of one sequence, pos_step
     // 1; or the same position of consecutive sequences, each with its own
     // cache seq_stride bytes on, pos_step 0)
+    kv += (size_t)blockIdx.y * seq_stride;
+    qkv += (size_t)blockIdx.y * (A.dim + 2 * kv_dim);
+    if (out) out += (size_t)blockIdx.y * A.dim;
+    const int16_t* kq = qkv + A.dim + kvh * hd;           // this group's K (q16)
+    const int16_t* vq = qkv + A.dim + kv_dim + kvh * hd;  // and V
+    const int16_t* qh = qkv + h * hd;                     // this head's q
+
+    // --- every global read of the launch is issued before any store, so
+    // that their latencies overlap.  First the ones that do not depend on the
+    // position: this thread's element i = tid of q, K, V with its RoPE partner
+    // j, the norm weights, the elements of the sums of squares; they go out
+    // ahead of the position's own load (a launch replayed from a graph reads
+    // it from device memory, and everything below waits for it).  Then the
+    // rotation, the K vectors of this thread's first scored position (lpp
+    // lanes per position, vectors sj, sj+lpp, ...) and the V values of its
+    // element in its wave's chunk of the first round of the weighted-V pass
+    // (below).  The element loads are unconditional, from clamped in-range
+    // addresses, and unused values are discarded afterwards (a select between
+    // a load and a constant would become a branch whose load is waited for
+    // before the next one issues).  The K and V row loads are buffer loads
+    // bounded to the rows below npos.
+    const bool el = tid < hd;
+    const int ie = min(tid, hd - 1);
+    int j, ti;
+    bool first;
+    rope_pair(A.rope_half, hd, ie, j, ti, first);
+    const int16_t* knp = A.qk_norm ? kn : kq;
+    const int16_t* qnp = A.qk_norm ? qn : qh;
+    const int kqi = kq[ie], kqj = kq[j], vqi = vq[ie], qhi = qh[ie], qhj = qh[j];
+    const int kni = knp[ie], knj = knp[j], qni = qnp[ie], qnj = qnp[j];
+    int ke[4], qe[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int l = min(lane + 64 * c, hd - 1);
+        ke[c] = kq[l];
+        qe[c] = qh[l];
+    }
+    asm volatile("" ::: "memory");
+
     // pos_ptr: the position read from device memory (a launch captured once
     // and replayed for every token), clamped into the cache
     const int p0 = pos_ptr ? min(max(*pos_ptr, 0), A.seq - 1) : pos0;
     const int pos = p0 + blockIdx.y * pos_step;
-    kv += (size_t)blockIdx.y * seq_stride;
-    qkv += (size_t)blockIdx.y * (A.dim + 2 * kv_dim);
-    if (out) out += (size_t)blockIdx.y * A.dim;
     const int npos = pos + 1;
     const int nch = (npos + kChunk - 1) / kChunk;
     const bool own_row = do_write != 0;  // row pos comes from LDS, not from HBM
@@ -362,39 +398,8 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     uint8_t* const vhead_w = kv + (size_t)(A.kv_heads + kvh) * A.seq * A.pstride;
     const uint8_t* khead = khead_w;
     const uint8_t* vhead = vhead_w;
-    const int16_t* kq = qkv + A.dim + kvh * hd;           // this group's K (q16)
-    const int16_t* vq = qkv + A.dim + kv_dim + kvh * hd;  // and V
-    const int16_t* qh = qkv + h * hd;                     // this head's q
     const int32_t* rt = rtab + (size_t)pos * (hd / 2) * 2;
-
-    // --- every global read of the launch is issued here, before any store,
-    // so that their latencies overlap: this thread's element i = tid of q, K,
-    // V with its RoPE partner j, the rotation, the norm weights; the elements
-    // of the sums of squares; the K vectors of its first scored position (lpp
-    // lanes per position, vectors sj, sj+lpp, ...) and the V values of its
-    // element in its wave's chunk of the first round of the weighted-V pass
-    // (below).  The element loads are unconditional, from clamped
-    // in-range addresses, and unused values are discarded afterwards (a
-    // select between a load and a constant would become a branch whose load
-    // is waited for before the next one issues).  The K and V row loads are
-    // buffer loads bounded to the rows below npos.
-    const bool el = tid < hd;
-    const int ie = min(tid, hd - 1);
-    int j, ti;
-    bool first;
-    rope_pair(A.rope_half, hd, ie, j, ti, first);
-    const int16_t* knp = A.qk_norm ? kn : kq;
-    const int16_t* qnp = A.qk_norm ? qn : qh;
     const int rc = rt[2 * ti], rs = rt[2 * ti + 1];
-    const int kqi = kq[ie], kqj = kq[j], vqi = vq[ie], qhi = qh[ie], qhj = qh[j];
-    const int kni = knp[ie], knj = knp[j], qni = qnp[ie], qnj = qnp[j];
-    int ke[4], qe[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const int l = min(lane + 64 * c, hd - 1);
-        ke[c] = kq[l];
-        qe[c] = qh[l];
-    }
     const int nv = hd * KVB / 128;  // 16-byte vectors per K row slice
     const int lpp = A.lpp, sj = tid & (lpp - 1), P = kThreads / lpp;
     // weighted-V lanes: wave w takes chunk slot w / vG of each round and the
