@@ -223,14 +223,14 @@ __device__ __forceinline__ void rms_stats(const GemmLaunch& G, int t0, unsigned 
 // sums in LDS, and every thread adds the waves' sums for its outputs of the
 // tile and applies the epilogue.  NW = 4 when the launch has many
 // tiles; 8 when it has few (the decode batch of up to 32 sequences), so that
-// each wave walks fewer steps.  RMS: the input rows go through RMSNorm first,
-// the statistics formed in the workgroup.
-// Four-wave workgroups are built for two a CU (at most 256 VGPRs a lane):
-// left alone the compiler gave the q8 and q4 gate 260-280, one workgroup a
-// CU, and the 608-tile C3 gate ran in 2.4 rounds (q8 gate GEMM 10.4 -> 9.1
-// us, q4 14.5 -> 13.8, no spills).
+// each wave walks fewer steps; 2 above two tiles a CU.  RMS: the input rows go
+// through RMSNorm first, the statistics formed in the workgroup.
+// Two- and four-wave workgroups are built for two waves a SIMD (at most 256
+// VGPRs a lane): left alone the compiler gave the q8 and q4 gate 260-280, one
+// workgroup a CU, and the 608-tile C3 gate ran in 2.4 rounds (q8 gate GEMM
+// 10.4 -> 9.1 us, q4 14.5 -> 13.8, no spills).
 template <int KIND, int EPI, int NW, bool RMS, bool PART>
-__global__ void __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) gemm_kernel(const GemmLaunch G) {
+__global__ void __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) gemm_kernel(const GemmLaunch G) {
     constexpr int NT = 64 * NW;
     constexpr int NA = EPI == BEPI_STORE ? 1 : 2;  // accumulator sets: W1/W3 or the two halves
     constexpr int NPF = 4;                         // k-steps a round
@@ -633,6 +633,7 @@ template <int EPI, bool RMS>
 GemmFn pick_nw(int kind, int nw, bool part) {
     if (part) return nw == 4 ? pick_kind<EPI, 4, RMS, true>(kind) : nullptr;
     switch (nw) {
+        case 2: return pick_kind<EPI, 2, RMS, false>(kind);
         case 4: return pick_kind<EPI, 4, RMS, false>(kind);
         case 8: return pick_kind<EPI, 8, RMS, false>(kind);
     }
@@ -696,8 +697,12 @@ bool workspace(vgx_ctx* ctx, size_t bytes, long long** out) {
 // few row tiles: a decode batch, a short prompt) 8 when the row has more than
 // 16 k-steps, so the tiles' k-steps are spread over more waves.  (16 waves
 // would cap a lane at 128 registers and spill the operands in flight; 8 waves
-// with four steps in flight keep as many bytes in flight per CU.)
+// with four steps in flight keep as many bytes in flight per CU.)  Above two
+// tiles a CU, 2: four 2-wave workgroups fit a CU, so the launch still runs in
+// one round (the 256-token q4 gate, 608 tiles: 22.5 -> 21.1 us; with 4 waves
+// its last 96 tiles started when the first round ended).
 int waves_for(int tiles, int nsteps, int num_cu) {
+    if (tiles > 2 * num_cu) return 2;
     return tiles < num_cu && nsteps > 16 ? 8 : 4;
 }
 
@@ -751,8 +756,8 @@ int launch(vgx_ctx* ctx, const vgx_mat* W, const vgx_mat* W3, int ntok, const in
     const int na = epi == BEPI_STORE ? 1 : 2;
     const int lds = std::max(nw * kTile * 4 * kTile * 2, nw * na * 16 * 64 * 8);
     if (lds > 48 * 1024) {
-        static bool lds_set[128];
-        const int slot = (((epi * 2 + (rw ? 1 : 0)) * 4 + M.kind) * 2 + (nw == 8 ? 1 : 0)) * 2 + (nz > 1 ? 1 : 0);
+        static bool lds_set[256];
+        const int slot = (((epi * 2 + (rw ? 1 : 0)) * 4 + M.kind) * 3 + (nw == 8 ? 2 : nw == 4 ? 1 : 0)) * 2 + (nz > 1 ? 1 : 0);
         if (!lds_set[slot]) {
             VGX_HIP(hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds));
             lds_set[slot] = true;
