@@ -44,8 +44,8 @@ __device__ __forceinline__ T shfl_xor(T v, int o) {
     return __shfl_xor(v, o, 64);
 }
 
-// The sum over the wave of integers held in doubles, every partial sum below
-// 2^53 (exact in any order): DPP exchanges within rows of 16 lanes
+// Sums over the wave (integers, or integers held in doubles with every
+// partial sum below 2^53: exact in any order): DPP exchanges within rows of 16 lanes
 // (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror),
 // then the four rows' totals by readlane.  Called with every lane active.
 template <int CTRL>
@@ -60,6 +60,14 @@ __device__ __forceinline__ double readlane_d(double x, int l) {
     const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, l);
     const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(b >> 32), l);
     return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+__device__ __forceinline__ int wave_sum_i(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false);
+    return (__builtin_amdgcn_readlane(x, 0) + __builtin_amdgcn_readlane(x, 16)) +
+           (__builtin_amdgcn_readlane(x, 32) + __builtin_amdgcn_readlane(x, 48));
 }
 __device__ __forceinline__ double wave_sum_d(double x) {
     x += dpp_d<0xB1>(x);
@@ -388,6 +396,27 @@ __host__ __device__ inline size_t lds_bytes(int kind, int cols, int xm) {
 template <int KIND, int LPR, int RI, int EPI, int XM, bool ONE>
 __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
     extern __shared__ uint4 lds[];
+    // Every kernel argument the launch reads, in scalar registers before
+    // anything else: the argument loads then go out as one batch.  Left to
+    // the compiler, the arguments past the matrix descriptor came in two more
+    // round trips, the x pointer's after the workgroup's first barrier.
+    // (one statement: a wait for its operands covers the whole batch; fields
+    // a variant does not read are constants here)
+    {
+        const MatDev m0 = ONE ? kernarg_mat0() : MatDev{};
+        const void* xin = XM == X_F32 ? (const void*)L.xf : (const void*)L.x;
+        const int16_t* rw0 = XM == X_RMS ? L.rw : nullptr;
+        const float eps0 = XM == X_RMS ? L.eps : 0.0f;
+        const int hs0 = EPI == EPI_GATE ? L.hs : 0;
+        const uint8_t* b3 = EPI == EPI_GATE ? L.md3.body : nullptr;
+        const float* w3 = EPI == EPI_GATE ? L.md3.wsr : nullptr;
+        const uint32_t* s3 = EPI == EPI_GATE ? L.md3.sm : nullptr;
+        const float p3 = EPI == EPI_GATE ? L.md3.ps : 0.0f;
+        const int sc0 = EPI == EPI_SPLIT ? L.split_chunk : 0;
+        asm volatile("" ::"s"(L.cols), "s"(L.blocks), "s"(L.grid), "s"(L.res), "s"(L.y), "s"(xin), "s"(rw0),
+                     "s"(eps0), "s"(hs0), "s"(b3), "s"(w3), "s"(s3), "s"(p3), "s"(sc0), "s"(m0.body), "s"(m0.wsr),
+                     "s"(m0.sm), "s"(m0.ps), "s"(m0.rows), "s"(m0.out_off), "s"(m0.blk_off));
+    }
     constexpr int RPI = 64 / LPR;
     constexpr int NV = (EPI == EPI_GATE || EPI == EPI_SPLIT) ? 2 : 1;
     // rows a wave owns: t3 counts row *pairs*
@@ -509,8 +538,7 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
     // --- stage x planes (and the row-independent sums) in LDS
     // the byte split's bias sums, per column half (the split epilogue adds the
     // two halves separately; every other epilogue uses their total)
-    __shared__ int s_xsum[2];
-    if (threadIdx.x < 2) s_xsum[threadIdx.x] = 0;
+    __shared__ int s_xpart[kWaves][2];  // each wave's share of the two sums (no clearing, no atomics)
     uint32_t* lut = nullptr;
     int* xg = nullptr;
     const int plane_u4 = KIND == VGX_Q8 ? 2 * nch : 4 * nch;  // uint4 per plane block
@@ -589,7 +617,7 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
         for (int o = 4; o >= 1; o >>= 1) P += shfl_xor(P, o);
         if (sub == 0) s_rms[p] = (P + 8) >> 4;
     }
-    if (!rms_fast) __syncthreads();
+    if (XM == X_RMS && !rms_fast) __syncthreads();
     float rinv = 0.0f;
     if (XM == X_RMS) {
         long long tot = 0;
@@ -717,17 +745,21 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
         }
     }
     if (KIND != VGX_Q4) {
-        for (int o = 32; o >= 1; o >>= 1) {
-            part[0] += shfl_xor(part[0], o);
-            part[1] += shfl_xor(part[1], o);
-        }
+        const int p0 = wave_sum_i(part[0]), p1 = EPI == EPI_SPLIT ? wave_sum_i(part[1]) : 0;
         if (lane == 0) {
-            atomicAdd(&s_xsum[0], part[0]);
-            atomicAdd(&s_xsum[1], part[1]);
+            s_xpart[wave][0] = p0;
+            s_xpart[wave][1] = p1;
         }
     }
     __syncthreads();
-    const int xs0 = KIND == VGX_Q4 ? 0 : s_xsum[0], xs1 = KIND == VGX_Q4 ? 0 : s_xsum[1];
+    int xs0 = 0, xs1 = 0;
+    if (KIND != VGX_Q4) {
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            xs0 += s_xpart[w][0];
+            xs1 += s_xpart[w][1];
+        }
+    }
 
     unsigned long long akey = 0ull;  // EPI_STORE_ARGMAX: this lane's best key
     for (int tile = blockIdx.x;;) {
