@@ -312,11 +312,12 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     // Every kernel argument in scalar registers before the first branch: the
     // argument loads then issue as one batch instead of one round trip at
     // each place of first use.
+    // (one statement: a wait for its operands covers the whole batch; two
+    // statements were waited for one after the other)
     asm volatile("" ::"s"(kv), "s"(rtab), "s"(qn), "s"(kn), "s"(qkv), "s"(out), "s"(pos0), "s"(do_write),
-                 "s"(do_attend), "s"(seq_stride), "s"(pos_step), "s"(pos_ptr));
-    asm volatile("" ::"s"(A.dim), "s"(A.kv_heads), "s"(A.hd), "s"(A.seq), "s"(A.rope_half), "s"(A.qk_norm),
-                 "s"(A.group), "s"(A.pstride), "s"(A.lpp), "s"(A.vG1), "s"(A.vC1), "s"(A.vG2), "s"(A.vC2),
-                 "s"(A.nchmax), "s"(A.o_wmax),
+                 "s"(do_attend), "s"(seq_stride), "s"(pos_step), "s"(pos_ptr), "s"(A.dim), "s"(A.kv_heads),
+                 "s"(A.hd), "s"(A.seq), "s"(A.rope_half), "s"(A.qk_norm), "s"(A.group), "s"(A.pstride),
+                 "s"(A.lpp), "s"(A.vG1), "s"(A.vC1), "s"(A.vG2), "s"(A.vC2), "s"(A.nchmax), "s"(A.o_wmax),
                  "s"(A.o_vpk), "s"(A.o_kpk), "s"(A.o_qhw), "s"(A.o_qlw), "s"(A.o_sc), "s"(A.o_ep), "s"(A.o_csum),
                  "s"(A.o_vpart), "s"(A.o_acc));
     constexpr int E = KVB == 16 ? 2 : 4;  // values per 32-bit word

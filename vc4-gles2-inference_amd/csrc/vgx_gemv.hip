@@ -333,11 +333,17 @@ __global__ void __launch_bounds__(256) argmax_keys_kernel(const unsigned long lo
                                                           const StepTail T) {
     __shared__ unsigned long long s_k[4];
     __shared__ int s_tok;
+    // every argument in scalar registers first, one batch of loads (left to
+    // the compiler they came in several dependent round trips); the loop
+    // stride is the launch's 256 threads, not blockDim.x (an implicit
+    // argument in a line of its own)
+    asm volatile("" ::"s"(keys), "s"(n), "s"(out), "s"(T.pos), "s"(T.hist), "s"(T.hist_len), "s"(T.emb),
+                 "s"(T.emb_scale), "s"(T.vocab), "s"(T.dim), "s"(T.x));
     // the position (read before the keys: only this launch writes it, at its
     // end) so the bookkeeping below waits for no further round trip
     const int p = T.pos && threadIdx.x == 0 ? *T.pos : 0;
     unsigned long long key = 0ull;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) key = keys[i] > key ? keys[i] : key;
+    for (int i = threadIdx.x; i < n; i += 256) key = keys[i] > key ? keys[i] : key;
     for (int o = 32; o >= 1; o >>= 1) {
         const unsigned long long other = __shfl_xor(key, o, 64);
         key = other > key ? other : key;
@@ -364,7 +370,7 @@ __global__ void __launch_bounds__(256) argmax_keys_kernel(const unsigned long lo
     if (tok < 0) tok = 0;
     if (tok >= T.vocab) tok = T.vocab - 1;
     const float sc = T.emb_scale[tok];
-    for (int i = threadIdx.x; i < T.dim; i += blockDim.x) {
+    for (int i = threadIdx.x; i < T.dim; i += 256) {
         const float v = (float)T.emb[(size_t)tok * T.dim + i] * sc;
         float r = __builtin_rintf(v * 256.0f);
         r = fminf(fmaxf(r, -32768.0f), 32767.0f);

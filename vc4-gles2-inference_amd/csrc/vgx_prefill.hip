@@ -237,6 +237,24 @@ __global__ void __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) gemm_kernel(const Ge
     // LDS: each wave's activation block for a round (32 tokens x NPF steps of
     // 32 columns, int16: 256 bytes a token), reused for the reduction once
     // every wave is past its last round
+    // every kernel argument the launch reads, in scalar registers first: one
+    // batch of loads instead of a round trip at each first use (fields a
+    // variant does not read are constants here)
+    {
+        const uint8_t* b3 = EPI == BEPI_GATE ? G.M3.body : nullptr;
+        const float* w3 = EPI == BEPI_GATE ? G.M3.wsr : nullptr;
+        const uint32_t* s3 = EPI == BEPI_GATE ? G.M3.sm : nullptr;
+        const float p3 = EPI == BEPI_GATE ? G.M3.ps : 0.0f;
+        const int hs0 = EPI == BEPI_GATE ? G.hs : 0;
+        const int sp0 = EPI == BEPI_SPLIT ? G.split : 0;
+        const int16_t* rw0 = RMS ? G.rw : nullptr;
+        const float eps0 = RMS ? G.eps : 0.0f;
+        long long* part0 = PART ? G.part : nullptr;
+        const int nz0 = PART ? G.nz : 1;
+        asm volatile("" ::"s"(G.M.body), "s"(G.M.wsr), "s"(G.M.sm), "s"(G.M.ps), "s"(G.M.rows), "s"(G.ntok),
+                     "s"(G.cols), "s"(G.x), "s"(G.ldx), "s"(G.res), "s"(G.y), "s"(G.ldy), "s"(b3), "s"(w3),
+                     "s"(s3), "s"(p3), "s"(hs0), "s"(sp0), "s"(rw0), "s"(eps0), "s"(part0), "s"(nz0));
+    }
     extern __shared__ __align__(16) unsigned char s_dyn[];
     __shared__ int s_wsum[NW][NA][64];  // each wave's weight sums per lane
     __shared__ int s_xg[NW][kTile];  // q4: this step's group sum of x per token
@@ -566,8 +584,15 @@ __device__ __forceinline__ int16_t epi_value(const GemmLaunch& G, int nz, int tt
 
 // The epilogue of a split-K launch: a thread per output row n of token
 // blockIdx.y.
+// Every argument an epilogue launch reads, in scalar registers in one batch
+// of loads (left to the compiler they came in three or four round trips).
+#define VGX_EPI_ARGS(G, nz)                                                                                      \
+    asm volatile("" ::"s"(G.M.rows), "s"(G.M.kind), "s"(G.M.ps), "s"(G.M.wsr), "s"(G.M3.ps), "s"(G.M3.wsr),  \
+                 "s"(G.part), "s"(G.ntok), "s"(G.res), "s"(G.y), "s"(G.ldy), "s"(G.hs), "s"(nz))
+
 template <int EPI>
 __global__ void __launch_bounds__(256) gemm_epi_kernel(const GemmLaunch G, int nz) {
+    VGX_EPI_ARGS(G, nz);
     const int n = blockIdx.x * 256 + threadIdx.x, tt = blockIdx.y;
     if (n >= G.M.rows) return;
     G.y[(size_t)tt * G.ldy + n] = epi_value<EPI>(G, nz, tt, n);
@@ -582,6 +607,9 @@ constexpr int kNormThreads = 1024;  // a row of up to 1024 values: one value a t
 template <int EPI>
 __global__ void __launch_bounds__(kNormThreads) gemm_epi_norm_kernel(const GemmLaunch G, int nz, const int16_t* nw,
                                                                      float neps, int16_t* yn) {
+    asm volatile("" ::"s"(G.M.rows), "s"(G.M.kind), "s"(G.M.ps), "s"(G.M.wsr), "s"(G.M3.ps), "s"(G.M3.wsr),
+                 "s"(G.part), "s"(G.ntok), "s"(G.res), "s"(G.y), "s"(G.ldy), "s"(G.hs), "s"(nz), "s"(nw), "s"(neps),
+                 "s"(yn));
     extern __shared__ __align__(16) unsigned char s_dyn[];
     int16_t* row = reinterpret_cast<int16_t*>(s_dyn);
     __shared__ long long part[32];
