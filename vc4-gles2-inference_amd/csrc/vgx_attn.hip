@@ -363,8 +363,16 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     rope_pair(A.rope_half, hd, ie, j, ti, first);
     const int16_t* knp = A.qk_norm ? kn : kq;
     const int16_t* qnp = A.qk_norm ? qn : qh;
-    const int kqi = kq[ie], kqj = kq[j], vqi = vq[ie], qhi = qh[ie], qhj = qh[j];
-    const int kni = knp[ie], knj = knp[j], qni = qnp[ie], qnj = qnp[j];
+    // (a wave with no element of the head below head_dim issues none of the
+    // per-element loads: a wave-uniform branch, so the loads of a wave that
+    // does need them still go out back to back)
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    const bool welm = wave_u * 64 < hd;
+    int kqi = 0, kqj = 0, vqi = 0, qhi = 0, qhj = 0, kni = 0, knj = 0, qni = 0, qnj = 0;
+    if (welm) {
+        kqi = kq[ie]; kqj = kq[j]; vqi = vq[ie]; qhi = qh[ie]; qhj = qh[j];
+        kni = knp[ie]; knj = knp[j]; qni = qnp[ie]; qnj = qnp[j];
+    }
     int ke[4], qe[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -400,7 +408,11 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     const uint8_t* khead = khead_w;
     const uint8_t* vhead = vhead_w;
     const int32_t* rt = rtab + (size_t)pos * (hd / 2) * 2;
-    const int rc = rt[2 * ti], rs = rt[2 * ti + 1];
+    int rc = 0, rs = 0;
+    if (welm) {
+        rc = rt[2 * ti];
+        rs = rt[2 * ti + 1];
+    }
     const int nv = hd * KVB / 128;  // 16-byte vectors per K row slice
     const int lpp = A.lpp, sj = tid & (lpp - 1), P = kThreads / lpp;
     // weighted-V lanes: wave w takes chunk slot w / vG of each round and the
@@ -434,8 +446,16 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     }
     // the K loads first: the scores wait for them, not for the V loads after
     asm volatile("" ::: "memory");
-    if (pair) v_pair_load<KVB>(A, vrs, pch, pvi, vch);
-    else v_chunk_load<KVB>(A, vrs, vE, slot < vC ? slot : A.nchmax, vi, vch);
+    // a wave whose first-round chunk lies past the context issues no V loads
+    // (a wave-uniform branch; such a wave does not read vch in that round):
+    // every V load takes the CU's address unit whether it reads memory or not
+    if (pair ? 2 * wave_u < nch : (slot < vC && slot < nch)) {
+        if (pair) v_pair_load<KVB>(A, vrs, pch, pvi, vch);
+        else v_chunk_load<KVB>(A, vrs, vE, slot, vi, vch);
+    } else {
+#pragma unroll
+        for (int u = 0; u < kChunk; ++u) vch[u] = 0;
+    }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         keep(ke[c]);
@@ -630,7 +650,12 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
             const int nr = min(kPC, nch - c0);
             const bool more = c0 + kPC < nch;
             int vnx[kChunk];
-            if (more) v_pair_load<KVB>(A, vrs, c0 + kPC + pch, pvi, vnx);
+            if (more && c0 + kPC + 2 * wave_u < nch) {
+                v_pair_load<KVB>(A, vrs, c0 + kPC + pch, pvi, vnx);
+            } else {
+#pragma unroll
+                for (int u = 0; u < kChunk; ++u) vnx[u] = 0;
+            }
             if (2 * wave < nr) {
                 const int c = c0 + pch;  // this lane's chunk (past nch: weights zero)
                 const int tlo = c * kChunk + (lane & 15), thi = tlo + 16, tmax = A.nchmax * kChunk - 1;
@@ -694,7 +719,12 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
         // the next round's V values load while this round is summed
         const bool more = c0 + vC < nch;
         int vnx[kChunk];
-        if (more) v_chunk_load<KVB>(A, vrs, vE, slot < vC ? c0 + vC + slot : A.nchmax, vi, vnx);
+        if (more && slot < vC && c0 + vC + slot < nch) {
+            v_chunk_load<KVB>(A, vrs, vE, c0 + vC + slot, vi, vnx);
+        } else {
+#pragma unroll
+            for (int u = 0; u < kChunk; ++u) vnx[u] = 0;
+        }
         if (slot < nr) {
             const int c = c0 + slot;
             // lane 16r + n: the weights of the chunk's positions n (lo) and
