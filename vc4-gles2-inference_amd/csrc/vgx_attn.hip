@@ -155,6 +155,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const uint8_t* base,
 // load and a constant is otherwise lowered to a branch around the load, and a
 // load under a branch is waited for before the next one issues.
 __device__ __forceinline__ void keep(int& x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void keep(uint16_t& x) { asm volatile("" : "+v"(x)); }
+// A 16-bit field as loaded, and its signed value.
+__device__ __forceinline__ uint16_t u16_at(const int16_t* p, int i) { return reinterpret_cast<const uint16_t*>(p)[i]; }
+__device__ __forceinline__ int s16(uint16_t raw) { return (int)(int16_t)raw; }
 __device__ __forceinline__ void keep(int4& x) { asm volatile("" : "+v"(x.x), "+v"(x.y), "+v"(x.z), "+v"(x.w)); }
 
 // The query split into bytes for the packed integer dot products: q = 256*qh
@@ -368,17 +372,26 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     // does need them still go out back to back)
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     const bool welm = wave_u * 64 < hd;
-    int kqi = 0, kqj = 0, vqi = 0, qhi = 0, qhj = 0, kni = 0, knj = 0, qni = 0, qnj = 0;
+    uint16_t kqr = 0, kqjr = 0, vqr = 0, qhr = 0, qhjr = 0, knr = 0, knjr = 0, qnr = 0, qnjr = 0;
+    // the whole head's K and q for the sums of squares, which only the
+    // threads of an element use: loaded by those waves alone, 64 elements a
+    // load (every vector load of the launch takes the CU's address unit, the
+    // unit the loads at the start of the launch queue for)
+    // (the values are held as loaded, zero-extended 16-bit fields, and
+    // sign-extended where they are first used: a value converted where the
+    // branch joins is waited for there, before the loads below issue)
+    uint16_t ker[4] = {0, 0, 0, 0}, qer[4] = {0, 0, 0, 0};
     if (welm) {
-        kqi = kq[ie]; kqj = kq[j]; vqi = vq[ie]; qhi = qh[ie]; qhj = qh[j];
-        kni = knp[ie]; knj = knp[j]; qni = qnp[ie]; qnj = qnp[j];
-    }
-    int ke[4], qe[4];
+        kqr = u16_at(kq, ie); kqjr = u16_at(kq, j); vqr = u16_at(vq, ie); qhr = u16_at(qh, ie); qhjr = u16_at(qh, j);
+        knr = u16_at(knp, ie); knjr = u16_at(knp, j); qnr = u16_at(qnp, ie); qnjr = u16_at(qnp, j);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const int l = min(lane + 64 * c, hd - 1);
-        ke[c] = kq[l];
-        qe[c] = qh[l];
+        for (int c = 0; c < 4; ++c) {
+            if (64 * c < hd) {
+                const int l = min(lane + 64 * c, hd - 1);
+                ker[c] = u16_at(kq, l);
+                qer[c] = u16_at(qh, l);
+            }
+        }
     }
     asm volatile("" ::: "memory");
 
@@ -436,13 +449,23 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     // rows 0..npos-1 of this head's K and V slices
     const __amdgpu_buffer_rsrc_t krs = rows_rsrc(khead, npos * A.pstride);
     const __amdgpu_buffer_rsrc_t vrs = rows_rsrc(vhead, npos * A.pstride);
+    // vector slots k a lane takes: sj + k*lpp < nv for some lane when k < nk;
+    // the slots from nk on are past the row in every lane, and their loads
+    // are skipped here (wave-uniform branches)
+    const int nk = (nv + lpp - 1) / lpp;
     {
-        // only the lanes of a scored position read its K row
+        // only the lanes of a scored position read its K row, and a wave
+        // whose first position lies past the context issues no K load
         const int t = min(tid / lpp, npos);
 #pragma unroll
-        for (int k = 0; k < KP; ++k)
-            kreg[k] = __builtin_bit_cast(
-                uint4, __builtin_amdgcn_raw_buffer_load_b128(krs, t * A.pstride + 16 * min(sj + k * lpp, nv - 1), 0, 0));
+        for (int k = 0; k < KP; ++k) kreg[k] = make_uint4(0, 0, 0, 0);
+        if (wave_u * (64 / lpp) < npos) {
+#pragma unroll
+            for (int k = 0; k < KP; ++k)
+                if (k < nk)
+                    kreg[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                            krs, t * A.pstride + 16 * min(sj + k * lpp, nv - 1), 0, 0));
+        }
     }
     // the K loads first: the scores wait for them, not for the V loads after
     asm volatile("" ::: "memory");
@@ -456,10 +479,20 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
 #pragma unroll
         for (int u = 0; u < kChunk; ++u) vch[u] = 0;
     }
+    // the element values are first used here: without this the compiler
+    // moves their conversions up beside the loads, into the element waves'
+    // branch, which then waits for those loads before any later load issues
+    keep(kqr); keep(kqjr); keep(vqr); keep(qhr); keep(qhjr);
+    keep(knr); keep(knjr); keep(qnr); keep(qnjr);
+    const int kqi = s16(kqr), kqj = s16(kqjr), vqi = s16(vqr), qhi = s16(qhr), qhj = s16(qhjr);
+    const int kni = s16(knr), knj = s16(knjr), qni = s16(qnr), qnj = s16(qnjr);
+    int ke[4], qe[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-        keep(ke[c]);
-        keep(qe[c]);
+        keep(ker[c]);
+        keep(qer[c]);
+        ke[c] = s16(ker[c]);
+        qe[c] = s16(qer[c]);
     }
 
     // sums of squares of the K head and the query head (exact integers in
@@ -475,6 +508,8 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     }
     ssk = wave_sum_exact(ssk);
     ssq = wave_sum_exact(ssq);
+    keep(rc);  // (as the element values: converted here, not in the branch)
+    keep(rs);
     const float co = (float)rc / 4096.0f, sn = (float)rs / 4096.0f;
 
     // --- KV pack of position pos (att_kv_rope)
