@@ -456,9 +456,12 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     {
         // only the lanes of a scored position read its K row, and a wave
         // whose first position lies past the context issues no K load
+        // (kreg is left unset where nothing is loaded: a wave past the
+        // context scores no position, and a slot from nk on meets zero query
+        // words and a zero ones word in every lane, so its value adds nothing;
+        // set to zero, the value would be copied where the branches join,
+        // and the copy would wait for the load)
         const int t = min(tid / lpp, npos);
-#pragma unroll
-        for (int k = 0; k < KP; ++k) kreg[k] = make_uint4(0, 0, 0, 0);
         if (wave_u * (64 / lpp) < npos) {
 #pragma unroll
             for (int k = 0; k < KP; ++k)
@@ -582,21 +585,12 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
         qb[k] = in ? qb[k] : make_int4(0, 0, 0, 0);
         ones[k] = in ? 0x01010101 : 0;
     }
-    for (int it = 0;; ++it) {
-        const int t = tid / lpp + it * P;
-        if (t >= npos) break;
+    // One pass: the dot products of position t with its K row w (the own
+    // position's K from the LDS copy: its cache row is being written; one
+    // branch, taken by the lanes of one position), joined over the lpp lanes,
+    // the score stored on its grid.
+    auto score = [&](int t, uint4 (&w)[KP]) {
         int sh = 0, sl = 0, sk = 0;
-        uint4 w[KP];
-        if (it == 0) {
-#pragma unroll
-            for (int k = 0; k < KP; ++k) w[k] = kreg[k];
-        } else {
-            const uint4* src = reinterpret_cast<const uint4*>(khead + (size_t)t * A.pstride);
-#pragma unroll
-            for (int k = 0; k < KP; ++k) w[k] = src[min(sj + k * lpp, nv - 1)];
-        }
-        // the own position's K is the LDS copy (its cache row is being
-        // written): one branch, taken by the lanes of one position
         if (own_row && t == pos) {
             const uint4* own4 = reinterpret_cast<const uint4*>(kpk);
 #pragma unroll
@@ -614,6 +608,37 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
             sc[t] = (int16_t)f;
             m = max(m, (int)f);
         }
+    };
+    // The K rows of the next pass (P positions on) are in flight while this
+    // pass's dot products run; a wave whose next positions all lie past the
+    // context issues none (wave-uniform), and a row at or past npos reads
+    // zero.  The first pass (rows loaded at the start) is straight-line code
+    // ahead of the loop: inside it, the wait for those rows would be a wait
+    // for every load in flight, the first V round's included.
+    uint4 knx[KP];
+    const int wt0 = wave_u * (64 / lpp);  // the wave's first position of pass 0
+    auto prefetch = [&](int it, int t) {
+        if (wt0 + (it + 1) * P < npos) {
+            const int tn = min(t + P, npos);
+#pragma unroll
+            for (int k = 0; k < KP; ++k)
+                knx[k] = __builtin_bit_cast(
+                    uint4, __builtin_amdgcn_raw_buffer_load_b128(krs, tn * A.pstride + 16 * min(sj + k * lpp, nv - 1), 0, 0));
+        }
+    };
+    {
+        const int t = tid / lpp;  // below npos (the branch above)
+        prefetch(0, t);
+        score(t, kreg);
+    }
+    for (int it = 1;; ++it) {
+        const int t = tid / lpp + it * P;
+        if (t >= npos) break;
+        uint4 w[KP];
+#pragma unroll
+        for (int k = 0; k < KP; ++k) w[k] = knx[k];
+        prefetch(it, t);
+        score(t, w);
     }
     }
     m = wave_max(m);
