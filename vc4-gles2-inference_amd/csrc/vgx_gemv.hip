@@ -170,6 +170,13 @@ __device__ __forceinline__ void planes8eo(const uint32_t d[4], uint32_t& xle, ui
 }
 
 
+// Sixteen q16 values of x already in registers (two 16-byte loads), as
+// load_x16 returns them.
+__device__ __forceinline__ void x_regs(const u32x4_t a, const u32x4_t b, uint32_t d[8]) {
+    d[0] = a.x; d[1] = a.y; d[2] = a.z; d[3] = a.w;
+    d[4] = b.x; d[5] = b.y; d[6] = b.z; d[7] = b.w;
+}
+
 // Load 16 consecutive activations as q16 dwords: from int16, from f32 with
 // the host quantisation, or through RMSNorm from the workgroup's LDS copies of
 // x (xr) and the q16 norm weight (wr), inv = the row's inverse RMS.  Columns
@@ -538,8 +545,6 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
             }
         }
     };
-    // the first tile's loads go out before staging x so the latencies overlap
-    begin_tile(blockIdx.x);
 
     // --- stage x planes (and the row-independent sums) in LDS
     // the byte split's bias sums, per column half (the split epilogue adds the
@@ -577,6 +582,27 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
     // of x and of the norm weight in registers from the load to the planes
     const int npieces = K / 8;
     u32x4_t rxa[kRmsPieces / kThreads], rwa[kRmsPieces / kThreads];
+    // x (and the norm weight) go out first, the first tile's weight chunks
+    // right after: loads complete in the order they are issued, so the wait
+    // for x is not a wait for the weights (whose latency still overlaps the
+    // staging).  Without the fused norm a thread's first chunk of x is loaded
+    // here when it is a whole chunk (q8, q4: always; t3: all but a short last
+    // chunk), and the staging below takes it from these registers.
+    const int xcw = KIND == VGX_Q8 ? 16 : 32;  // x columns a chunk
+    const int xc0 = min((int)threadIdx.x, nch - 1);
+    const bool xpre = XM == X_I16 && (int)threadIdx.x < nch && (xc0 + 1) * xcw <= K;
+    u32x4_t xp[4];
+    if (XM == X_I16 && K >= xcw) {
+        // (a clamped whole chunk: every thread loads, a thread past the
+        // chunks or at a short last chunk discards it)
+        const u32x4_t* p = reinterpret_cast<const u32x4_t*>(L.x + (size_t)min(xc0 * xcw, K - xcw));
+        xp[0] = gld(p);
+        xp[1] = gld(p + 1);
+        if (KIND != VGX_Q8) {
+            xp[2] = gld(p + 2);
+            xp[3] = gld(p + 3);
+        }
+    }
     if (XM == X_RMS && rms_fast) {
 #pragma unroll
         for (int it = 0; it < kRmsPieces / kThreads; ++it) {
@@ -585,6 +611,9 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
             rxa[it] = gld(reinterpret_cast<const u32x4_t*>(L.x + 8 * i));
             rwa[it] = gld(reinterpret_cast<const u32x4_t*>(L.rw + 8 * i));
         }
+    }
+    begin_tile(blockIdx.x);
+    if (XM == X_RMS && rms_fast) {
 #pragma unroll
         for (int it = 0; it < kRmsPieces / kThreads; ++it) {
             const int i = (int)threadIdx.x + it * kThreads;
@@ -703,7 +732,8 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
         for (int c = threadIdx.x; c < nch; c += kThreads) {
             const int hh = (EPI == EPI_SPLIT && c >= L.split_chunk) ? 1 : 0;
             uint32_t d[8], xh[4], xl[4];
-            load_x16<XM>(L, c * 16, K, rinv, d, xr, wr);
+            if (XM == X_I16 && xpre && c == (int)threadIdx.x) x_regs(xp[0], xp[1], d);
+            else load_x16<XM>(L, c * 16, K, rinv, d, xr, wr);
             planes16(d, xh, xl);
             lds[2 * c] = make_uint4(xh[0], xh[1], xh[2], xh[3]);
             lds[2 * c + 1] = make_uint4(xl[0], xl[1], xl[2], xl[3]);
@@ -713,9 +743,12 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
         for (int c = threadIdx.x; c < nch; c += kThreads) {
             const int hh = (EPI == EPI_SPLIT && c >= L.split_chunk) ? 1 : 0;
             uint32_t d[8], xh[4], xl[4], xh2[4], xl2[4];
-            load_x16<XM>(L, c * 32, K, rinv, d, xr, wr);
+            const bool fx = XM == X_I16 && xpre && c == (int)threadIdx.x;
+            if (fx) x_regs(xp[0], xp[1], d);
+            else load_x16<XM>(L, c * 32, K, rinv, d, xr, wr);
             planes16(d, xh, xl);
-            load_x16<XM>(L, c * 32 + 16, K, rinv, d, xr, wr);
+            if (fx) x_regs(xp[2], xp[3], d);
+            else load_x16<XM>(L, c * 32 + 16, K, rinv, d, xr, wr);
             planes16(d, xh2, xl2);
             lds[4 * c + 0] = make_uint4(xh[0], xh[1], xh[2], xh[3]);
             lds[4 * c + 1] = make_uint4(xh2[0], xh2[1], xh2[2], xh2[3]);
@@ -729,8 +762,13 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
     } else {  // Q4
         for (int c = threadIdx.x; c < nch; c += kThreads) {
             uint32_t d[8], d2[8];
-            load_x16<XM>(L, c * 32, K, rinv, d, xr, wr);
-            load_x16<XM>(L, c * 32 + 16, K, rinv, d2, xr, wr);
+            if (XM == X_I16 && xpre && c == (int)threadIdx.x) {
+                x_regs(xp[0], xp[1], d);
+                x_regs(xp[2], xp[3], d2);
+            } else {
+                load_x16<XM>(L, c * 32, K, rinv, d, xr, wr);
+                load_x16<XM>(L, c * 32 + 16, K, rinv, d2, xr, wr);
+            }
             uint32_t he[4], le[4], ho[4], lo[4];
             const uint32_t q0[4] = {d[0], d[1], d[2], d[3]}, q1[4] = {d[4], d[5], d[6], d[7]};
             const uint32_t q2[4] = {d2[0], d2[1], d2[2], d2[3]}, q3[4] = {d2[4], d2[5], d2[6], d2[7]};
