@@ -993,11 +993,45 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
     };
     if (PF) {
         for (int j0 = 0; j0 < niter; j0 += NPF) {
+            if (KIND == VGX_Q8) {
+                // every step's x planes are read before the first product (one
+                // LDS round trip for the group, not one per step: under a
+                // per-lane test each step was a branch whose reads were waited
+                // for before the next step's went out); a chunk past the row
+                // reads a clamped chunk and adds nothing
+                uint4 xh[NPF], xl[NPF];
 #pragma unroll
-            for (int s = 0; s < NPF; ++s) {
-                const int c = cl + (j0 + s) * LPR;
-                if (c < nch) step(0, c, pb[s], pb3[s]);
-                if (j0 + s + NPF < niter) pf_load(s, c + NPF * LPR);
+                for (int s = 0; s < NPF; ++s) {
+                    const int cc = min(cl + (j0 + s) * LPR, nch - 1);
+                    xh[s] = lds[2 * cc];
+                    xl[s] = lds[2 * cc + 1];
+                }
+#pragma unroll
+                for (int s = 0; s < NPF; ++s) {
+                    const int c = cl + (j0 + s) * LPR;
+                    const bool ok = c < nch;
+                    const int o = (EPI == EPI_SPLIT && c >= L.split_chunk) ? 2 : 0;
+                    int s1 = 0;
+                    uint32_t s2 = 0;
+                    q8_chunk(pb[s], xh[s], xl[s], s1, s2);
+                    acc[0][o] += ok ? s1 : 0;
+                    acc[0][o + 1] += ok ? (int)s2 : 0;
+                    if (EPI == EPI_GATE) {
+                        int t1 = 0;
+                        uint32_t t2 = 0;
+                        q8_chunk(pb3[s], xh[s], xl[s], t1, t2);
+                        acc[0][2] += ok ? t1 : 0;
+                        acc[0][3] += ok ? (int)t2 : 0;
+                    }
+                    if (j0 + s + NPF < niter) pf_load(s, c + NPF * LPR);
+                }
+            } else {
+#pragma unroll
+                for (int s = 0; s < NPF; ++s) {
+                    const int c = cl + (j0 + s) * LPR;
+                    if (c < nch) step(0, c, pb[s], pb3[s]);
+                    if (j0 + s + NPF < niter) pf_load(s, c + NPF * LPR);
+                }
             }
         }
     }
