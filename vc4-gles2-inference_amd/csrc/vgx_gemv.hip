@@ -250,8 +250,43 @@ __device__ __forceinline__ uint32_t t3_lut_entry(uint32_t b) {
 // Multi-row butterfly over the LPR lanes of a row segment.  v[r][k], r < R,
 // k < NV.  After the call the lane whose segment index has zero low bits
 // (cl % (LPR/R) == 0) holds the complete sums of row `row` in v[0][*].
+//
+// One row a lane (R == 1) with exact int32 sums: DPP moves instead of
+// shuffles through the LDS crossbar (exchanges inside rows of 16 lanes --
+// quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror -- then the row
+// broadcasts of lane 15 into rows 1 and 3 and of lane 31 into rows 2 and 3).
+// Every lane of a segment's last row of 16 then holds the segment's sums
+// (seg_leader).  Integer sums: the pairing does not change the total.
+template <int CTRL, int RM>
+__device__ __forceinline__ int dpp_row(int x) {
+    return __builtin_amdgcn_update_dpp(0, x, CTRL, RM, 0xF, false);
+}
+template <int LPR, int R, typename T>
+__device__ constexpr bool seg_dpp() {
+    return R == 1 && std::is_same<T, int>::value && LPR >= 2 && LPR <= 64;
+}
+// The lane of a segment that holds its complete sums after seg_reduce.
+template <int LPR, int R, typename T>
+__device__ __forceinline__ bool seg_leader(int cl) {
+    if (seg_dpp<LPR, R, T>()) return cl == (LPR <= 16 ? 0 : LPR - 16);
+    return (cl % (LPR / R > 0 ? LPR / R : 1)) == 0;
+}
 template <int LPR, int R, int NV, typename T>
 __device__ __forceinline__ int seg_reduce(T (&v)[R][NV], int cl) {
+    if constexpr (seg_dpp<LPR, R, T>()) {
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            int x = (int)v[0][k];
+            if (LPR >= 2) x += dpp_row<0xB1, 0xF>(x);
+            if (LPR >= 4) x += dpp_row<0x4E, 0xF>(x);
+            if (LPR >= 8) x += dpp_row<0x141, 0xF>(x);
+            if (LPR >= 16) x += dpp_row<0x140, 0xF>(x);
+            if (LPR >= 32) x += dpp_row<0x142, 0xA>(x);
+            if (LPR >= 64) x += dpp_row<0x143, 0xC>(x);
+            v[0][k] = (T)x;
+        }
+        return 0;
+    }
     int base = 0;
     int m = R;
     int o = LPR / 2;
@@ -881,7 +916,7 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
             }
         }
         const int row_it = seg_reduce<LPR, RI, NV, long long>(acc, cl);
-        if ((cl % (LPR / RI > 0 ? LPR / RI : 1)) == 0) {
+        if (seg_leader<LPR, RI, long long>(cl)) {
             const int u = unit0 + row_it * RPI + rs;
             if (u < units) {
                 const float v = (float)acc[0][0] * ps;
@@ -1068,7 +1103,7 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
 
     const int row_it = seg_reduce<LPR, RI, NI, int>(acc, cl);
     const int u = unit0 + row_it * RPI + rs;
-    if ((cl % (LPR / RI > 0 ? LPR / RI : 1)) == 0 && u < units) {
+    if (seg_leader<LPR, RI, int>(cl) && u < units) {
     // bias of the byte split: q8 -128*sum(xl), t3 -sum(x)
     const long long cmul = KIND == VGX_Q8 ? 128LL : 1LL;
 #pragma unroll
