@@ -248,10 +248,11 @@ __device__ __forceinline__ uint32_t t3_lut_entry(uint32_t b) {
 
 // ---------------------------------------------------------------------------
 // Multi-row butterfly over the LPR lanes of a row segment.  v[r][k], r < R,
-// k < NV.  After the call the lane whose segment index has zero low bits
-// (cl % (LPR/R) == 0) holds the complete sums of row `row` in v[0][*].
+// k < NV.  After the call the lane seg_leader picks holds the complete sums
+// of row `row` (the returned row slot) in v[0][*]: with several rows a lane,
+// the lane whose segment index has zero low bits (cl % (LPR/R) == 0).
 //
-// One row a lane (R == 1) with exact int32 sums: DPP moves instead of
+// One row a lane (R == 1), exact int32 or int64 sums: DPP moves instead of
 // shuffles through the LDS crossbar (exchanges inside rows of 16 lanes --
 // quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror -- then the row
 // broadcasts of lane 15 into rows 1 and 3 and of lane 31 into rows 2 and 3).
@@ -261,9 +262,16 @@ template <int CTRL, int RM>
 __device__ __forceinline__ int dpp_row(int x) {
     return __builtin_amdgcn_update_dpp(0, x, CTRL, RM, 0xF, false);
 }
+template <int CTRL, int RM>
+__device__ __forceinline__ long long dpp_row(long long x) {
+    const unsigned long long b = (unsigned long long)x;
+    const unsigned lo = (unsigned)dpp_row<CTRL, RM>((int)(unsigned)b);
+    const unsigned hi = (unsigned)dpp_row<CTRL, RM>((int)(unsigned)(b >> 32));
+    return (long long)(((unsigned long long)hi << 32) | lo);
+}
 template <int LPR, int R, typename T>
 __device__ constexpr bool seg_dpp() {
-    return R == 1 && std::is_same<T, int>::value && LPR >= 2 && LPR <= 64;
+    return R == 1 && (std::is_same<T, int>::value || std::is_same<T, long long>::value) && LPR >= 2 && LPR <= 64;
 }
 // The lane of a segment that holds its complete sums after seg_reduce.
 template <int LPR, int R, typename T>
@@ -276,14 +284,14 @@ __device__ __forceinline__ int seg_reduce(T (&v)[R][NV], int cl) {
     if constexpr (seg_dpp<LPR, R, T>()) {
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
-            int x = (int)v[0][k];
+            T x = v[0][k];
             if (LPR >= 2) x += dpp_row<0xB1, 0xF>(x);
             if (LPR >= 4) x += dpp_row<0x4E, 0xF>(x);
             if (LPR >= 8) x += dpp_row<0x141, 0xF>(x);
             if (LPR >= 16) x += dpp_row<0x140, 0xF>(x);
             if (LPR >= 32) x += dpp_row<0x142, 0xA>(x);
             if (LPR >= 64) x += dpp_row<0x143, 0xC>(x);
-            v[0][k] = (T)x;
+            v[0][k] = x;
         }
         return 0;
     }
