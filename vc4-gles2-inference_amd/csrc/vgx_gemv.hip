@@ -363,15 +363,30 @@ __device__ __forceinline__ unsigned long long argmax_key(int q, int row) {
     return ((unsigned long long)(unsigned)(q + 32768) << 32) | (unsigned long long)(0xFFFFFFFFu - (unsigned)row);
 }
 
+// The largest key of the wave (unsigned; zero is the identity) in lane 63:
+// DPP exchanges inside rows of 16 lanes, then the lane-15 and lane-31 row
+// broadcasts (rows a mask leaves out read zero), as seg_reduce's sums.
+__device__ __forceinline__ unsigned long long wave_max_key63(unsigned long long key) {
+    auto step = [&](auto ctrl, auto rm) {
+        const unsigned long long o = (unsigned long long)dpp_row<decltype(ctrl)::value, decltype(rm)::value>((long long)key);
+        key = o > key ? o : key;
+    };
+    step(std::integral_constant<int, 0xB1>{}, std::integral_constant<int, 0xF>{});
+    step(std::integral_constant<int, 0x4E>{}, std::integral_constant<int, 0xF>{});
+    step(std::integral_constant<int, 0x141>{}, std::integral_constant<int, 0xF>{});
+    step(std::integral_constant<int, 0x140>{}, std::integral_constant<int, 0xF>{});
+    step(std::integral_constant<int, 0x142>{}, std::integral_constant<int, 0xA>{});
+    step(std::integral_constant<int, 0x143>{}, std::integral_constant<int, 0xC>{});
+    return key;
+}
+
 __device__ __forceinline__ void argmax_tail(const GemvLaunch& L, unsigned long long key) {
     __shared__ unsigned long long s_k[kWaves];
-    for (int o = 32; o >= 1; o >>= 1) {
-        const unsigned long long other = shfl_xor(key, o);
-        key = other > key ? other : key;
-    }
-    if ((threadIdx.x & 63) == 0) s_k[threadIdx.x >> 6] = key;
+    key = wave_max_key63(key);
+    if ((threadIdx.x & 63) == 63) s_k[threadIdx.x >> 6] = key;
     __syncthreads();
     if (threadIdx.x == 0) {
+        key = s_k[0];  // (lane 0 holds only its row's maximum)
         for (int k = 1; k < kWaves; ++k) key = s_k[k] > key ? s_k[k] : key;
         gst(L.argmax_key + blockIdx.x, key);
     }
@@ -394,13 +409,11 @@ __global__ void __launch_bounds__(256) argmax_keys_kernel(const unsigned long lo
     const int p = T.pos && threadIdx.x == 0 ? *T.pos : 0;
     unsigned long long key = 0ull;
     for (int i = threadIdx.x; i < n; i += 256) key = keys[i] > key ? keys[i] : key;
-    for (int o = 32; o >= 1; o >>= 1) {
-        const unsigned long long other = __shfl_xor(key, o, 64);
-        key = other > key ? other : key;
-    }
-    if ((threadIdx.x & 63) == 0) s_k[threadIdx.x >> 6] = key;
+    key = wave_max_key63(key);
+    if ((threadIdx.x & 63) == 63) s_k[threadIdx.x >> 6] = key;
     __syncthreads();
     if (threadIdx.x == 0) {
+        key = s_k[0];  // (lane 0 holds only its row's maximum)
         for (int k = 1; k < 4; ++k) key = s_k[k] > key ? s_k[k] : key;
         const int tok = (int)(0xFFFFFFFFu - (unsigned)(key & 0xFFFFFFFFull));
         *out = tok;
@@ -743,8 +756,8 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
                 int X = 256 * (sdot4(he, 0x01010101u, 0) + sdot4(ho, 0x01010101u, 0)) +
                         (int)(udot4(le, 0x01010101u, 0u) + udot4(lo, 0x01010101u, 0u));
                 X = ok ? X : 0;
-                X += shfl_xor(X, 1);
-                X += shfl_xor(X, 2);
+                X += dpp_row<0xB1, 0xF>(X);  // the quad's four pieces (lanes 4c'..4c'+3)
+                X += dpp_row<0x4E, 0xF>(X);
                 if (ok) {
                     reinterpret_cast<uint32_t*>(&lds[4 * c + 0])[q] = he;
                     reinterpret_cast<uint32_t*>(&lds[4 * c + 1])[q] = le;
