@@ -717,7 +717,17 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvLaunch L) {
             long long t = 0;
             if (lane < 32) {
                 long long P = 0;
-                for (int k = 0; k < pps; ++k) P += s_rpiece[lane * pps + k];
+                if (pps <= 4) {
+                    // every piece read before the first add (exact integers:
+                    // the order is free), not one read waited for at a time
+                    long long q[4];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) q[k] = s_rpiece[lane * pps + min(k, pps - 1)];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) P += k < pps ? q[k] : 0;
+                } else {
+                    for (int k = 0; k < pps; ++k) P += s_rpiece[lane * pps + k];
+                }
                 t = (P + 8) >> 4;
             }
             // the 32 rounded slices (each below 2^32) added as doubles: every
