@@ -348,10 +348,14 @@ static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // Workgroups of a GEMV launch: one per row tile up to 4 per CU; past that each
 // workgroup loops over tiles (x is staged once per workgroup).  4 per CU was
-// the best of 2..16 on HBM-streamed q8 and q4 launches.
+// the best of 2..16 on HBM-streamed q8 and q4 launches.  A launch of at most
+// kGridOnePass tiles a CU still takes one workgroup per tile: capped, its
+// last tiles were streamed by a few workgroups after all the others had
+// finished (the 73,448-row LM head: 1148 tiles, 124 of them a second pass).
+static constexpr int kGridOnePass = 5;
 static int gemv_grid(const vgx_ctx* ctx, int tiles) {
-    const int cap = 4 * ctx->num_cu;
-    return tiles < cap ? tiles : cap;
+    if (tiles <= kGridOnePass * ctx->num_cu) return tiles;
+    return 4 * ctx->num_cu;
 }
 
 static int launch_single(vgx_ctx* ctx, const vgx_mat* W, const int16_t* x, const float* xf,
@@ -480,7 +484,7 @@ int vgx_group_create(vgx_ctx* ctx, int n, const vgx_mat* const* mats, vgx_group*
     hipError_t e = hipMalloc(&g->d_dev, sizeof(MatDev) * (size_t)n);
     if (e == hipSuccess) e = hipMemcpy(g->d_dev, ds.data(), sizeof(MatDev) * (size_t)n, hipMemcpyHostToDevice);
     // a key slot per workgroup of the largest grid a launch takes (gemv_grid)
-    g->nkeys = 4 * (ctx->num_cu > 0 ? ctx->num_cu : 256);
+    g->nkeys = kGridOnePass * (ctx->num_cu > 0 ? ctx->num_cu : 256);
     if (e == hipSuccess) e = hipMalloc(&g->keys, sizeof(unsigned long long) * (size_t)g->nkeys);
     if (e != hipSuccess) { vgx_group_free(g); return vgx_hip_fail(e, "vgx_group_create"); }
     *out = g;
