@@ -196,7 +196,7 @@ int vgx_logits_argmax_rms(vgx_ctx* ctx, const vgx_group* g, const int16_t* x, co
  * of the group's own: no counterpart in the reference; for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
  * loops).  The call allocates nothing.  A launch needing more workgroups than
- * there are slots is refused (VGX_ERANGE; the LM-head launch takes at most 4
+ * there are slots is refused (VGX_ERANGE; the LM-head launch takes at most 5
  * per CU).  Every call on one device shares the array: calls that overlap on
  * one GPU (other streams, other threads) race; every slot a call reads is
  * written by that call first. */
