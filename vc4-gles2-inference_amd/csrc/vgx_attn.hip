@@ -50,7 +50,8 @@ struct AttnDev {
     int dim, heads, kv_heads, hd, seq, kv_bits, rope_half, qk_norm, group;
     int row_bytes;  // one position of every head, K and V: the texel row MMKV1 persists
     int pstride;    // bytes of one position in a head's plane (head_dim values)
-    int lpp;     // lanes per scored position (a power of two)
+    int lpp;     // lanes per scored position (a power of two): query-block kernel
+    int lpp1;    // the same for the per-head kernel
     // the weighted-V lane plan with one element per lane (vG1 waves per chunk,
     // vC1 chunks per round) and with two (vG2, vC2; taken above head_dim 64
     // when the context needs more than one round of the first)
@@ -321,7 +322,7 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
     asm volatile("" ::"s"(kv), "s"(rtab), "s"(qn), "s"(kn), "s"(qkv), "s"(out), "s"(pos0), "s"(do_write),
                  "s"(do_attend), "s"(seq_stride), "s"(pos_step), "s"(pos_ptr), "s"(A.dim), "s"(A.kv_heads),
                  "s"(A.hd), "s"(A.seq), "s"(A.rope_half), "s"(A.qk_norm), "s"(A.group), "s"(A.pstride),
-                 "s"(A.lpp), "s"(A.vG1), "s"(A.vC1), "s"(A.vG2), "s"(A.vC2), "s"(A.nchmax), "s"(A.o_wmax),
+                 "s"(A.lpp1), "s"(A.vG1), "s"(A.vC1), "s"(A.vG2), "s"(A.vC2), "s"(A.nchmax), "s"(A.o_wmax),
                  "s"(A.o_vpk), "s"(A.o_kpk), "s"(A.o_qhw), "s"(A.o_qlw), "s"(A.o_sc), "s"(A.o_ep), "s"(A.o_csum),
                  "s"(A.o_vpart), "s"(A.o_acc));
     constexpr int E = KVB == 16 ? 2 : 4;  // values per 32-bit word
@@ -427,7 +428,7 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
         rs = rt[2 * ti + 1];
     }
     const int nv = hd * KVB / 128;  // 16-byte vectors per K row slice
-    const int lpp = A.lpp, sj = tid & (lpp - 1), P = kThreads / lpp;
+    const int lpp = A.lpp1, sj = tid & (lpp - 1), P = kThreads / lpp;
     // weighted-V lanes: wave w takes chunk slot w / vG of each round and the
     // elements vE*(64*(w % vG) + lane) .. +vE-1 of the head
     // (slot is wave-uniform; readfirstlane lets the compiler see it)
@@ -1403,6 +1404,15 @@ size_t attn_layout(AttnDev& A) {
     const int E = A.kv_bits == 16 ? 2 : 4;
     A.lpp = 1;
     while (A.lpp * kp < nv) A.lpp *= 2;
+    // The per-head kernel: one lane a position loads its whole K row, a load
+    // instruction per 16 bytes with the wave's 64 lanes a row stride apart;
+    // two lanes a position issue half the loads each (the slots past the row
+    // load nothing) and pair them on 32 contiguous bytes.  Measured on the
+    // 0.5B t3 decode (head_dim 64, q16 cache): batch 1 1586 -> 1593 tokens/s.
+    // The query-block kernel keeps one lane (two made the batch-32 step 1.173
+    // -> 1.192 ms), and doubling the lanes of every plan slowed C1 (5860 ->
+    // 5815) and the C3 attention.
+    A.lpp1 = (A.lpp == 1 && nv > 4) ? 2 : A.lpp;
     A.nchmax = (A.seq + kChunk - 1) / kChunk;
     A.vG1 = (hd + 63) / 64;
     A.vC1 = (kThreads / 64) / A.vG1;
