@@ -306,8 +306,12 @@ __device__ __forceinline__ double chunk_w(double lo, double hi) {
 
 // PAIR: the pair plan below is compiled in (the host sets it for heads of at
 // most 32 fields of 32 bits; without it the kernel of a wider head keeps the
-// registers and schedule of the one- and two-element plans alone).
-template <int KVB, bool PAIR>
+// registers and schedule of the one- and two-element plans alone).  KS: the
+// K vector slots a scoring lane holds, at least the lane plan's slots per row
+// (the host takes 4 when they fit: each slot is a 16-byte K load, two
+// query-word reads from LDS and a dot product, whether or not it lies past
+// the row).
+template <int KVB, bool PAIR, int KS>
 __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t* kv, const int32_t* rtab,
                                                         const int16_t* qn, const int16_t* kn,
                                                         const int16_t* qkv, int16_t* out, int pos0,
@@ -326,7 +330,7 @@ __global__ void __launch_bounds__(kThreads) attn_kernel(const AttnDev A, uint8_t
                  "s"(A.o_vpk), "s"(A.o_kpk), "s"(A.o_qhw), "s"(A.o_qlw), "s"(A.o_sc), "s"(A.o_ep), "s"(A.o_csum),
                  "s"(A.o_vpart), "s"(A.o_acc));
     constexpr int E = KVB == 16 ? 2 : 4;  // values per 32-bit word
-    constexpr int KP = kKPre<KVB>;
+    constexpr int KP = KS;
     const int hd = A.hd, G = A.group, kv_dim = A.kv_heads * hd;
     // An attending launch has one workgroup per query head; a write-only
     // launch one per KV head.  The first query head of a KV head's group packs
@@ -1393,8 +1397,12 @@ using AttnKernelFn = void (*)(const AttnDev, uint8_t*, const int32_t*, const int
                               const int16_t*, int16_t*, int, int, int, size_t, int, const int*);
 AttnKernelFn attn_kernel_for(const AttnDev& A) {
     const bool pair = A.hd * A.kv_bits <= 32 * 32 && A.nchmax > A.vC1;
-    if (A.kv_bits == 16) return pair ? attn_kernel<16, true> : attn_kernel<16, false>;
-    return pair ? attn_kernel<8, true> : attn_kernel<8, false>;
+    const int nv = A.hd * A.kv_bits / 128;
+    if (A.kv_bits == 16) {
+        if ((nv + A.lpp1 - 1) / A.lpp1 <= 4) return pair ? attn_kernel<16, true, 4> : attn_kernel<16, false, 4>;
+        return pair ? attn_kernel<16, true, kKPre<16>> : attn_kernel<16, false, kKPre<16>>;
+    }
+    return pair ? attn_kernel<8, true, kKPre<8>> : attn_kernel<8, false, kKPre<8>>;
 }
 
 size_t attn_layout(AttnDev& A) {
