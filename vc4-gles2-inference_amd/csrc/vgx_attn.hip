@@ -308,7 +308,7 @@ __device__ __forceinline__ double chunk_w(double lo, double hi) {
 // most 32 fields of 32 bits; without it the kernel of a wider head keeps the
 // registers and schedule of the one- and two-element plans alone).  KS: the
 // K vector slots a scoring lane holds, at least the lane plan's slots per row
-// (the host takes 4 when they fit: each slot is a 16-byte K load, two
+// (the host takes 3 or 4 when they fit: each slot is a 16-byte K load, two
 // query-word reads from LDS and a dot product, whether or not it lies past
 // the row).
 template <int KVB, bool PAIR, int KS>
@@ -1399,6 +1399,7 @@ AttnKernelFn attn_kernel_for(const AttnDev& A) {
     const bool pair = A.hd * A.kv_bits <= 32 * 32 && A.nchmax > A.vC1;
     const int nv = A.hd * A.kv_bits / 128;
     if (A.kv_bits == 16) {
+        if ((nv + A.lpp1 - 1) / A.lpp1 <= 3) return pair ? attn_kernel<16, true, 3> : attn_kernel<16, false, 3>;
         if ((nv + A.lpp1 - 1) / A.lpp1 <= 4) return pair ? attn_kernel<16, true, 4> : attn_kernel<16, false, 4>;
         return pair ? attn_kernel<16, true, kKPre<16>> : attn_kernel<16, false, kKPre<16>>;
     }
@@ -1412,15 +1413,22 @@ size_t attn_layout(AttnDev& A) {
     const int E = A.kv_bits == 16 ? 2 : 4;
     A.lpp = 1;
     while (A.lpp * kp < nv) A.lpp *= 2;
-    // The per-head kernel: one lane a position loads its whole K row, a load
-    // instruction per 16 bytes with the wave's 64 lanes a row stride apart;
-    // two lanes a position issue half the loads each (the slots past the row
-    // load nothing) and pair them on 32 contiguous bytes.  Measured on the
-    // 0.5B t3 decode (head_dim 64, q16 cache): batch 1 1586 -> 1593 tokens/s.
-    // The query-block kernel keeps one lane (two made the batch-32 step 1.173
-    // -> 1.192 ms), and doubling the lanes of every plan slowed C1 (5860 ->
-    // 5815) and the C3 attention.
-    A.lpp1 = (A.lpp == 1 && nv > 4) ? 2 : A.lpp;
+    // The per-head kernel at a q16 cache: the fewest lanes a position (a power
+    // of two) that leave at most 4 K vectors a lane, run by the 3- or 4-slot
+    // kernel instance.  With more slots a lane, each slot is a 16-byte K load (one
+    // lane a position: the wave's 64 lanes a row stride apart), two
+    // query-word reads from LDS and a dot product, and the 8-slot instance
+    // does all eight whether or not they lie past the row.  Measured against
+    // the plan above with the 8-slot kernel: head_dim 64 (two lanes instead
+    // of one) C5 batch 1 1579 -> 1608 tokens/s, C4 3126 -> 3151; head_dim 96
+    // (four lanes instead of two, 3 slots) C1 5882 -> 5972.  The query-block kernel
+    // keeps the plan above (two lanes made the C5 batch-32 step 1.173 -> 1.192
+    // ms).
+    A.lpp1 = A.lpp;
+    if (A.kv_bits == 16) {
+        A.lpp1 = 1;
+        while ((nv + A.lpp1 - 1) / A.lpp1 > 4) A.lpp1 *= 2;
+    }
     A.nchmax = (A.seq + kChunk - 1) / kChunk;
     A.vG1 = (hd + 63) / 64;
     A.vC1 = (kThreads / 64) / A.vG1;
