@@ -1403,6 +1403,7 @@ AttnKernelFn attn_kernel_for(const AttnDev& A) {
         if ((nv + A.lpp1 - 1) / A.lpp1 <= 4) return pair ? attn_kernel<16, true, 4> : attn_kernel<16, false, 4>;
         return pair ? attn_kernel<16, true, kKPre<16>> : attn_kernel<16, false, kKPre<16>>;
     }
+    if ((nv + A.lpp1 - 1) / A.lpp1 <= 3) return pair ? attn_kernel<8, true, 3> : attn_kernel<8, false, 3>;
     return pair ? attn_kernel<8, true, kKPre<8>> : attn_kernel<8, false, kKPre<8>>;
 }
 
