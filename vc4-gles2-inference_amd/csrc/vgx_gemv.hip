@@ -404,11 +404,27 @@ __global__ void __launch_bounds__(256) argmax_keys_kernel(const unsigned long lo
     // argument in a line of its own)
     asm volatile("" ::"s"(keys), "s"(n), "s"(out), "s"(T.pos), "s"(T.hist), "s"(T.hist_len), "s"(T.emb),
                  "s"(T.emb_scale), "s"(T.vocab), "s"(T.dim), "s"(T.x));
-    // the position (read before the keys: only this launch writes it, at its
-    // end) so the bookkeeping below waits for no further round trip
-    const int p = T.pos && threadIdx.x == 0 ? *T.pos : 0;
+    // Every load that waits for nothing goes out in one batch: the position
+    // (read by every lane from its uniform address: read by one lane, the
+    // load was waited for before the keys issued; only this launch writes
+    // it, at its end) and up to kKeysPer keys a thread from clamped addresses
+    // (a repeat of the last key changes no maximum).  Issued one per loop
+    // iteration, each 256 keys were a round trip of their own.
+    constexpr int kKeysPer = 8;
+    // (from a valid address either way: a load under the test was waited
+    // for where the branch joined)
+    int p = *(T.pos ? T.pos : reinterpret_cast<const int*>(keys));
+    const int last = n > 0 ? n - 1 : 0;
+    unsigned long long kv[kKeysPer];
+#pragma unroll
+    for (int j = 0; j < kKeysPer; ++j) kv[j] = keys[min((int)threadIdx.x + 256 * j, last)];
     unsigned long long key = 0ull;
-    for (int i = threadIdx.x; i < n; i += 256) key = keys[i] > key ? keys[i] : key;
+#pragma unroll
+    for (int j = 0; j < kKeysPer; ++j) key = kv[j] > key ? kv[j] : key;
+    // (held here, past the keys it was issued before: left to the compiler
+    // the load moved into the one lane's bookkeeping below)
+    asm volatile("" : "+v"(p));
+    for (int i = threadIdx.x + 256 * kKeysPer; i < n; i += 256) key = keys[i] > key ? keys[i] : key;
     key = wave_max_key63(key);
     if ((threadIdx.x & 63) == 63) s_k[threadIdx.x >> 6] = key;
     __syncthreads();
@@ -428,17 +444,31 @@ __global__ void __launch_bounds__(256) argmax_keys_kernel(const unsigned long lo
     if (!T.pos) return;
     __syncthreads();
     // the next step's input: the token's embedding row, as embed_q8_kernel
-    // forms it (Session::embedding, engine/src/session.cpp:362-365)
+    // forms it (Session::embedding, engine/src/session.cpp:362-365); the
+    // scale and up to kEmbPer bytes a thread load in one batch (clamped
+    // addresses, the surplus never stored)
+    constexpr int kEmbPer = 8;
     int tok = s_tok;
     if (tok < 0) tok = 0;
     if (tok >= T.vocab) tok = T.vocab - 1;
+    const int8_t* er = T.emb + (size_t)tok * T.dim;
+    const int dlast = T.dim > 0 ? T.dim - 1 : 0;
     const float sc = T.emb_scale[tok];
-    for (int i = threadIdx.x; i < T.dim; i += 256) {
-        const float v = (float)T.emb[(size_t)tok * T.dim + i] * sc;
+    int8_t ev[kEmbPer];
+#pragma unroll
+    for (int j = 0; j < kEmbPer; ++j) ev[j] = er[min((int)threadIdx.x + 256 * j, dlast)];
+    auto put = [&](int i, int8_t e) {
+        const float v = (float)e * sc;
         float r = __builtin_rintf(v * 256.0f);
         r = fminf(fmaxf(r, -32768.0f), 32767.0f);
         T.x[i] = (int16_t)r;
+    };
+#pragma unroll
+    for (int j = 0; j < kEmbPer; ++j) {
+        const int i = threadIdx.x + 256 * j;
+        if (i < T.dim) put(i, ev[j]);
     }
+    for (int i = threadIdx.x + 256 * kEmbPer; i < T.dim; i += 256) put(i, er[i]);
 }
 
 // Dynamic LDS of a launch: the x planes (q8: 32 B per 16 columns; t3 and
