@@ -49,11 +49,12 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const int16_t* x, const in
         for (int k = 0; sub + 8 * k < per; ++k)
             if (in(k)) P += (long long)x[i0 + 8 * k] * x[i0 + 8 * k];
     }
-    for (int o = 4; o >= 1; o >>= 1) P += __shfl_xor(P, o, 64);
+    // (the slice's 8 lanes and then the 32 slices joined by DPP: exact
+    // integers, so the order does not matter)
+    P = sum8_i64(P);
     if (sub == 0) part[p] = (P + 8) >> 4;
     __syncthreads();
-    long long tot = lane < 32 ? part[lane] : 0;
-    for (int o = 32; o >= 1; o >>= 1) tot += __shfl_xor(tot, o, 64);
+    const long long tot = sum32_i64(part[lane & 31]);
     const float ss = (float)tot / 4096.0f;
     const float inv = (float)(1.0 / sqrt((double)(ss / (float)dim + eps)));
     auto put = [&](int i, int xi, int wi) {
@@ -113,11 +114,12 @@ __global__ void __launch_bounds__(256) embed_rms_kernel(const int8_t* emb, const
             P += (long long)xr[k] * xr[k];
             x[i0 + 8 * k] = (int16_t)xr[k];
         }
-    for (int o = 4; o >= 1; o >>= 1) P += __shfl_xor(P, o, 64);
+    // (the slice's 8 lanes and then the 32 slices joined by DPP: exact
+    // integers, so the order does not matter)
+    P = sum8_i64(P);
     if (sub == 0) part[p] = (P + 8) >> 4;
     __syncthreads();
-    long long tot = lane < 32 ? part[lane] : 0;
-    for (int o = 32; o >= 1; o >>= 1) tot += __shfl_xor(tot, o, 64);
+    const long long tot = sum32_i64(part[lane & 31]);
     const float ss = (float)tot / 4096.0f;
     const float inv = (float)(1.0 / sqrt((double)(ss / (float)dim + eps)));
 #pragma unroll

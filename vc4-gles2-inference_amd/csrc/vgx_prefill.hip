@@ -613,36 +613,36 @@ __global__ void __launch_bounds__(kNormThreads) gemm_epi_norm_kernel(const GemmL
     extern __shared__ __align__(16) unsigned char s_dyn[];
     int16_t* row = reinterpret_cast<int16_t*>(s_dyn);
     __shared__ long long part[32];
-    __shared__ float s_inv;
     const int tt = blockIdx.x, rows = G.M.rows, tid = threadIdx.x;
+    // the norm weight of this thread's first output, loaded before the
+    // epilogue's loads (issued after the barriers below it was a round trip
+    // of its own at the end)
+    uint16_t nw0 = (uint16_t)nw[min(tid, rows - 1)];
     for (int n = tid; n < rows; n += kNormThreads) {
         const int16_t q = epi_value<EPI>(G, nz, tt, n);
         G.y[(size_t)tt * G.ldy + n] = q;
         row[n] = q;
     }
+    asm volatile("" : "+v"(nw0));
     __syncthreads();
     const int per = (rows + 31) / 32;
-    if (tid < 256) {  // 8 threads a partial slice
+    if (tid < 256) {  // 8 threads a partial slice (whole waves)
         const int p = tid >> 3, sub = tid & 7;
         long long P = 0;
         for (int k = sub; k < per; k += 8) {
             const int i = p * per + k;
             if (i < rows) P += (long long)row[i] * row[i];
         }
-        for (int o = 4; o >= 1; o >>= 1) P += __shfl_xor(P, o, 64);
+        P = sum8_i64(P);  // (DPP; exact integers, any order)
         if (sub == 0) part[p] = (P + 8) >> 4;
     }
     __syncthreads();
-    if (tid == 0) {
-        long long tot = 0;
-        for (int p = 0; p < 32; ++p) tot += part[p];
-        const float ss = (float)tot / 4096.0f;
-        s_inv = (float)(1.0 / sqrt((double)(ss / (float)rows + neps)));
-    }
-    __syncthreads();
-    const float inv = s_inv;
+    // every wave adds the 32 slices itself (exact integers) and forms inv
+    const long long tot = sum32_i64(part[tid & 31]);
+    const float ss = (float)tot / 4096.0f;
+    const float inv = (float)(1.0 / sqrt((double)(ss / (float)rows + neps)));
     for (int i = tid; i < rows; i += kNormThreads)
-        yn[(size_t)tt * rows + i] = (int16_t)rms_elem((uint16_t)row[i], (uint16_t)nw[i], inv);
+        yn[(size_t)tt * rows + i] = (int16_t)rms_elem((uint16_t)row[i], i == tid ? nw0 : (uint16_t)nw[i], inv);
 }
 
 using GemmFn = void (*)(const GemmLaunch);

@@ -21,6 +21,38 @@ __device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel)
     return __builtin_amdgcn_perm(s0, s1, sel);
 }
 
+// A 64-bit integer moved between lanes by one DPP control (both halves).
+template <int CTRL>
+__device__ __forceinline__ long long dpp_i64(long long x) {
+    const unsigned long long b = (unsigned long long)x;
+    const unsigned lo = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)b, CTRL, 0xF, 0xF, false);
+    const unsigned hi = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)(b >> 32), CTRL, 0xF, 0xF, false);
+    return (long long)(((unsigned long long)hi << 32) | lo);
+}
+// The exact sum over each aligned group of 8 lanes, in every lane of the
+// group: lane ^ 1, lane ^ 2 (quad permutes), then the half-row mirror.  Every
+// lane of the wave active.
+__device__ __forceinline__ long long sum8_i64(long long x) {
+    x += dpp_i64<0xB1>(x);
+    x += dpp_i64<0x4E>(x);
+    x += dpp_i64<0x141>(x);
+    return x;
+}
+// The exact sum over lanes 0..31 (the other lanes' values are ignored), in
+// every lane: each row of 16 lanes summed by DPP, rows 0 and 1 read out.
+// Every lane of the wave active.
+__device__ __forceinline__ long long sum32_i64(long long x) {
+    x = sum8_i64(x);
+    x += dpp_i64<0x140>(x);
+    const unsigned long long b = (unsigned long long)x;
+    const unsigned lo = (unsigned)b, hi = (unsigned)(b >> 32);
+    const unsigned long long r0 = ((unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)hi, 0) << 32) |
+                                  (unsigned)__builtin_amdgcn_readlane((int)lo, 0);
+    const unsigned long long r1 = ((unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)hi, 16) << 32) |
+                                  (unsigned)__builtin_amdgcn_readlane((int)lo, 16);
+    return (long long)r0 + (long long)r1;
+}
+
 // clamp(floor(v + 0.5)) -- the shader's q16 store of a value in Q units.
 __device__ __forceinline__ int q16_round(float v) {
     float f = floorf(v + 0.5f);
