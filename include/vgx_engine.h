@@ -56,9 +56,10 @@ int vgx_engine_prefill(vgx_engine* e, const int* tokens, int n, int pos0, int16_
  * min(seq, 512), which is also the default.  Applies to vgx_engine_prefill
  * and to vgx_engine_generate's prompt. */
 int vgx_engine_set_prefill_batch(vgx_engine* e, int n);
-/* Decode steps of vgx_engine_generate[_from] as one HIP graph replayed per
- * token (on: the default) or as individual launches (off); the tokens are
- * the same either way. */
+/* Decode steps of vgx_engine_generate[_from] as replayed HIP graphs (on: the
+ * default; one step a graph, and four steps a graph for runs of four tokens
+ * where a step has at most 100 launches) or as individual launches (off);
+ * the tokens are the same either way. */
 int vgx_engine_set_graphs(vgx_engine* e, int on);
 /* Greedy generation for nseq sequences in lockstep (no counterpart in the
  * reference, which decodes one sequence): prompts is nseq x n_prompt, out
