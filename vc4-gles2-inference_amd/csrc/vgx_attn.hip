@@ -1421,9 +1421,10 @@ size_t attn_layout(AttnDev& A) {
     // query-word reads from LDS and a dot product, and the 8-slot instance
     // does all eight whether or not they lie past the row.  Measured against
     // the plan above with the 8-slot kernel: head_dim 64 (two lanes instead
-    // of one) C5 batch 1 1579 -> 1608 tokens/s, C4 3126 -> 3151; head_dim 96
-    // (four lanes instead of two, 3 slots) C1 5882 -> 5972.  The query-block kernel
-    // keeps the plan above (two lanes made the C5 batch-32 step 1.173 -> 1.192
+    // of one) the 0.5B t3 decode 1579 -> 1608 tokens/s, the LFM2.5-shaped
+    // hybrid's 3126 -> 3151; head_dim 96 (four lanes instead of two, 3 slots)
+    // MiniMind3 q8 decode 5882 -> 5972.  The query-block kernel keeps the plan
+    // above (two lanes made the 0.5B t3 step over 32 sequences 1.173 -> 1.192
     // ms).
     A.lpp1 = A.lpp;
     if (A.kv_bits == 16) {

@@ -1375,7 +1375,7 @@ int vgx_gemv_plan(int kind, int rows, int cols, int num_cu, int* lpr, int* ri, i
     }
     // a q8 launch of at most 1024 rows (few workgroups) takes at least 32
     // lanes a row: MiniMind3's 768 x 768 wo GEMV (48 workgroups at 16 lanes,
-    // 96 at 32) made C1 decode 5931 -> 5956 tokens/s, where 64 lanes were
+    // 96 at 32) made its q8 decode 5931 -> 5956 tokens/s, where 64 lanes were
     // slower and 32 lanes on every 768-column GEMV had cost 0.7%
     if (r == 1 && kind == VGX_Q8 && rows <= 1024 && l < 32) l = 32;
     const int rpi = 64 / l;

@@ -227,7 +227,7 @@ __device__ __forceinline__ void rms_stats(const GemmLaunch& G, int t0, unsigned 
 // through RMSNorm first, the statistics formed in the workgroup.
 // Two- and four-wave workgroups are built for two waves a SIMD (at most 256
 // VGPRs a lane): left alone the compiler gave the q8 and q4 gate 260-280, one
-// workgroup a CU, and the 608-tile C3 gate ran in 2.4 rounds (q8 gate GEMM
+// workgroup a CU, and the 608-tile 256-token gate ran in 2.4 rounds (q8 gate GEMM
 // 10.4 -> 9.1 us, q4 14.5 -> 13.8, no spills).
 template <int KIND, int EPI, int NW, bool RMS, bool PART>
 __global__ void __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) gemm_kernel(const GemmLaunch G) {
@@ -681,7 +681,7 @@ GemmFn pick(int epi, int kind, int nw, bool rms, bool part) {
 // wave of an 8-wave workgroup): enough workgroups to cover the CUs, at least
 // four k-steps (one per wave) a split; 1 = no split.  Up to 32 k-steps the
 // whole row in one 8-wave workgroup beats the split and its epilogue launch
-// (C5 batch-32 qkv, 1280 x 1024: 5.7 against 8.3 us).
+// (the 32-sequence qkv of the 0.5B t3 model, 1280 x 1024: 5.7 against 8.3 us).
 int k_splits(int tiles_x, int tiles_y, int nsteps, int num_cu) {
     if (tiles_y != 1 || tiles_x >= num_cu / 2 || nsteps <= 32) return 1;
     return std::max(1, std::min({num_cu / tiles_x, nsteps / 4, kMaxSplit}));
@@ -721,7 +721,7 @@ bool workspace(vgx_ctx* ctx, size_t bytes, long long** out) {
 // Waves per workgroup: 4 when the launch has at least one tile per CU (two
 // 4-wave workgroups fit a CU's registers where one 8-wave workgroup does, so
 // up to two tiles a CU run in one round: the 256-token qkv, 384 tiles, took
-// 0.8% less of the C3 prefill than with 8 waves in two rounds); otherwise (a
+// 0.8% less of MiniMind3's 256-token q4 prefill than with 8 waves in two rounds); otherwise (a
 // few row tiles: a decode batch, a short prompt) 8 when the row has more than
 // 16 k-steps, so the tiles' k-steps are spread over more waves.  (16 waves
 // would cap a lane at 128 registers and spill the operands in flight; 8 waves
