@@ -515,6 +515,25 @@ def test_decode_graph_equals_launches(gpu, scheme):
     b.close()
 
 
+def test_decode_multi_step_graph_counts(gpu):
+    """Greedy generation replays a graph of four decode steps for each run of
+    four tokens and the one-step graph for the rest (a step of this tiny model
+    has far fewer than 100 launches): every token count around the multiples
+    of four -- no replay, only one-step replays, exactly one four-step replay,
+    one with a remainder, several -- gives the step-by-step launches' tokens."""
+    spec = synth.tiny_spec(seq=64, hidden=2112)
+    blob = synth.container(spec, "q8", seed=23)
+    a, b = Engine(blob), Engine(blob)
+    b.set_graphs(False)
+    prompt = synth.prompt(6, spec.vocab, seed=41)
+    for n in (1, 2, 4, 5, 6, 9, 13):
+        ga, _, _ = a.generate(prompt, n)
+        gb, _, _ = b.generate(prompt, n)
+        assert list(ga) == list(gb), n
+    a.close()
+    b.close()
+
+
 def test_decode_graph_hybrid_and_cache(gpu, tmp_path):
     """The graph on a hybrid (conv state advancing inside the replay) and
     resuming from a loaded prefix cache."""
